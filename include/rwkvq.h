@@ -1,0 +1,120 @@
+/*
+ * rwkvq.h -- C ABI of librwkvq_hip.so, the MI355X (gfx950) group-affine
+ * quantized-linear library.
+ *
+ * The reference (RafaelUI/rwkv-metal) reaches quantized arithmetic only through
+ * the upstream MLX op API.  Each entry point below replaces one of those ops:
+ *
+ *   rq_quantize    <- mx.quantize(w, group_size, bits)            (affine mode)
+ *                     called via nn.quantize at rwkv_metal/lora/finetune.py:88-89
+ *                     and QuantizedLinear.from_linear at rwkv_metal/lora/lora.py:45-46
+ *   rq_dequantize  <- mx.dequantize(w_q, scales, biases, group_size, bits)
+ *                     tests/dev_pack_native_mlx.py:70, tests/dev_check_hybrid.py:13
+ *   rq_qmm         <- mx.quantized_matmul(x, w_q, scales, biases, transpose, group_size, bits)
+ *                     rwkv_metal/lora/rwkvq_native.py:120-122 (transpose=True, forward);
+ *                     its VJP w.r.t. x (transpose=False) is the QLoRA backward
+ *                     reached from nn.value_and_grad at rwkv_metal/lora/finetune.py:141
+ *   rq_pack        <- _pack_codes_mlx / codec.pack_mlx_affine, rwkv_metal/lora/rwkvq_native.py:81-90
+ *                     (codes -> MLX bitstream; executable form tests/dev_pack_native_mlx.py:38-57)
+ *   rq_unpack      <- the inverse of that packing rule (rwkvq_native.py:18-33), i.e. the
+ *                     code extraction inside mx.dequantize
+ *   rq_qmm_grouped <- several independent mx.quantized_matmul(transpose=True) nodes of one
+ *                     lazy MLX graph evaluated together (e.g. tmix r/k/v projections,
+ *                     rwkv_metal/model/rwkv7_x070.py:142-144); one launch for all of them
+ *
+ * Layout (identical to MLX's): W is [rows, cols], cols (= in_features) is the
+ * grouped and packed axis.  w_q is uint32[rows, cols*bits/32], each row an
+ * LSB-first bitstream with code j at bits [j*bits, (j+1)*bits).  scales and
+ * biases are [rows, cols/group_size] in scales' dtype; ŵ = scale*code + bias.
+ *
+ * Conventions: every pointer is a device pointer owned by the caller; nothing
+ * is allocated; work is enqueued on `stream` (a hipStream_t, NULL = the
+ * default stream) with no implicit synchronisation.  Row-major, contiguous.
+ * All device pointers must be 16-byte aligned.
+ *
+ * Return codes: RQ_OK (0); RQ_EINVAL (-1): bits not in {2,3,4,5,6,8},
+ * group_size not in {32,64,128}, cols % group_size != 0, a negative size, a
+ * NULL pointer or an unknown dtype; RQ_EALIGN (-2): a pointer not 16-byte
+ * aligned; RQ_ELAUNCH (-3): the HIP launch failed.  rq_last_error() returns a
+ * thread-local message describing the last non-zero return.
+ *
+ * Reentrant: calls from several host threads on different streams are safe.
+ */
+#ifndef RWKVQ_H
+#define RWKVQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RWKVQ_ABI_VERSION 1
+
+typedef enum { RQ_BF16 = 0, RQ_F16 = 1, RQ_F32 = 2 } rq_dtype;
+
+enum { RQ_OK = 0, RQ_EINVAL = -1, RQ_EALIGN = -2, RQ_ELAUNCH = -3 };
+
+/* ABI version of the loaded library (RWKVQ_ABI_VERSION). */
+int rq_abi_version(void);
+
+/* Thread-local description of the last non-zero return ("" if none). */
+const char* rq_last_error(void);
+
+/* mx.quantize, affine mode.  w: [rows, cols] in w_dt.  Writes w_q
+ * uint32[rows, cols*bits/32] and scales/biases [rows, cols/group_size] in w_dt.
+ * Per group: fp32 min/max; scale = max((max-min)/(2^bits-1), 1e-7), negated
+ * unless |min| > |max|; the larger-magnitude extreme e becomes the bias and
+ * scale = e/rint(e/scale) when rint(e/scale) != 0 (else bias = 0);
+ * code = clip(rint((w-bias)/scale), 0, 2^bits-1) with IEEE division and
+ * round-half-even. */
+int rq_quantize(const void* w, rq_dtype w_dt, int64_t rows, int64_t cols, int group_size,
+                int bits, uint32_t* w_q, void* scales, void* biases, void* stream);
+
+/* mx.dequantize.  out[r, k] = T(T(code*scale) + bias) with T = sb_dt (MLX's
+ * multiply-then-add in the scales dtype), then cast to out_dt. */
+int rq_dequantize(const uint32_t* w_q, const void* scales, const void* biases, rq_dtype sb_dt,
+                  int64_t rows, int64_t cols, int group_size, int bits, void* out,
+                  rq_dtype out_dt, void* stream);
+
+/* mx.quantized_matmul.  transpose=1: y[m, rows] = x[m, cols] . Ŵ^T;
+ * transpose=0: y[m, cols] = x[m, rows] . Ŵ.  x_dt and sb_dt may differ
+ * (MLX promotes both to a common type); accumulation is fp32; y in y_dt.
+ * m <= 16 with transpose=1 runs the decode GEMV; larger m runs the MFMA GEMM. */
+int rq_qmm(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
+           const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
+           int group_size, int bits, int transpose, void* y, rq_dtype y_dt, void* stream);
+
+/* Pack codes uint8[rows, cols] (values < 2^bits) into the MLX bitstream
+ * w_q uint32[rows, cols*bits/32].  cols must be a multiple of 32. */
+int rq_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* w_q,
+            void* stream);
+
+/* Inverse of rq_pack: w_q -> codes uint8[rows, cols]. */
+int rq_unpack(const uint32_t* w_q, int64_t rows, int64_t cols, int bits, uint8_t* codes,
+              void* stream);
+
+/* One transpose=True product of a grouped launch. */
+typedef struct {
+    const void* x;          /* [m, cols] in x_dt */
+    const uint32_t* w_q;    /* [rows, cols*bits/32] */
+    const void* scales;     /* [rows, cols/group_size] in sb_dt */
+    const void* biases;
+    void* y;                /* [m, rows] in y_dt */
+    int64_t rows;
+    int64_t cols;
+} rq_problem;
+
+/* Several independent decode GEMVs (m <= 16, transpose=True) sharing m, bits,
+ * group_size and dtypes.  `problems` is a HOST array of n descriptors; they
+ * are copied into kernel arguments, RQ_MAX_GROUPED per launch, so n
+ * descriptors cost ceil(n / RQ_MAX_GROUPED) launches. */
+#define RQ_MAX_GROUPED 48
+int rq_qmm_grouped(const rq_problem* problems, int n, rq_dtype x_dt, rq_dtype sb_dt,
+                   rq_dtype y_dt, int64_t m, int group_size, int bits, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RWKVQ_H */

@@ -1,0 +1,203 @@
+// rq_abi.cpp -- the extern "C" boundary of librwkvq_hip.so (include/rwkvq.h).
+//
+// Validates arguments the way MLX's quantization ops do (bits, group size,
+// shapes and dtypes), checks alignment, then dispatches to the kernel
+// launchers.  Every failure returns a negative code and leaves a message in a
+// thread-local buffer read by rq_last_error().
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/rwkvq.h"
+#include "rq_launch.h"
+
+namespace rq {
+
+#define RQ_DECLARE_BITS(B)                                                                     \
+    hipError_t launch_qmv_b##B(const rq_problem*, int, int, int, int, int64_t, int,             \
+                               hipStream_t);                                                    \
+    hipError_t launch_qmm_t_b##B(const void*, int, const uint32_t*, const void*, const void*,    \
+                                 int, int64_t, int64_t, int64_t, int, void*, int, hipStream_t); \
+    hipError_t launch_qmm_n_b##B(const void*, int, const uint32_t*, const void*, const void*,    \
+                                 int, int64_t, int64_t, int64_t, int, void*, int, hipStream_t);
+RQ_DECLARE_BITS(2)
+RQ_DECLARE_BITS(3)
+RQ_DECLARE_BITS(4)
+RQ_DECLARE_BITS(5)
+RQ_DECLARE_BITS(6)
+RQ_DECLARE_BITS(8)
+
+hipError_t launch_qmv(const rq_problem* problems, int n, int x_dt, int sb_dt, int y_dt,
+                      int64_t m, int gs, int bits, hipStream_t stream) {
+    switch (bits) {
+        case 2: return launch_qmv_b2(problems, n, x_dt, sb_dt, y_dt, m, gs, stream);
+        case 3: return launch_qmv_b3(problems, n, x_dt, sb_dt, y_dt, m, gs, stream);
+        case 4: return launch_qmv_b4(problems, n, x_dt, sb_dt, y_dt, m, gs, stream);
+        case 5: return launch_qmv_b5(problems, n, x_dt, sb_dt, y_dt, m, gs, stream);
+        case 6: return launch_qmv_b6(problems, n, x_dt, sb_dt, y_dt, m, gs, stream);
+        case 8: return launch_qmv_b8(problems, n, x_dt, sb_dt, y_dt, m, gs, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+#define RQ_QMM_SWITCH(FN)                                                                      \
+    switch (bits) {                                                                            \
+        case 2: return FN##2(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
+        case 3: return FN##3(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
+        case 4: return FN##4(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
+        case 5: return FN##5(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
+        case 6: return FN##6(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
+        case 8: return FN##8(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
+        default: return hipErrorInvalidValue;                                                  \
+    }
+
+static hipError_t launch_qmm(int transpose, const void* x, int x_dt, const uint32_t* wq,
+                             const void* scales, const void* biases, int sb_dt, int64_t m,
+                             int64_t rows, int64_t cols, int gs, int bits, void* y, int y_dt,
+                             hipStream_t stream) {
+    if (transpose) {
+        RQ_QMM_SWITCH(launch_qmm_t_b)
+    } else {
+        RQ_QMM_SWITCH(launch_qmm_n_b)
+    }
+}
+
+}  // namespace rq
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok() {
+    g_err[0] = '\0';
+    return RQ_OK;
+}
+
+bool valid_bits(int b) { return b == 2 || b == 3 || b == 4 || b == 5 || b == 6 || b == 8; }
+bool valid_gs(int g) { return g == 32 || g == 64 || g == 128; }
+bool valid_dt(int d) { return d == RQ_BF16 || d == RQ_F16 || d == RQ_F32; }
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_common(int64_t rows, int64_t cols, int gs, int bits) {
+    if (!valid_bits(bits)) return fail(RQ_EINVAL, "bits must be one of 2,3,4,5,6,8 (got %d)", bits);
+    if (!valid_gs(gs)) return fail(RQ_EINVAL, "group_size must be 32, 64 or 128 (got %d)", gs);
+    if (rows < 0 || cols < 0) return fail(RQ_EINVAL, "negative size (rows=%lld cols=%lld)",
+                                          (long long)rows, (long long)cols);
+    if (cols % gs != 0)
+        return fail(RQ_EINVAL, "the last dimension (%lld) must be divisible by group_size %d",
+                    (long long)cols, gs);
+    return RQ_OK;
+}
+
+int launch_status(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(RQ_ELAUNCH, "%s: HIP launch failed: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int rq_abi_version(void) { return RWKVQ_ABI_VERSION; }
+
+const char* rq_last_error(void) { return g_err; }
+
+int rq_quantize(const void* w, rq_dtype w_dt, int64_t rows, int64_t cols, int group_size, int bits,
+                uint32_t* w_q, void* scales, void* biases, void* stream) {
+    if (int rc = check_common(rows, cols, group_size, bits)) return rc;
+    if (!valid_dt(w_dt)) return fail(RQ_EINVAL, "unsupported weight dtype %d", (int)w_dt);
+    if (rows * cols == 0) return ok();
+    if (!w || !w_q || !scales || !biases) return fail(RQ_EINVAL, "rq_quantize: NULL pointer");
+    if (!aligned16(w) || !aligned16(w_q)) return fail(RQ_EALIGN, "rq_quantize: w and w_q must be 16-byte aligned");
+    return launch_status(rq::launch_quantize(w, w_dt, rows, cols, group_size, bits, w_q, scales,
+                                             biases, (hipStream_t)stream),
+                         "rq_quantize");
+}
+
+int rq_dequantize(const uint32_t* w_q, const void* scales, const void* biases, rq_dtype sb_dt,
+                  int64_t rows, int64_t cols, int group_size, int bits, void* out,
+                  rq_dtype out_dt, void* stream) {
+    if (int rc = check_common(rows, cols, group_size, bits)) return rc;
+    if (!valid_dt(sb_dt) || !valid_dt(out_dt)) return fail(RQ_EINVAL, "unsupported dtype");
+    if (rows * cols == 0) return ok();
+    if (!w_q || !scales || !biases || !out) return fail(RQ_EINVAL, "rq_dequantize: NULL pointer");
+    if (!aligned16(w_q) || !aligned16(out)) return fail(RQ_EALIGN, "rq_dequantize: w_q and out must be 16-byte aligned");
+    return launch_status(rq::launch_dequantize(w_q, scales, biases, sb_dt, rows, cols, group_size,
+                                               bits, out, out_dt, (hipStream_t)stream),
+                         "rq_dequantize");
+}
+
+int rq_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* w_q,
+            void* stream) {
+    if (int rc = check_common(rows, cols, 32, bits)) return rc;
+    if (rows * cols == 0) return ok();
+    if (!codes || !w_q) return fail(RQ_EINVAL, "rq_pack: NULL pointer");
+    if (!aligned16(codes) || !aligned16(w_q)) return fail(RQ_EALIGN, "rq_pack: pointers must be 16-byte aligned");
+    return launch_status(rq::launch_pack(codes, rows, cols, bits, w_q, (hipStream_t)stream), "rq_pack");
+}
+
+int rq_unpack(const uint32_t* w_q, int64_t rows, int64_t cols, int bits, uint8_t* codes,
+              void* stream) {
+    if (int rc = check_common(rows, cols, 32, bits)) return rc;
+    if (rows * cols == 0) return ok();
+    if (!codes || !w_q) return fail(RQ_EINVAL, "rq_unpack: NULL pointer");
+    if (!aligned16(codes) || !aligned16(w_q)) return fail(RQ_EALIGN, "rq_unpack: pointers must be 16-byte aligned");
+    return launch_status(rq::launch_unpack(w_q, rows, cols, bits, codes, (hipStream_t)stream), "rq_unpack");
+}
+
+int rq_qmm(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
+           const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
+           int group_size, int bits, int transpose, void* y, rq_dtype y_dt, void* stream) {
+    if (int rc = check_common(rows, cols, group_size, bits)) return rc;
+    if (!valid_dt(x_dt) || !valid_dt(sb_dt) || !valid_dt(y_dt)) return fail(RQ_EINVAL, "unsupported dtype");
+    if (m < 0) return fail(RQ_EINVAL, "negative m");
+    const int64_t n_out = transpose ? rows : cols;
+    if (m == 0 || n_out == 0) return ok();
+    if (!y) return fail(RQ_EINVAL, "rq_qmm: NULL output");
+    const int64_t n_in = transpose ? cols : rows;
+    if (n_in == 0) return fail(RQ_EINVAL, "rq_qmm: empty contraction with a non-empty output is not supported");
+    if (!x || !w_q || !scales || !biases) return fail(RQ_EINVAL, "rq_qmm: NULL pointer");
+    if (!aligned16(x) || !aligned16(w_q)) return fail(RQ_EALIGN, "rq_qmm: x and w_q must be 16-byte aligned");
+    hipError_t e;
+    if (transpose && m <= 16) {
+        rq_problem p = {x, w_q, scales, biases, y, rows, cols};
+        e = rq::launch_qmv(&p, 1, x_dt, sb_dt, y_dt, m, group_size, bits, (hipStream_t)stream);
+    } else {
+        e = rq::launch_qmm(transpose, x, x_dt, w_q, scales, biases, sb_dt, m, rows, cols,
+                           group_size, bits, y, y_dt, (hipStream_t)stream);
+    }
+    return launch_status(e, "rq_qmm");
+}
+
+int rq_qmm_grouped(const rq_problem* problems, int n, rq_dtype x_dt, rq_dtype sb_dt,
+                   rq_dtype y_dt, int64_t m, int group_size, int bits, void* stream) {
+    if (n < 0 || (n > 0 && !problems)) return fail(RQ_EINVAL, "rq_qmm_grouped: bad problem list");
+    if (!valid_dt(x_dt) || !valid_dt(sb_dt) || !valid_dt(y_dt)) return fail(RQ_EINVAL, "unsupported dtype");
+    if (m < 1 || m > 16) return fail(RQ_EINVAL, "rq_qmm_grouped: m must be in [1, 16] (got %lld)", (long long)m);
+    for (int i = 0; i < n; ++i) {
+        const rq_problem& p = problems[i];
+        if (int rc = check_common(p.rows, p.cols, group_size, bits)) return rc;
+        if (p.cols == 0 && p.rows > 0)
+            return fail(RQ_EINVAL, "rq_qmm_grouped: problem %d has an empty contraction", i);
+        if (p.rows > 0 && (!p.x || !p.w_q || !p.scales || !p.biases || !p.y))
+            return fail(RQ_EINVAL, "rq_qmm_grouped: NULL pointer in problem %d", i);
+        if (!aligned16(p.x) || !aligned16(p.w_q))
+            return fail(RQ_EALIGN, "rq_qmm_grouped: problem %d: x and w_q must be 16-byte aligned", i);
+    }
+    if (n == 0) return ok();
+    return launch_status(rq::launch_qmv(problems, n, x_dt, sb_dt, y_dt, m, group_size, bits,
+                                        (hipStream_t)stream),
+                         "rq_qmm_grouped");
+}
+
+}  // extern "C"

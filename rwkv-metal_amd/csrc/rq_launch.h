@@ -1,0 +1,39 @@
+// rq_launch.h -- host-side launchers, one per kernel family.  Arguments are
+// validated by the C ABI layer (rq_abi.cpp) before any of these is called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/rwkvq.h"
+
+namespace rq {
+
+hipError_t launch_quantize(const void* w, int w_dt, int64_t rows, int64_t cols, int gs, int bits,
+                           uint32_t* wq, void* scales, void* biases, hipStream_t stream);
+
+hipError_t launch_dequantize(const uint32_t* wq, const void* scales, const void* biases,
+                             int sb_dt, int64_t rows, int64_t cols, int gs, int bits, void* out,
+                             int out_dt, hipStream_t stream);
+
+hipError_t launch_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* wq,
+                       hipStream_t stream);
+
+hipError_t launch_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bits,
+                         uint8_t* codes, hipStream_t stream);
+
+// Decode GEMV, transpose=True, 1 <= m <= 16, over n independent problems.
+hipError_t launch_qmv(const rq_problem* problems, int n, int x_dt, int sb_dt, int y_dt,
+                      int64_t m, int gs, int bits, hipStream_t stream);
+
+// MFMA GEMM, transpose=True: y[m, rows] = x[m, cols] . W^T.
+hipError_t launch_qmm_t(const void* x, int x_dt, const uint32_t* wq, const void* scales,
+                        const void* biases, int sb_dt, int64_t m, int64_t rows, int64_t cols,
+                        int gs, int bits, void* y, int y_dt, hipStream_t stream);
+
+// MFMA GEMM, transpose=False: y[m, cols] = x[m, rows] . W.
+hipError_t launch_qmm_n(const void* x, int x_dt, const uint32_t* wq, const void* scales,
+                        const void* biases, int sb_dt, int64_t m, int64_t rows, int64_t cols,
+                        int gs, int bits, void* y, int y_dt, hipStream_t stream);
+
+}  // namespace rq

@@ -1,0 +1,214 @@
+"""LoRA / QLoRA layer on a frozen quantized base, with the reference's API.
+
+    LoRALinear(linear, rank, alpha, dropout, quantize_base, q_group_size,
+               base_module, dtype)                       <- rwkv_metal/lora/lora.py:24-67
+    add_lora(model, rank, alpha, dropout, tmix_targets, cmix_targets,
+             quantize_base, q_group_size, layers)        <- rwkv_metal/lora/lora.py:74-108
+    quantize_base_model(model, bits, group_size, targets) <- rwkv_metal/lora/finetune.py:70-91
+    BIG_QUANT_TARGETS                                     <- rwkv_metal/lora/finetune.py:42
+    lora_state / save_lora / load_lora / merge_lora       <- rwkv_metal/lora/lora.py:132-172
+
+y = base(x) + (alpha/rank) * (x @ A^T) @ B^T with A ~ N(0, 1)/sqrt(in_features)
+and B = 0 (lora.py:54-56).  Only lora_a / lora_b are trainable (lora.py:101-102).
+The model layout is the reference's: model.blocks[i].tmix.{r,k,v,o}_proj and
+model.blocks[i].cmix.{key,value}.
+
+merge_lora differs on purpose: the reference adds the float delta to the
+packed words of a quantized base (lora.py:65-67), which yields garbage; here a
+quantized base is refused unless requantize=True, which dequantizes, adds the
+delta and quantizes again with the base's group size and bits.
+"""
+from __future__ import annotations
+
+import math
+from typing import Iterable, Optional, Tuple
+
+import torch
+from torch import Tensor, nn
+
+from . import ops
+from .nn import QuantizedEmbedding, QuantizedLinear, is_quantizable
+from .nn import quantize as nn_quantize
+
+BIG_QUANT_TARGETS = ("cmix.key", "cmix.value", "head", "emb")
+TMIX_TARGETS = ("r_proj", "k_proj", "v_proj", "o_proj")
+CMIX_TARGETS = ("key", "value")
+
+
+def _promote(a: torch.dtype, b: torch.dtype) -> torch.dtype:
+    return a if a == b else torch.float32
+
+
+class LoRALinear(nn.Module):
+    """Frozen base (bf16 Linear, QuantizedLinear, or any module with
+    out_features/in_features/__call__) plus a trainable low-rank update."""
+
+    def __init__(self, linear: Optional[nn.Linear] = None, rank: int = 16, alpha: float = 32.0,
+                 dropout: float = 0.0, quantize_base: int = 0, q_group_size: int = 64,
+                 base_module: Optional[nn.Module] = None, dtype: Optional[torch.dtype] = None):
+        super().__init__()
+        if base_module is not None:
+            out_features, in_features = base_module.out_features, base_module.in_features
+            dtype = dtype or torch.bfloat16
+            device = next((t.device for t in base_module.buffers()), None) or next(
+                (t.device for t in base_module.parameters()), torch.device("cpu"))
+            self.linear = base_module
+        else:
+            out_features, in_features = linear.weight.shape
+            dtype = linear.weight.dtype
+            device = linear.weight.device
+            if quantize_base:
+                self.linear = QuantizedLinear.from_linear(linear, group_size=q_group_size,
+                                                          bits=quantize_base)
+            else:
+                self.linear = linear
+        self.in_features, self.out_features = in_features, out_features
+        self.rank = rank
+        self.scale = alpha / rank
+        self.dropout = nn.Dropout(dropout) if dropout > 0 else None
+        scale_a = 1.0 / math.sqrt(in_features)
+        self.lora_a = nn.Parameter(
+            (torch.randn(rank, in_features, device=device) * scale_a).to(dtype))
+        self.lora_b = nn.Parameter(torch.zeros(out_features, rank, device=device, dtype=dtype))
+
+    def forward(self, x: Tensor) -> Tensor:
+        base = self.linear(x)
+        ct = _promote(x.dtype, self.lora_a.dtype)
+        z = x.to(ct) @ self.lora_a.to(ct).t()
+        if self.dropout is not None:
+            z = self.dropout(z)
+        return base + self.scale * (z @ self.lora_b.to(ct).t())
+
+    def merged_weight(self, requantize: bool = False):
+        delta = self.scale * (self.lora_b.float() @ self.lora_a.float())
+        if isinstance(self.linear, QuantizedLinear):
+            if not requantize:
+                raise ValueError(
+                    "cannot add a float delta to a quantized base (its weight holds packed "
+                    "codes); pass requantize=True to dequantize, merge and quantize again")
+            w = self.linear.dequantized_weight().float() + delta
+            return w.to(self.linear.scales.dtype)
+        w = self.linear.weight
+        return w + delta.to(w.dtype)
+
+
+def _blocks(model):
+    return model.blocks
+
+
+def add_lora(model: nn.Module, rank: int = 16, alpha: float = 32.0, dropout: float = 0.0,
+             tmix_targets=TMIX_TARGETS, cmix_targets=(), quantize_base: int = 0,
+             q_group_size: int = 64, layers: Optional[Iterable[int]] = None):
+    """Wrap the target Linears of the selected blocks in LoRALinear and freeze
+    everything but the adapters.  quantize_base: 0 keeps the base as is; 2-8
+    quantizes it (QLoRA)."""
+    wrapped = []
+
+    def mk(mod):
+        return LoRALinear(mod, rank, alpha, dropout, quantize_base, q_group_size)
+
+    blocks = _blocks(model)
+    n_layer = len(blocks)
+    sel = set(range(n_layer)) if layers is None else set(i % n_layer for i in layers)
+    for li, blk in enumerate(blocks):
+        if li not in sel:
+            continue
+        for name in tmix_targets:
+            mod = getattr(blk.tmix, name, None)
+            if isinstance(mod, nn.Linear):
+                setattr(blk.tmix, name, mk(mod))
+                wrapped.append(f"tmix.{name}")
+        for name in cmix_targets:
+            mod = getattr(blk.cmix, name, None)
+            if isinstance(mod, nn.Linear):
+                setattr(blk.cmix, name, mk(mod))
+                wrapped.append(f"cmix.{name}")
+
+    for p in model.parameters():
+        p.requires_grad_(False)
+    _unfreeze_adapters(model)
+
+    info = _param_stats(model)
+    info["wrapped_per_block"] = sorted(set(wrapped))
+    info["num_adapters"] = len(wrapped)
+    return model, info
+
+
+def _unfreeze_adapters(model: nn.Module) -> None:
+    for m in model.modules():
+        if isinstance(m, LoRALinear):
+            m.lora_a.requires_grad_(True)
+            m.lora_b.requires_grad_(True)
+
+
+def _param_stats(model: nn.Module) -> dict:
+    total = sum(p.numel() for p in model.parameters())
+    # packed quantized tensors count as parameters, as in MLX's parameter tree
+    for m in model.modules():
+        if isinstance(m, (QuantizedLinear, QuantizedEmbedding)):
+            total += m.weight.numel() + m.scales.numel() + m.biases.numel()
+    train = sum(p.numel() for p in model.parameters() if p.requires_grad)
+    return {"total_params": total, "trainable_params": train,
+            "trainable_pct": 100.0 * train / max(1, total)}
+
+
+def lora_state(model: nn.Module) -> dict:
+    return {k: v for k, v in model.named_parameters() if v.requires_grad}
+
+
+def save_lora(model: nn.Module, path: str) -> None:
+    from safetensors.torch import save_file
+    save_file({k: v.detach().contiguous().cpu() for k, v in lora_state(model).items()}, path)
+
+
+def load_lora(model: nn.Module, path: str) -> nn.Module:
+    from safetensors.torch import load_file
+    weights = load_file(path)
+    params = dict(model.named_parameters())
+    for k, v in weights.items():
+        if k not in params:
+            raise KeyError(f"adapter tensor {k} has no matching parameter")
+        with torch.no_grad():
+            params[k].copy_(v.to(params[k].device, params[k].dtype))
+    return model
+
+
+def merge_lora(model: nn.Module, requantize: bool = False) -> nn.Module:
+    """Fold every LoRALinear back into its base (in place)."""
+    def merged(child: LoRALinear) -> nn.Module:
+        base = child.linear
+        if isinstance(base, QuantizedLinear):
+            w = child.merged_weight(requantize=requantize)
+            lin = nn.Linear(base.in_features, base.out_features, bias=base.bias is not None,
+                            device=w.device, dtype=w.dtype)
+            with torch.no_grad():
+                lin.weight.copy_(w)
+                if base.bias is not None:
+                    lin.bias.copy_(base.bias)
+            return QuantizedLinear.from_linear(lin, base.group_size, base.bits)
+        with torch.no_grad():
+            base.weight.copy_(child.merged_weight())
+        return base
+
+    def replace_in(parent: nn.Module) -> None:
+        for cname, child in list(parent.named_children()):
+            if isinstance(child, LoRALinear):
+                setattr(parent, cname, merged(child))
+            else:
+                replace_in(child)
+
+    replace_in(model)
+    for p in model.parameters():
+        p.requires_grad_(True)
+    return model
+
+
+def quantize_base_model(model: nn.Module, bits: int = 4, group_size: int = 64,
+                        targets: Tuple[str, ...] = BIG_QUANT_TARGETS) -> nn.Module:
+    """Quantize, in place, only the modules whose path ends with one of
+    `targets` (cmix.key/value, head, emb by default)."""
+    def predicate(path, module):
+        return is_quantizable(module) and any(path.endswith(t) for t in targets)
+
+    nn_quantize(model, group_size=group_size, bits=bits, class_predicate=predicate)
+    return model

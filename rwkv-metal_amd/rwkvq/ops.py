@@ -1,0 +1,356 @@
+"""torch custom ops over the C ABI: the MLX quantization op surface.
+
+    quantize(w, group_size=64, bits=4)                    <- mx.quantize
+    dequantize(w_q, scales, biases, group_size, bits)     <- mx.dequantize
+    quantized_matmul(x, w_q, scales, biases, transpose,   <- mx.quantized_matmul
+                     group_size, bits)
+    pack_codes(codes, bits) / unpack_codes(w_q, bits)     <- the MLX bitstream rule
+
+Reference call sites: rwkv_metal/lora/finetune.py:88-89 (nn.quantize),
+rwkv_metal/lora/lora.py:45-46 (QuantizedLinear.from_linear),
+rwkv_metal/lora/rwkvq_native.py:120-122 (quantized_matmul, transpose=True),
+tests/dev_pack_native_mlx.py:70 (dequantize), rwkv_metal/lora/rwkvq_native.py:81-90
+(packing).  MLX semantics kept: the grouped axis is the last one, leading
+dimensions of x fold into M, x and scales are promoted to a common dtype
+(equal dtypes stay, any other mix computes in float32), and the gradient of
+quantized_matmul flows to x only, as dY through the opposite transpose.
+
+Packed weights are int32 tensors holding the uint32 words bit for bit
+(uint32 tensors are accepted and viewed as int32).  Tensors must live on the
+ROCm GPU; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Sequence, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from ._lib import DTYPE_CODE, RqProblem, check, lib
+
+VALID_BITS = (2, 3, 4, 5, 6, 8)
+VALID_GROUP_SIZES = (32, 64, 128)
+
+
+def _promote(a: torch.dtype, b: torch.dtype) -> torch.dtype:
+    return a if a == b else torch.float32
+
+
+def _check_args(group_size: int, bits: int) -> None:
+    if bits not in VALID_BITS:
+        raise ValueError(f"bits must be one of {VALID_BITS} (got {bits})")
+    if group_size not in VALID_GROUP_SIZES:
+        raise ValueError(f"group_size must be one of {VALID_GROUP_SIZES} (got {group_size})")
+
+
+def _on_gpu(*ts: Tensor) -> None:
+    for t in ts:
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "rwkvq ops run only on a ROCm GPU (HIP library); got a tensor on "
+                f"'{t.device}'. There is no CPU implementation.")
+
+
+def _float(t: Tensor, name: str) -> None:
+    if t.dtype not in DTYPE_CODE:
+        raise ValueError(f"{name} must be bfloat16, float16 or float32 (got {t.dtype})")
+
+
+def _ready(t: Tensor) -> Tensor:
+    """Contiguous and 16-byte aligned (the ABI's requirement)."""
+    t = t.contiguous()
+    if t.numel() and t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _words(w_q: Tensor) -> Tensor:
+    if w_q.dtype == torch.uint32:
+        w_q = w_q.view(torch.int32)
+    if w_q.dtype != torch.int32:
+        raise ValueError(f"packed weights must be int32/uint32 words (got {w_q.dtype})")
+    return w_q
+
+
+def _stream(t: Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: Tensor) -> int:
+    return t.data_ptr() if t.numel() else 0
+
+
+# --------------------------------------------------------------- quantize
+
+@torch.library.custom_op("rwkvq::quantize", mutates_args=())
+def _quantize_op(w: Tensor, group_size: int, bits: int) -> Tuple[Tensor, Tensor, Tensor]:
+    _on_gpu(w)
+    w = _ready(w)
+    K = w.shape[-1]
+    R = w.numel() // K if K else 0
+    lead = w.shape[:-1]
+    wq = torch.empty(*lead, K * bits // 32, dtype=torch.int32, device=w.device)
+    s = torch.empty(*lead, K // group_size, dtype=w.dtype, device=w.device)
+    b = torch.empty_like(s)
+    with torch.cuda.device(w.device):
+        rc = lib().rq_quantize(_ptr(w), DTYPE_CODE[w.dtype], R, K, group_size, bits, _ptr(wq),
+                               _ptr(s), _ptr(b), _stream(w))
+    check(rc, "quantize")
+    return wq, s, b
+
+
+@_quantize_op.register_fake
+def _(w, group_size, bits):
+    K = w.shape[-1]
+    lead = w.shape[:-1]
+    return (w.new_empty(*lead, K * bits // 32, dtype=torch.int32),
+            w.new_empty(*lead, K // group_size), w.new_empty(*lead, K // group_size))
+
+
+def quantize(w: Tensor, group_size: int = 64, bits: int = 4) -> Tuple[Tensor, Tensor, Tensor]:
+    """mx.quantize (affine): w[..., K] -> (w_q int32[..., K*bits/32], scales, biases)."""
+    _check_args(group_size, bits)
+    _float(w, "w")
+    if w.dim() < 2:
+        raise ValueError("quantize expects a matrix (at least 2 dimensions)")
+    if w.shape[-1] % group_size:
+        raise ValueError(f"the last dimension ({w.shape[-1]}) must be divisible by "
+                         f"group_size {group_size}")
+    return _quantize_op(w, group_size, bits)
+
+
+# ------------------------------------------------------------- dequantize
+
+@torch.library.custom_op("rwkvq::dequantize", mutates_args=())
+def _dequantize_op(w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int,
+                   bits: int) -> Tensor:
+    _on_gpu(w_q, scales, biases)
+    w_q, scales, biases = _ready(w_q), _ready(scales), _ready(biases.to(scales.dtype))
+    K = w_q.shape[-1] * 32 // bits
+    R = w_q.numel() // w_q.shape[-1] if w_q.shape[-1] else 0
+    out = torch.empty(*w_q.shape[:-1], K, dtype=scales.dtype, device=w_q.device)
+    with torch.cuda.device(w_q.device):
+        rc = lib().rq_dequantize(_ptr(w_q), _ptr(scales), _ptr(biases), DTYPE_CODE[scales.dtype],
+                                 R, K, group_size, bits, _ptr(out), DTYPE_CODE[out.dtype],
+                                 _stream(w_q))
+    check(rc, "dequantize")
+    return out
+
+
+@_dequantize_op.register_fake
+def _(w_q, scales, biases, group_size, bits):
+    K = w_q.shape[-1] * 32 // bits
+    return scales.new_empty(*w_q.shape[:-1], K)
+
+
+def _check_packed(w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int, bits: int):
+    if (w_q.shape[-1] * 32) % bits:
+        raise ValueError("packed width is not a whole number of codes")
+    K = w_q.shape[-1] * 32 // bits
+    if K % group_size:
+        raise ValueError(f"unpacked width {K} is not divisible by group_size {group_size}")
+    want = (*w_q.shape[:-1], K // group_size)
+    if tuple(scales.shape) != want or tuple(biases.shape) != want:
+        raise ValueError(f"scales/biases must have shape {want} "
+                         f"(got {tuple(scales.shape)} / {tuple(biases.shape)})")
+    return K
+
+
+def dequantize(w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int = 64,
+               bits: int = 4) -> Tensor:
+    """mx.dequantize: scales*code + biases, evaluated in the scales dtype."""
+    _check_args(group_size, bits)
+    w_q = _words(w_q)
+    _float(scales, "scales")
+    _check_packed(w_q, scales, biases, group_size, bits)
+    return _dequantize_op(w_q, scales, biases, group_size, bits)
+
+
+# ------------------------------------------------------- quantized_matmul
+
+@torch.library.custom_op("rwkvq::quantized_matmul", mutates_args=())
+def _qmm_op(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, transpose: bool,
+            group_size: int, bits: int) -> Tensor:
+    _on_gpu(x, w_q, scales, biases)
+    x, w_q, scales = _ready(x), _ready(w_q), _ready(scales)
+    biases = _ready(biases.to(scales.dtype))
+    R = w_q.shape[0]
+    K = w_q.shape[1] * 32 // bits
+    n_out = R if transpose else K
+    out_dtype = _promote(x.dtype, scales.dtype)
+    m = x.numel() // x.shape[-1] if x.shape[-1] else 0
+    y = torch.empty(*x.shape[:-1], n_out, dtype=out_dtype, device=x.device)
+    if y.numel() == 0:
+        return y
+    with torch.cuda.device(x.device):
+        rc = lib().rq_qmm(_ptr(x), DTYPE_CODE[x.dtype], _ptr(w_q), _ptr(scales), _ptr(biases),
+                          DTYPE_CODE[scales.dtype], m, R, K, group_size, bits,
+                          1 if transpose else 0, _ptr(y), DTYPE_CODE[out_dtype], _stream(x))
+    check(rc, "quantized_matmul")
+    return y
+
+
+@_qmm_op.register_fake
+def _(x, w_q, scales, biases, transpose, group_size, bits):
+    R = w_q.shape[0]
+    K = w_q.shape[1] * 32 // bits
+    return x.new_empty(*x.shape[:-1], R if transpose else K,
+                       dtype=_promote(x.dtype, scales.dtype))
+
+
+def _qmm_setup(ctx, inputs, output):
+    x, w_q, scales, biases, transpose, group_size, bits = inputs
+    ctx.save_for_backward(w_q, scales, biases)
+    ctx.transpose, ctx.group_size, ctx.bits = transpose, group_size, bits
+    ctx.x_dtype = x.dtype
+
+
+def _qmm_backward(ctx, grad):
+    w_q, scales, biases = ctx.saved_tensors
+    dx = None
+    if ctx.needs_input_grad[0]:
+        dx = _qmm_op(grad.contiguous(), w_q, scales, biases, not ctx.transpose, ctx.group_size,
+                     ctx.bits).to(ctx.x_dtype)
+    return dx, None, None, None, None, None, None
+
+
+_qmm_op.register_autograd(_qmm_backward, setup_context=_qmm_setup)
+
+
+def quantized_matmul(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor,
+                     transpose: bool = True, group_size: int = 64, bits: int = 4) -> Tensor:
+    """mx.quantized_matmul.  transpose=True: x @ W^T ; transpose=False: x @ W."""
+    _check_args(group_size, bits)
+    w_q = _words(w_q)
+    _float(x, "x")
+    _float(scales, "scales")
+    if w_q.dim() != 2:
+        raise ValueError("quantized_matmul expects a 2-D packed weight")
+    K = _check_packed(w_q, scales, biases, group_size, bits)
+    n_in = K if transpose else w_q.shape[0]
+    if x.shape[-1] != n_in:
+        raise ValueError(f"x has inner dimension {x.shape[-1]} but the quantized weight expects "
+                         f"{n_in} (transpose={transpose})")
+    return _qmm_op(x, w_q, scales, biases, bool(transpose), group_size, bits)
+
+
+class GroupedQmv:
+    """A validated set of independent decode products y_i = x_i @ W_i^T
+    (m <= 16) run by rq_qmm_grouped: one ctypes call per run(), as few kernel
+    launches as the C ABI allows.  All x_i share m and dtype; all W_i share
+    bits, group size and the scales dtype.  The plan keeps references to every
+    tensor, so run() may be called repeatedly (e.g. one decode step each)."""
+
+    def __init__(self, xs: Sequence[Tensor], ws: Sequence[Tuple[Tensor, Tensor, Tensor]],
+                 group_size: int = 64, bits: int = 4, out: Sequence[Tensor] | None = None):
+        _check_args(group_size, bits)
+        if len(xs) != len(ws):
+            raise ValueError("need one weight triple per activation")
+        if not xs:
+            raise ValueError("grouped_qmv needs at least one problem")
+        x0 = xs[0]
+        _on_gpu(x0)
+        m = x0.numel() // x0.shape[-1]
+        if not 1 <= m <= 16:
+            raise ValueError(f"grouped_qmv: m must be in [1, 16] (got {m})")
+        sdt = ws[0][1].dtype
+        ydt = _promote(x0.dtype, sdt)
+        self.probs = (RqProblem * len(xs))()
+        self._keep, self.outs = [], []
+        for i, (x, (w_q, s, b)) in enumerate(zip(xs, ws)):
+            _on_gpu(x, w_q, s, b)
+            w_q = _words(w_q)
+            K = _check_packed(w_q, s, b, group_size, bits)
+            if x.dtype != x0.dtype or s.dtype != sdt or x.numel() // x.shape[-1] != m:
+                raise ValueError("grouped_qmv: every problem must share m and dtypes")
+            if x.shape[-1] != K:
+                raise ValueError(f"grouped_qmv: problem {i}: x width {x.shape[-1]} != {K}")
+            x, w_q, s, b = _ready(x), _ready(w_q), _ready(s), _ready(b.to(sdt))
+            y = out[i] if out is not None else torch.empty(
+                *x.shape[:-1], w_q.shape[0], dtype=ydt, device=x.device)
+            if y.dtype != ydt or not y.is_contiguous() or y.shape[-1] != w_q.shape[0]:
+                raise ValueError(f"grouped_qmv: bad output buffer for problem {i}")
+            self._keep += [x, w_q, s, b]
+            self.outs.append(y)
+            self.probs[i] = RqProblem(x.data_ptr(), w_q.data_ptr(), s.data_ptr(), b.data_ptr(),
+                                      y.data_ptr(), w_q.shape[0], K)
+        self.n, self.m, self.device = len(xs), m, x0.device
+        self.codes = (DTYPE_CODE[x0.dtype], DTYPE_CODE[sdt], DTYPE_CODE[ydt])
+        self.group_size, self.bits = group_size, bits
+
+    def run(self) -> List[Tensor]:
+        with torch.cuda.device(self.device):
+            rc = lib().rq_qmm_grouped(self.probs, self.n, *self.codes, self.m, self.group_size,
+                                      self.bits, torch.cuda.current_stream(self.device).cuda_stream)
+        check(rc, "grouped_qmv")
+        return self.outs
+
+
+def grouped_qmv(xs: Sequence[Tensor], ws: Sequence[Tuple[Tensor, Tensor, Tensor]],
+                group_size: int = 64, bits: int = 4, out: Sequence[Tensor] | None = None
+                ) -> List[Tensor]:
+    """One-shot form of GroupedQmv: y_i = x_i @ W_i^T for every i."""
+    if not xs:
+        return []
+    return GroupedQmv(xs, ws, group_size, bits, out).run()
+
+
+# ---------------------------------------------------------- pack / unpack
+
+@torch.library.custom_op("rwkvq::pack_codes", mutates_args=())
+def _pack_op(codes: Tensor, bits: int) -> Tensor:
+    _on_gpu(codes)
+    codes = _ready(codes)
+    K = codes.shape[-1]
+    R = codes.numel() // K if K else 0
+    wq = torch.empty(*codes.shape[:-1], K * bits // 32, dtype=torch.int32, device=codes.device)
+    with torch.cuda.device(codes.device):
+        rc = lib().rq_pack(_ptr(codes), R, K, bits, _ptr(wq), _stream(codes))
+    check(rc, "pack_codes")
+    return wq
+
+
+@_pack_op.register_fake
+def _(codes, bits):
+    return codes.new_empty(*codes.shape[:-1], codes.shape[-1] * bits // 32, dtype=torch.int32)
+
+
+@torch.library.custom_op("rwkvq::unpack_codes", mutates_args=())
+def _unpack_op(w_q: Tensor, bits: int) -> Tensor:
+    _on_gpu(w_q)
+    w_q = _ready(w_q)
+    K = w_q.shape[-1] * 32 // bits
+    R = w_q.numel() // w_q.shape[-1] if w_q.shape[-1] else 0
+    codes = torch.empty(*w_q.shape[:-1], K, dtype=torch.uint8, device=w_q.device)
+    with torch.cuda.device(w_q.device):
+        rc = lib().rq_unpack(_ptr(w_q), R, K, bits, _ptr(codes), _stream(w_q))
+    check(rc, "unpack_codes")
+    return codes
+
+
+@_unpack_op.register_fake
+def _(w_q, bits):
+    return w_q.new_empty(*w_q.shape[:-1], w_q.shape[-1] * 32 // bits, dtype=torch.uint8)
+
+
+def pack_codes(codes: Tensor, bits: int) -> Tensor:
+    """codes uint8[..., K] (K % 32 == 0) -> MLX bitstream words int32[..., K*bits/32]."""
+    if bits not in VALID_BITS:
+        raise ValueError(f"bits must be one of {VALID_BITS} (got {bits})")
+    if codes.dtype != torch.uint8:
+        raise ValueError("codes must be uint8")
+    if codes.shape[-1] % 32:
+        raise ValueError("the code row length must be a multiple of 32")
+    return _pack_op(codes, bits)
+
+
+def unpack_codes(w_q: Tensor, bits: int) -> Tensor:
+    """Inverse of pack_codes."""
+    if bits not in VALID_BITS:
+        raise ValueError(f"bits must be one of {VALID_BITS} (got {bits})")
+    w_q = _words(w_q)
+    if w_q.shape[-1] % bits:
+        raise ValueError("packed width must be a multiple of bits words")
+    return _unpack_op(w_q, bits)

@@ -1,0 +1,77 @@
+"""The C ABI library loads on a machine without a GPU, exports every entry
+point include/rwkvq.h declares, and rejects bad arguments before touching the
+device (no compute calls here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rwkvq.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(rq_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from rwkvq import _lib
+    return _lib.lib()
+
+
+def test_header_declares_the_expected_surface():
+    assert declared_functions() == sorted([
+        "rq_abi_version", "rq_last_error", "rq_quantize", "rq_dequantize", "rq_qmm",
+        "rq_pack", "rq_unpack", "rq_qmm_grouped"])
+
+
+def test_library_exports_every_declared_symbol(L):
+    from rwkvq import _lib
+    for name in declared_functions():
+        assert hasattr(L, name), f"{name} missing from librwkvq_hip.so"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert L.rq_abi_version() == 1
+
+
+def _err(L):
+    return L.rq_last_error().decode()
+
+
+def test_invalid_arguments_return_einval(L):
+    p = 0x1000  # never dereferenced: validation fails first
+    assert L.rq_qmm(p, 0, p, p, p, 0, 1, 64, 64, 64, 7, 1, p, 0, None) == -1
+    assert "bits" in _err(L)
+    assert L.rq_qmm(p, 0, p, p, p, 0, 1, 64, 64, 48, 4, 1, p, 0, None) == -1
+    assert "group_size" in _err(L)
+    assert L.rq_quantize(p, 0, 4, 96, 64, 4, p, p, p, None) == -1
+    assert "divisible" in _err(L)
+    assert L.rq_dequantize(p, p, p, 0, -1, 64, 64, 4, p, 0, None) == -1
+    assert L.rq_qmm(p, 7, p, p, p, 0, 1, 64, 64, 64, 4, 1, p, 0, None) == -1
+    assert L.rq_qmm(0, 0, p, p, p, 0, 1, 64, 64, 64, 4, 1, p, 0, None) == -1
+    assert "NULL" in _err(L)
+
+
+def test_misaligned_pointers_return_ealign(L):
+    p, odd = 0x1000, 0x1002
+    assert L.rq_qmm(odd, 0, p, p, p, 0, 1, 64, 64, 64, 4, 1, p, 0, None) == -2
+    assert L.rq_quantize(odd, 0, 4, 64, 64, 4, p, p, p, None) == -2
+    assert L.rq_unpack(p, 4, 64, 4, odd, None) == -2
+
+
+def test_empty_problems_are_no_ops(L):
+    assert L.rq_quantize(0, 0, 0, 64, 64, 4, 0, 0, 0, None) == 0
+    assert L.rq_dequantize(0, 0, 0, 0, 5, 0, 64, 4, 0, 0, None) == 0
+    assert L.rq_qmm(0, 0, 0, 0, 0, 0, 0, 64, 64, 64, 4, 1, 0, 0, None) == 0
+    assert L.rq_qmm_grouped(None, 0, 0, 0, 0, 1, 64, 4, None) == 0
+    assert _err(L) == ""
+
+
+def test_grouped_rejects_large_m(L):
+    from rwkvq._lib import RqProblem
+    probs = (RqProblem * 1)()
+    assert L.rq_qmm_grouped(probs, 1, 0, 0, 0, 17, 64, 4, None) == -1
+    assert "m must be" in _err(L)

@@ -1,0 +1,159 @@
+"""Host logic of the Python API without a GPU: argument checks, shape and
+dtype inference (meta tensors), module swapping by path predicate, LoRA
+wiring, and the refusal to run compute anywhere but the GPU."""
+import pytest
+import torch
+from torch import nn
+
+
+class TMix(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.r_proj, self.k_proj = nn.Linear(d, d, bias=False), nn.Linear(d, d, bias=False)
+        self.v_proj, self.o_proj = nn.Linear(d, d, bias=False), nn.Linear(d, d, bias=False)
+        self.w_lora = nn.Linear(d, 32, bias=False)   # low-rank branch, never quantized
+
+
+class CMix(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.key, self.value = nn.Linear(d, 4 * d, bias=False), nn.Linear(4 * d, d, bias=False)
+
+
+class Block(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.tmix, self.cmix = TMix(d), CMix(d)
+
+
+class Tiny(nn.Module):
+    """The reference model's module layout (rwkv_metal/model/rwkv7_x070.py)."""
+
+    def __init__(self, d=128, n=3, vocab=256, device="meta"):
+        super().__init__()
+        with torch.device(device):
+            self.emb = nn.Embedding(vocab, d)
+            self.blocks = nn.ModuleList([Block(d) for _ in range(n)])
+            self.head = nn.Linear(d, vocab, bias=False)
+        self.to(torch.bfloat16)
+
+
+def test_ops_refuse_cpu_tensors(rq):
+    w = torch.randn(8, 64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        rq.quantize(w, 64, 4)
+    wq = torch.zeros(8, 8, dtype=torch.int32)
+    s = torch.zeros(8, 1)
+    with pytest.raises(RuntimeError, match="GPU"):
+        rq.quantized_matmul(torch.randn(2, 64), wq, s, s, True, 64, 4)
+    with pytest.raises(RuntimeError, match="GPU"):
+        rq.dequantize(wq, s, s, 64, 4)
+
+
+def test_argument_validation(rq):
+    w = torch.empty(8, 64, device="meta")
+    with pytest.raises(ValueError):
+        rq.quantize(w, 64, 7)
+    with pytest.raises(ValueError):
+        rq.quantize(w, 48, 4)
+    with pytest.raises(ValueError):
+        rq.quantize(torch.empty(8, 96, device="meta"), 64, 4)
+    wq = torch.empty(8, 8, dtype=torch.int32, device="meta")
+    s = torch.empty(8, 1, device="meta")
+    with pytest.raises(ValueError, match="inner dimension"):
+        rq.quantized_matmul(torch.empty(2, 32, device="meta"), wq, s, s, True, 64, 4)
+    with pytest.raises(ValueError, match="scales"):
+        rq.quantized_matmul(torch.empty(2, 64, device="meta"), wq, s[:4], s[:4], True, 64, 4)
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 64), (3, 64), (8, 32), (6, 128)])
+def test_meta_shapes_and_promotion(rq, bits, gs):
+    w = torch.empty(96, 256, device="meta", dtype=torch.bfloat16)
+    wq, s, b = rq.quantize(w, gs, bits)
+    assert wq.shape == (96, 256 * bits // 32) and wq.dtype == torch.int32
+    assert s.shape == b.shape == (96, 256 // gs) and s.dtype == torch.bfloat16
+    x = torch.empty(3, 5, 256, device="meta", dtype=torch.bfloat16)
+    y = rq.quantized_matmul(x, wq, s, b, True, gs, bits)
+    assert y.shape == (3, 5, 96) and y.dtype == torch.bfloat16
+    y32 = rq.quantized_matmul(x.float(), wq, s, b, True, gs, bits)
+    assert y32.dtype == torch.float32            # MLX promotion: f32 x bf16 -> f32
+    dy = torch.empty(7, 96, device="meta", dtype=torch.bfloat16)
+    assert rq.quantized_matmul(dy, wq, s, b, False, gs, bits).shape == (7, 256)
+    assert rq.dequantize(wq, s, b, gs, bits).shape == (96, 256)
+
+
+def test_quantize_base_model_selects_big_targets(rq):
+    m = Tiny()
+    rq.quantize_base_model(m, bits=4, group_size=64)
+    assert isinstance(m.head, rq.QuantizedLinear)
+    assert isinstance(m.emb, rq.QuantizedEmbedding)
+    for blk in m.blocks:
+        assert isinstance(blk.cmix.key, rq.QuantizedLinear)
+        assert isinstance(blk.cmix.value, rq.QuantizedLinear)
+        assert isinstance(blk.tmix.r_proj, nn.Linear)      # left for add_lora
+        assert isinstance(blk.tmix.w_lora, nn.Linear)      # low-rank: never quantized
+    assert m.blocks[0].cmix.value.weight.shape == (128, 512 * 4 // 32)
+    sd = m.state_dict()
+    assert {"head.weight", "head.scales", "head.biases"} <= set(sd)
+
+
+def test_mixed_bits_predicate(rq):
+    m = Tiny()
+    rq.quantize_model(m, group_size=64, bits=3, class_predicate=lambda p, mod: (
+        {"bits": 8} if p == "head" else (rq.is_quantizable(mod) and p.endswith(("key", "value")))))
+    assert m.head.bits == 8 and m.blocks[1].cmix.key.bits == 3
+    assert isinstance(m.emb, nn.Embedding)
+
+
+def test_add_lora_wiring_and_freeze(rq):
+    m = Tiny()
+    rq.quantize_base_model(m, bits=4)
+    m, info = rq.add_lora(m, rank=16, alpha=16.0, quantize_base=4, layers=range(1, 3))
+    assert info["wrapped_per_block"] == ["tmix.k_proj", "tmix.o_proj", "tmix.r_proj",
+                                         "tmix.v_proj"]
+    assert info["num_adapters"] == 8
+    assert isinstance(m.blocks[0].tmix.r_proj, nn.Linear)
+    lora = m.blocks[2].tmix.v_proj
+    assert isinstance(lora, rq.LoRALinear) and isinstance(lora.linear, rq.QuantizedLinear)
+    assert lora.scale == 1.0 and lora.lora_a.shape == (16, 128) and lora.lora_b.shape == (128, 16)
+    trainable = {k for k, p in m.named_parameters() if p.requires_grad}
+    assert trainable and all(k.endswith(("lora_a", "lora_b")) for k in trainable)
+    assert len(trainable) == 16
+    with pytest.raises(ValueError, match="requantize"):
+        lora.merged_weight()
+
+
+def test_negative_layer_indices(rq):
+    m = Tiny()
+    m, info = rq.add_lora(m, layers=[-1])
+    assert isinstance(m.blocks[2].tmix.r_proj, rq.LoRALinear)
+    assert not isinstance(m.blocks[0].tmix.r_proj, rq.LoRALinear)
+
+
+def test_merge_lora_dense_base_cpu(rq):
+    torch.manual_seed(0)
+    m = Tiny(device="cpu").float()
+    m, _ = rq.add_lora(m, rank=4, alpha=8.0, layers=[0])
+    lora = m.blocks[0].tmix.r_proj
+    with torch.no_grad():
+        lora.lora_b.normal_()
+    x = torch.randn(3, 128)
+    y = lora(x)
+    rq.merge_lora(m)
+    assert isinstance(m.blocks[0].tmix.r_proj, nn.Linear)
+    assert torch.allclose(m.blocks[0].tmix.r_proj(x), y, atol=1e-4, rtol=1e-4)
+
+
+def test_save_load_lora_roundtrip(rq, tmp_path):
+    torch.manual_seed(1)
+    m = Tiny(device="cpu").float()
+    m, _ = rq.add_lora(m, rank=4, layers=[1])
+    with torch.no_grad():
+        m.blocks[1].tmix.k_proj.lora_b.normal_()
+    path = str(tmp_path / "adapters.safetensors")
+    rq.save_lora(m, path)
+    m2 = Tiny(device="cpu").float()
+    m2, _ = rq.add_lora(m2, rank=4, layers=[1])
+    rq.load_lora(m2, path)
+    for k, v in rq.lora_state(m).items():
+        assert torch.equal(v, dict(m2.named_parameters())[k])

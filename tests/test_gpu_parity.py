@@ -1,0 +1,465 @@
+"""GPU parity: the HIP library (through the C ABI, via the torch ops) against
+the CPU oracle on identical seeded inputs.
+
+Bar: quantize codes/words, scales and biases bit-exact; pack/unpack
+bit-exact; dequantize bit-exact to the oracle's MLX arithmetic (multiply and
+add each rounded in the scales dtype); quantized_matmul within rel-err 1e-2
+(bf16 operands, fp32 accumulation) -- Frobenius-relative and elementwise
+against the largest reference magnitude.
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+BITS = (2, 3, 4, 5, 6, 8)
+GROUPS = (32, 64, 128)
+TOL = 1e-2
+
+
+def weights(R, K, seed, dtype=torch.bfloat16, std=0.02):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(R, K, generator=g) * std).to(dtype)
+
+
+def acts(M, K, seed, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed + 500)
+    return torch.randn(M, K, generator=g).to(dtype)
+
+
+def special_rows(K, dtype):
+    rows = [
+        torch.zeros(K),                                   # all-zero groups
+        torch.full((K,), 0.37),                           # constant groups
+        -torch.linspace(0.1, 2.0, K),                     # all negative
+        torch.linspace(0.1, 2.0, K),                      # all positive
+        torch.linspace(-1.0, 1.0, K),                     # exact ties at 2^b grids
+        torch.randn(K, generator=torch.Generator().manual_seed(9)) * 1e3,
+        torch.randn(K, generator=torch.Generator().manual_seed(10)) * 1e-5,
+    ]
+    r = torch.stack(rows)
+    r[:, ::5] = 0.0
+    r[0] = 0.0
+    return r.to(dtype)
+
+
+def rel_check(y, ref, tol=TOL, what=""):
+    y, ref = y.detach().double().cpu(), ref.detach().double().cpu()
+    assert y.shape == ref.shape, (what, y.shape, ref.shape)
+    assert torch.isfinite(y).all(), what
+    denom = ref.norm().item()
+    if denom == 0:
+        assert y.abs().max().item() == 0, what
+        return
+    fro = (y - ref).norm().item() / denom
+    elem = (y - ref).abs().max().item() / ref.abs().max().item()
+    assert fro <= tol and elem <= tol, f"{what}: frobenius rel-err {fro:.3e}, elementwise {elem:.3e}"
+
+
+def bits_equal(a, b):
+    a, b = a.detach().cpu().contiguous(), b.detach().cpu().contiguous()
+    if a.dtype in (torch.bfloat16, torch.float16):
+        return torch.equal(a.view(torch.int16), b.view(torch.int16))
+    if a.dtype == torch.float32:
+        return torch.equal(a.view(torch.int32), b.view(torch.int32))
+    return torch.equal(a, b)
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+# ------------------------------------------------------------ quantize
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_quantize_bit_exact(O, rq, dev, bits, gs, dtype):
+    K = 512
+    w = torch.cat([weights(57, K, 1000 * bits + gs, dtype), special_rows(K, dtype)])
+    say(f"quantize bits={bits} gs={gs} dtype={dtype} shape={tuple(w.shape)}")
+    wq, s, b = rq.quantize(w.to(dev), gs, bits)
+    torch.cuda.synchronize()
+    owq, os_, ob = O.quantize(w, gs, bits)
+    assert torch.equal(wq.cpu(), owq), "packed words differ"
+    assert bits_equal(s, os_) and bits_equal(b, ob), "scales/biases differ"
+    assert torch.equal(rq.unpack_codes(wq, bits).cpu(), O.unpack(owq, bits))
+
+
+def test_quantize_config1_shape(O, rq, dev):
+    """RWKV-7 0.1B FFN key [3072, 768], 4-bit g64."""
+    w = weights(3072, 768, 1_000_000 + 4)
+    say("quantize config1 [3072,768]")
+    wq, s, b = rq.quantize(w.to(dev), 64, 4)
+    owq, os_, ob = O.quantize(w, 64, 4)
+    assert torch.equal(wq.cpu(), owq) and bits_equal(s, os_) and bits_equal(b, ob)
+
+
+# ------------------------------------------------------- pack / unpack
+
+@pytest.mark.parametrize("bits", BITS)
+def test_pack_unpack_bit_exact(O, rq, dev, bits):
+    g = torch.Generator().manual_seed(bits)
+    codes = torch.randint(0, 1 << bits, (37, 384), generator=g).to(torch.uint8)
+    say(f"pack/unpack bits={bits}")
+    wq = rq.pack_codes(codes.to(dev), bits)
+    assert torch.equal(wq.cpu(), O.pack(codes, bits))
+    assert torch.equal(rq.unpack_codes(wq, bits).cpu(), codes)
+
+
+# ----------------------------------------------------------- dequantize
+
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_dequantize_bit_exact(O, rq, dev, bits, gs, sdt):
+    w = torch.cat([weights(45, 256, 77 * bits + gs, sdt), special_rows(256, sdt)])
+    wq, s, b = O.quantize(w, gs, bits)
+    say(f"dequantize bits={bits} gs={gs} sdt={sdt}")
+    got = rq.dequantize(wq.to(dev), s.to(dev), b.to(dev), gs, bits)
+    ref = O.dequantize(wq, s, b, gs, bits)
+    assert got.dtype == sdt and bits_equal(got, ref)
+
+
+# --------------------------------------------------------------- GEMV
+
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 16])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_qmv_parity_bf16(O, rq, dev, bits, gs, M):
+    R, K = 200, 640
+    w = weights(R, K, 31 * bits + gs)
+    wq, s, b = O.quantize(w, gs, bits)
+    x = acts(M, K, M + bits)
+    say(f"qmv bits={bits} gs={gs} M={M}")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
+    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32)
+    assert y.dtype == torch.bfloat16
+    rel_check(y, ref, what=f"qmv b{bits} g{gs} M{M}")
+
+
+@pytest.mark.parametrize("xdt,sdt", [(torch.float32, torch.bfloat16), (torch.float32, torch.float32),
+                                     (torch.float16, torch.float16), (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("bits,gs", [(4, 64), (4, 32), (6, 32), (3, 64), (8, 64), (5, 32)])
+def test_qmv_parity_dtypes(O, rq, dev, bits, gs, xdt, sdt):
+    """fp32 activations (the reference's default residual stream,
+    rwkv_metal/model/rwkv7_x070.py:51) and fp32 scales at g32 (RwkvqNativeLinear,
+    rwkv_metal/lora/rwkvq_native.py:119-122)."""
+    R, K, M = 130, 512, 3
+    w = weights(R, K, 5 * bits + gs, sdt)
+    wq, s, b = O.quantize(w, gs, bits)
+    x = acts(M, K, 8, xdt)
+    say(f"qmv dtypes x={xdt} s={sdt} bits={bits} gs={gs}")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
+    want = xdt if xdt == sdt else torch.float32
+    assert y.dtype == want
+    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32)
+    rel_check(y, ref, what="qmv dtypes")
+
+
+def test_qmv_edge_shapes(O, rq, dev):
+    cases = [(1, 32, 32, 4, 1), (17, 96, 32, 3, 4), (5, 160, 32, 6, 7), (33, 128, 128, 8, 16),
+             (1, 64, 64, 2, 1), (250, 96, 32, 5, 3)]
+    for R, K, gs, bits, M in cases:
+        w = weights(R, K, R + K)
+        wq, s, b = O.quantize(w, gs, bits)
+        x = acts(M, K, R)
+        say(f"qmv edge R={R} K={K} gs={gs} bits={bits} M={M}")
+        y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
+        ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32)
+        rel_check(y, ref, what=f"edge {R}x{K}")
+
+
+# --------------------------------------------------------------- GEMM
+
+@pytest.mark.parametrize("M", [17, 100, 300])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_qmm_t_parity(O, rq, dev, bits, gs, M):
+    R, K = 200, 384
+    w = weights(R, K, 13 * bits + gs)
+    wq, s, b = O.quantize(w, gs, bits)
+    x = acts(M, K, M)
+    say(f"qmm_t bits={bits} gs={gs} M={M}")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
+    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32)
+    rel_check(y, ref, what=f"qmm_t b{bits} g{gs} M{M}")
+
+
+@pytest.mark.parametrize("M", [1, 8, 33, 200])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_qmm_n_parity(O, rq, dev, bits, gs, M):
+    """transpose=False: dX = dY . W, the QLoRA backward through a frozen base."""
+    R, K = 136, 384
+    w = weights(R, K, 17 * bits + gs)
+    wq, s, b = O.quantize(w, gs, bits)
+    dy = acts(M, R, M + 1)
+    say(f"qmm_n bits={bits} gs={gs} M={M}")
+    y = rq.quantized_matmul(dy.to(dev), wq.to(dev), s.to(dev), b.to(dev), False, gs, bits)
+    ref = O.quantized_matmul(dy, wq, s, b, False, gs, bits, out_dtype=torch.float32)
+    rel_check(y, ref, what=f"qmm_n b{bits} g{gs} M{M}")
+
+
+@pytest.mark.parametrize("R", [130, 77, 64])
+def test_qmm_n_unaligned_rows(O, rq, dev, R):
+    """Row counts whose activation rows are not 16-byte multiples (scalar loads)."""
+    K, gs, bits = 256, 64, 4
+    w = weights(R, K, R)
+    wq, s, b = O.quantize(w, gs, bits)
+    for xdt in (torch.bfloat16, torch.float32):
+        dy = acts(45, R, R, xdt)
+        say(f"qmm_n unaligned R={R} x={xdt}")
+        y = rq.quantized_matmul(dy.to(dev), wq.to(dev), s.to(dev), b.to(dev), False, gs, bits)
+        ref = O.quantized_matmul(dy, wq, s, b, False, gs, bits, out_dtype=torch.float32)
+        rel_check(y, ref, what=f"qmm_n R{R}")
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16])
+def test_qmm_t_other_dtypes(O, rq, dev, xdt):
+    R, K, M, gs, bits = 192, 256, 70, 32, 5
+    w = weights(R, K, 3, torch.float32 if xdt == torch.float32 else xdt)
+    wq, s, b = O.quantize(w, gs, bits)
+    x = acts(M, K, 2, xdt)
+    say(f"qmm_t x={xdt}")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
+    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32)
+    rel_check(y, ref, what="qmm_t dtypes")
+
+
+# ---------------------------------------------------- BASELINE configs
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_config1_roundtrip_and_matmul(O, rq, dev, M):
+    """0.1B FFN key [3072, 768] 4-bit g64: quantize -> unpack -> dequant -> y = x.Wq^T."""
+    w = weights(3072, 768, 1_000_000 + 4)
+    x = acts(M, 768, 1_000_000 + 4)
+    say(f"config1 M={M}")
+    wq, s, b = rq.quantize(w.to(dev), 64, 4)
+    owq, os_, ob = O.quantize(w, 64, 4)
+    assert torch.equal(wq.cpu(), owq)
+    assert torch.equal(rq.unpack_codes(wq, 4).cpu(), O.unpack(owq, 4))
+    assert bits_equal(rq.dequantize(wq, s, b, 64, 4), O.dequantize(owq, os_, ob, 64, 4))
+    y = rq.quantized_matmul(x.to(dev), wq, s, b, True, 64, 4)
+    rel_check(y, O.quantized_matmul(x, owq, os_, ob, True, 64, 4, out_dtype=torch.float32))
+
+
+CONFIG2 = {"r": (2048, 2048), "ffn_key": (8192, 2048), "ffn_value": (2048, 8192),
+           "head": (65536, 2048)}
+
+
+@pytest.mark.parametrize("M", [1, 8])
+@pytest.mark.parametrize("name", list(CONFIG2))
+def test_config2_decode_shapes(O, rq, dev, name, M):
+    R, K = CONFIG2[name]
+    w = weights(R, K, 2_000_000 + 6)
+    wq, s, b = O.quantize(w, 64, 4)
+    x = acts(M, K, 2_000_000 + 6)
+    say(f"config2 {name} M={M}")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
+    ref = O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32)
+    rel_check(y, ref, what=f"config2 {name}")
+
+
+def _gpu_dense_ref(rq, x, wq, s, b, gs, bits, transpose):
+    wd = rq.dequantize(wq, s, b, gs, bits).float()   # bit-exact to the oracle (tested above)
+    return x.float() @ (wd.t() if transpose else wd)
+
+
+@pytest.mark.parametrize("M", [512, 2048, 4096])
+@pytest.mark.parametrize("shape", [(2560, 2560), (10240, 2560), (2560, 10240)])
+def test_config3_prefill_full_size(rq, dev, shape, M):
+    """2.9B prefill shapes at full size.  The oracle is too slow here, so the
+    reference is an fp32 matmul of the dequantized weights (dequantize is
+    bit-exact to the oracle) -- a size-independent consistency check."""
+    R, K = shape
+    say(f"config3 {shape} M={M}")
+    w = weights(R, K, 3_000_000 + R).to(dev)
+    wq, s, b = rq.quantize(w, 64, 4)
+    x = acts(M, K, 3_000_000 + M).to(dev)
+    y = rq.quantized_matmul(x, wq, s, b, True, 64, 4)
+    rel_check(y, _gpu_dense_ref(rq, x, wq, s, b, 64, 4, True), what=f"config3 {shape} M{M}")
+
+
+def test_config3_oracle_small_m(O, rq, dev):
+    R, K, M = 2560, 2560, 512
+    w = weights(R, K, 3_000_000 + R)
+    wq, s, b = O.quantize(w, 64, 4)
+    x = acts(M, K, 3_000_512)
+    say("config3 oracle M=512")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
+    rel_check(y, O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32))
+
+
+@pytest.mark.parametrize("shape", [(2048, 2048), (8192, 2048), (2048, 8192)])
+def test_config4_transposed_full_size(rq, dev, shape):
+    """QLoRA backward dX = dY . W at D=2048, M = 8 x 512."""
+    R, K = shape
+    say(f"config4 dX {shape}")
+    w = weights(R, K, 4_000_000 + R).to(dev)
+    wq, s, b = rq.quantize(w, 64, 4)
+    dy = acts(4096, R, 4_000_800).to(dev)
+    dx = rq.quantized_matmul(dy, wq, s, b, False, 64, 4)
+    rel_check(dx, _gpu_dense_ref(rq, dy, wq, s, b, 64, 4, False), what=f"config4 {shape}")
+
+
+@pytest.mark.parametrize("name,R,K,bits", [("proj", 4096, 4096, 3), ("ffn_key", 16384, 4096, 3),
+                                           ("ffn_value", 4096, 16384, 3),
+                                           ("head", 65536, 4096, 8)])
+def test_config5_mixed_bits(O, rq, dev, name, R, K, bits):
+    """7.2B shapes: 3-bit body (codes straddle words), 8-bit head; M=1 vs the
+    oracle, M=2048 vs the dequantized fp32 reference."""
+    say(f"config5 {name}")
+    w = weights(R, K, 5_000_000 + R + bits)
+    wq, s, b = O.quantize(w, 64, bits)
+    gq, gs_, gb = rq.quantize(w.to(dev), 64, bits)
+    assert torch.equal(gq.cpu(), wq) and bits_equal(gs_, s) and bits_equal(gb, b)
+    x1 = acts(1, K, 5_000_500)
+    y1 = rq.quantized_matmul(x1.to(dev), gq, gs_, gb, True, 64, bits)
+    rel_check(y1, O.quantized_matmul(x1, wq, s, b, True, 64, bits, out_dtype=torch.float32))
+    x = acts(2048, K, 5_000_501).to(dev)
+    y = rq.quantized_matmul(x, gq, gs_, gb, True, 64, bits)
+    rel_check(y, _gpu_dense_ref(rq, x, gq, gs_, gb, 64, bits, True), what=f"config5 {name}")
+
+
+# ------------------------------------------------------ grouped launch
+
+def test_grouped_matches_single_calls(O, rq, dev):
+    shapes = [(2048, 2048)] * 4 + [(8192, 2048), (2048, 8192), (300, 640)]
+    xs, ws, refs = [], [], []
+    for i, (R, K) in enumerate(shapes):
+        w = weights(R, K, 60 + i)
+        wq, s, b = O.quantize(w, 64, 4)
+        x = acts(8, K, 60 + i)
+        xs.append(x.to(dev))
+        ws.append((wq.to(dev), s.to(dev), b.to(dev)))
+        refs.append(O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32))
+    say("grouped qmv")
+    ys = rq.grouped_qmv(xs, ws, 64, 4)
+    for y, ref, x, (wq, s, b) in zip(ys, refs, xs, ws):
+        rel_check(y, ref, what="grouped")
+        single = rq.quantized_matmul(x, wq, s, b, True, 64, 4)
+        assert torch.allclose(y.float(), single.float(), rtol=1e-2, atol=1e-3)
+
+
+def test_grouped_more_problems_than_one_launch(O, rq, dev):
+    n = 70   # > RQ_MAX_GROUPED descriptors: two launches
+    xs, ws, refs = [], [], []
+    for i in range(n):
+        w = weights(64, 256, 900 + i)
+        wq, s, b = O.quantize(w, 64, 4)
+        x = acts(1, 256, 900 + i)
+        xs.append(x.to(dev))
+        ws.append((wq.to(dev), s.to(dev), b.to(dev)))
+        refs.append(O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32))
+    say("grouped qmv, 70 problems")
+    for y, ref in zip(rq.grouped_qmv(xs, ws, 64, 4), refs):
+        rel_check(y, ref, what="grouped70")
+
+
+# ---------------------------------------------- autograd / modules / LoRA
+
+def test_autograd_dx_is_transposed_qmm(O, rq, dev):
+    R, K, M = 256, 512, 24
+    w = weights(R, K, 44)
+    wq, s, b = O.quantize(w, 64, 4)
+    x = acts(M, K, 44).to(dev).requires_grad_(True)
+    say("autograd")
+    y = rq.quantized_matmul(x, wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
+    g = acts(M, R, 45)
+    y.backward(g.to(dev))
+    ref = O.quantized_matmul(g, wq, s, b, False, 64, 4, out_dtype=torch.float32)
+    rel_check(x.grad, ref, what="dX")
+
+
+def test_qlora_layer_forward_backward(rq, dev):
+    """BASELINE config 4 math at a reduced shape: y = qmm(x,Wq) + (a/r)(xA^T)B^T;
+    grads of x, A, B against an fp32 dense reference on the dequantized base."""
+    torch.manual_seed(0)
+    D, R, M, r, alpha = 512, 768, 96, 16, 16.0
+    lin = torch.nn.Linear(D, R, bias=False).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(weights(R, D, 7).to(dev))
+    layer = rq.LoRALinear(lin, rank=r, alpha=alpha, quantize_base=4, q_group_size=64)
+    g = torch.Generator().manual_seed(600)
+    with torch.no_grad():
+        layer.lora_a.copy_((torch.randn(r, D, generator=g) / D ** 0.5).to(torch.bfloat16))
+        layer.lora_b.copy_((torch.randn(R, r, generator=g) * 0.01).to(torch.bfloat16))
+    x = acts(M, D, 9).to(dev).requires_grad_(True)
+    say("qlora layer")
+    y = layer(x)
+    dy = acts(M, R, 800).to(dev)
+    y.backward(dy)
+    wd = layer.linear.dequantized_weight().float()
+    xr = x.detach().float().requires_grad_(True)
+    A = layer.lora_a.detach().float().requires_grad_(True)
+    B = layer.lora_b.detach().float().requires_grad_(True)
+    yr = xr @ wd.t() + (alpha / r) * ((xr @ A.t()) @ B.t())
+    yr.backward(dy.float())
+    rel_check(y, yr, what="qlora y")
+    rel_check(x.grad, xr.grad, what="qlora dx")
+    rel_check(layer.lora_a.grad, A.grad, what="qlora dA")
+    rel_check(layer.lora_b.grad, B.grad, what="qlora dB")
+
+
+def test_quantized_embedding_and_linear_module(O, rq, dev):
+    emb = torch.nn.Embedding(1000, 256).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        emb.weight.copy_(weights(1000, 256, 3).to(dev))
+    qe = rq.QuantizedEmbedding.from_embedding(emb, 64, 4)
+    idx = torch.tensor([[0, 5, 999], [17, 17, 3]], device=dev)
+    say("quantized embedding")
+    out = qe(idx)
+    owq, os_, ob = O.quantize(weights(1000, 256, 3), 64, 4)
+    ref = O.dequantize(owq, os_, ob, 64, 4)[idx.cpu()]
+    assert bits_equal(out, ref)
+    lin = torch.nn.Linear(256, 96, bias=True).to(dev, torch.bfloat16)
+    ql = rq.QuantizedLinear.from_linear(lin, 64, 4)
+    x = acts(4, 256, 1).to(dev)
+    ref = x.float() @ ql.dequantized_weight().float().t() + lin.bias.float()
+    rel_check(ql(x), ref, what="QuantizedLinear")
+
+
+# --------------------------------------------------- determinism / edges
+
+def test_repeated_launches_bitwise_identical(rq, dev):
+    """Race regression: five launches of each kernel family give identical bits."""
+    w = weights(4096, 2048, 12).to(dev)
+    wq, s, b = rq.quantize(w, 64, 4)
+    say("determinism")
+    for M, tr in ((1, True), (8, True), (256, True), (256, False)):
+        x = acts(M, 2048 if tr else 4096, M).to(dev)
+        outs = [rq.quantized_matmul(x, wq, s, b, tr, 64, 4) for _ in range(5)]
+        assert all(torch.equal(outs[0], o) for o in outs[1:]), (M, tr)
+    q2 = [rq.quantize(w, 64, 4)[0] for _ in range(3)]
+    assert all(torch.equal(q2[0], q) for q in q2)
+
+
+def test_empty_and_unaligned_inputs(O, rq, dev):
+    w = weights(64, 256, 1)
+    wq, s, b = O.quantize(w, 64, 4)
+    wq, s, b = wq.to(dev), s.to(dev), b.to(dev)
+    say("empty/unaligned")
+    y = rq.quantized_matmul(torch.empty(0, 256, device=dev, dtype=torch.bfloat16), wq, s, b,
+                            True, 64, 4)
+    assert y.shape == (0, 64)
+    big = acts(3, 257, 2).to(dev)
+    x = big[:, 1:]                      # storage offset 1 element: not 16-byte aligned
+    y = rq.quantized_matmul(x, wq, s, b, True, 64, 4)
+    ref = O.quantized_matmul(x.cpu().contiguous(), wq.cpu(), s.cpu(), b.cpu(), True, 64, 4,
+                             out_dtype=torch.float32)
+    rel_check(y, ref, what="unaligned x")
+    xt = acts(256, 3, 4).to(dev).t()    # non-contiguous view
+    y = rq.quantized_matmul(xt, wq, s, b, True, 64, 4)
+    ref = O.quantized_matmul(xt.cpu().contiguous(), wq.cpu(), s.cpu(), b.cpu(), True, 64, 4,
+                             out_dtype=torch.float32)
+    rel_check(y, ref, what="transposed view x")
+
+
+def test_uint32_words_accepted(O, rq, dev):
+    w = weights(32, 128, 2)
+    wq, s, b = O.quantize(w, 64, 4)
+    x = acts(1, 128, 2)
+    y1 = rq.quantized_matmul(x.to(dev), wq.to(dev).view(torch.uint32), s.to(dev), b.to(dev))
+    y2 = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev))
+    assert torch.equal(y1, y2)

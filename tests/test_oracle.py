@@ -1,0 +1,224 @@
+"""Pins the CPU oracle (oracle/rq_oracle.c) before it is trusted as the checker.
+
+Each check is an independent statement of what the reference fixes, not a
+retyping of the oracle's formula:
+  * packing: a Python big-integer bitstream, hand-derived word/bit positions
+    (rwkv_metal/lora/rwkvq_native.py:18-33) and the reference's own one-hot
+    probe (tests/dev_reverse_mlx_pack.py:8-44) with hand-derived codes;
+  * quantize: nearest-code brute force, exact extremes, exactly representable
+    zero, constant and all-zero groups, reconstruction bound;
+  * dequantize: torch's own bf16/fp32 elementwise arithmetic (multiply then
+    add, each rounded -- MLX's composite op order);
+  * quantized_matmul: float64 dense matmul of the dequantized weights and a
+    pure-Python loop on tiny shapes, for both transposes.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+BITS = (2, 3, 4, 5, 6, 8)
+GROUPS = (32, 64, 128)
+
+
+def bigint_pack(codes, bits):
+    """Row-wise LSB-first bitstream via Python integers."""
+    rows, K = codes.shape
+    out = np.zeros((rows, K * bits // 32), dtype=np.uint32)
+    for r in range(rows):
+        acc = 0
+        for j in range(K):
+            acc |= int(codes[r, j]) << (j * bits)
+        for w in range(K * bits // 32):
+            out[r, w] = (acc >> (32 * w)) & 0xFFFFFFFF
+    return out
+
+
+@pytest.mark.parametrize("bits", BITS)
+def test_pack_matches_bigint_bitstream(O, bits):
+    g = torch.Generator().manual_seed(100 + bits)
+    codes = torch.randint(0, 1 << bits, (5, 256), generator=g, dtype=torch.int64).to(torch.uint8)
+    wq = O.pack(codes, bits)
+    ref = bigint_pack(codes.numpy(), bits)
+    assert np.array_equal(wq.numpy().view(np.uint32), ref)
+    assert torch.equal(O.unpack(wq, bits), codes)
+
+
+def _one_code(bits, pos, val, K=64):
+    c = torch.zeros(1, K, dtype=torch.uint8)
+    c[0, pos] = val
+    return c
+
+
+def test_pack_worked_positions(O):
+    # 4-bit: word = c0 | c1<<4 | ... | c7<<28
+    c = torch.tensor([[0, 1, 2, 3, 4, 5, 6, 7] + [0] * 24], dtype=torch.uint8)
+    assert O.pack(c, 4)[0, 0].item() & 0xFFFFFFFF == 0x76543210
+    # 8-bit: c0 | c1<<8 | c2<<16 | c3<<24
+    c = torch.tensor([[1, 2, 3, 4] + [0] * 28], dtype=torch.uint8)
+    assert O.pack(c, 8)[0, 0].item() & 0xFFFFFFFF == 0x04030201
+    u = lambda t: [int(v) & 0xFFFFFFFF for v in t[0].tolist()]
+    # 3-bit: code 10 = bits 30..32 -> word0 bits 30,31 and word1 bit 0
+    assert u(O.pack(_one_code(3, 10, 0b111, 32), 3)) == [0xC0000000, 0x1, 0x0]
+    # 3-bit: code 21 = bits 63..65 -> word1 bit 31 (lsb of 0b101) and word2 bits 0..1 (0b10)
+    assert u(O.pack(_one_code(3, 21, 0b101, 32), 3)) == [0x0, 0x80000000, 0x2]
+    # 6-bit: code 5 = bits 30..35; code 10 = bits 60..65
+    assert u(O.pack(_one_code(6, 5, 0x3F, 32), 6))[:2] == [0xC0000000, 0xF]
+    assert u(O.pack(_one_code(6, 10, 0x3F, 32), 6))[1:3] == [0xF0000000, 0x3]
+    # 5-bit: code 6 = bits 30..34 -> word0 bits 30,31 and word1 bits 0..2
+    assert u(O.pack(_one_code(5, 6, 0x1F, 32), 5))[:2] == [0xC0000000, 0x7]
+
+
+def test_reference_probe_6bit_g32(O):
+    """tests/dev_reverse_mlx_pack.py:20-44: anchors 0 and 31 fix min/max, the
+    interior holds 15.0; moving one interior position to 20.0 must change only
+    the 6 bits of that position.  Hand derivation for this input:
+      min=0, max=31, |min|<=|max| -> scale = -(31/63), edge = 31,
+      q0 = rint(31/scale) = -63 -> scale = 31/-63, bias = 31;
+      code(0) = 63, code(15) = rint(32.516) = 33, code(31) = 0, code(20) = rint(22.35) = 22."""
+    base = [0.0] + [15.0] * 30 + [31.0]
+    w = torch.tensor([base], dtype=torch.float32)
+    wq, s, b = O.quantize(w, group_size=32, bits=6)
+    assert s.item() == np.float32(31.0) / np.float32(-63.0)
+    assert b.item() == 31.0
+    assert O.unpack(wq, 6)[0].tolist() == [63] + [33] * 30 + [0]
+    row = lambda t: sum((int(v) & 0xFFFFFFFF) << (32 * i) for i, v in enumerate(t[0].tolist()))
+    base_bits = row(wq)
+    for p in range(1, 31):
+        vals = list(base)
+        vals[p] = 20.0
+        wq_p, s_p, b_p = O.quantize(torch.tensor([vals]), group_size=32, bits=6)
+        assert s_p.item() == s.item() and b_p.item() == b.item()
+        diff = row(wq_p) ^ base_bits
+        assert diff & ~(0x3F << (6 * p)) == 0, f"position {p} touched bits outside its field"
+        assert (row(wq_p) >> (6 * p)) & 0x3F == 22
+
+
+def _groups_f32(gs, n, seed):
+    g = torch.Generator().manual_seed(seed)
+    kinds = [
+        torch.randn(n, gs, generator=g) * 0.02,
+        torch.rand(n, gs, generator=g) * 3 + 0.5,          # all positive
+        -(torch.rand(n, gs, generator=g) * 3 + 0.5),       # all negative
+        torch.randn(n, gs, generator=g) * torch.logspace(-4, 4, n).unsqueeze(1),
+    ]
+    w = torch.cat(kinds)
+    w[::7, 3] = 0.0   # exact zeros inside groups
+    return w
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("gs", GROUPS)
+def test_quantize_nearest_code_and_extremes(O, bits, gs):
+    n_bins = (1 << bits) - 1
+    w = _groups_f32(gs, 16, 7 * bits + gs)
+    wq, s, b = O.quantize(w, group_size=gs, bits=bits)   # one group per row, f32 scales
+    codes = O.unpack(wq, bits).to(torch.float64)
+    s64, b64, w64 = s.double(), b.double(), w.double()
+    recon = s64 * codes + b64
+    err = (w64 - recon).abs()
+    # every code is the nearest grid point (up to fp32 rounding of (w-b)/s)
+    grid = s64 * torch.arange(n_bins + 1, dtype=torch.float64) + b64      # [rows, n_bins+1]
+    best = (w64.unsqueeze(-1) - grid.unsqueeze(1)).abs().min(-1).values
+    assert torch.all(err <= best + 1e-5 * s64.abs() + 1e-12)
+    # inside the grid the error is at most half a step (the zero-point rounding
+    # can leave the far extreme outside the grid, where the nearest end is used)
+    lo, hi = grid.min(-1, keepdim=True).values, grid.max(-1, keepdim=True).values
+    inside = (w64 >= lo) & (w64 <= hi)
+    assert torch.all(err[inside] <= (s64.abs() * (0.5 + 1e-5) + 1e-12).expand_as(err)[inside])
+    # the larger-magnitude extreme is stored exactly as the bias, at code 0
+    mn, mx = w.min(1).values, w.max(1).values
+    edge = torch.where(mn.abs() > mx.abs(), mn, mx)
+    nz = b != 0
+    assert torch.equal(b[nz.squeeze(1)].squeeze(1), edge[nz.squeeze(1)])
+    idx = torch.where(mn.abs() > mx.abs(), w.argmin(1), w.argmax(1))
+    assert torch.all(codes[torch.arange(len(w)), idx][nz.squeeze(1)] == 0)
+    # zero is exactly representable: code(0) = -q0 and s*code + b == 0 in exact arithmetic
+    rows0 = torch.nonzero((w == 0).any(1) & nz.squeeze(1)).flatten()
+    for r in rows0.tolist():
+        c = codes[r, (w[r] == 0).nonzero()[0, 0]]
+        assert abs(s64[r, 0] * c + b64[r, 0]) <= 4e-7 * abs(b64[r, 0])
+
+
+@pytest.mark.parametrize("bits", BITS)
+def test_quantize_constant_and_zero_groups(O, bits):
+    w = torch.tensor([[0.0] * 64, [0.75] * 64, [-3.5] * 64], dtype=torch.bfloat16)
+    wq, s, b = O.quantize(w, group_size=64, bits=bits)
+    codes = O.unpack(wq, bits)
+    assert torch.all(codes == 0)
+    assert b.float().tolist() == [[0.0], [0.75], [-3.5]]
+    dq = O.dequantize(wq, s, b, 64, bits)
+    assert torch.equal(dq, w)
+
+
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("bits", (3, 4, 8))
+def test_dequantize_matches_torch_elementwise(O, sdt, bits):
+    g = torch.Generator().manual_seed(3 + bits)
+    R, K, gs = 16, 256, 64
+    codes = torch.randint(0, 1 << bits, (R, K), generator=g).to(torch.uint8)
+    wq = O.pack(codes, bits)
+    s = (torch.randn(R, K // gs, generator=g) * 0.01).to(sdt)
+    b = (torch.randn(R, K // gs, generator=g) * 0.1).to(sdt)
+    got = O.dequantize(wq, s, b, gs, bits)
+    s_e = s.repeat_interleave(gs, 1)
+    b_e = b.repeat_interleave(gs, 1)
+    ref = codes.to(sdt) * s_e      # torch rounds the product to sdt
+    ref = ref + b_e                # and the sum again
+    assert got.dtype == sdt
+    assert torch.equal(got.view(torch.int16) if sdt != torch.float32 else got.view(torch.int32),
+                       ref.view(torch.int16) if sdt != torch.float32 else ref.view(torch.int32))
+
+
+@pytest.mark.parametrize("transpose", [True, False])
+@pytest.mark.parametrize("bits,gs", [(4, 64), (3, 64), (8, 32), (5, 128)])
+def test_qmm_matches_dense_float64(O, transpose, bits, gs):
+    g = torch.Generator().manual_seed(bits * 10 + gs)
+    R, K, M = 48, 256, 5
+    w = (torch.randn(R, K, generator=g) * 0.02).to(torch.bfloat16)
+    wq, s, b = O.quantize(w, gs, bits)
+    wd = O.dequantize(wq, s, b, gs, bits).double()
+    x = torch.randn(M, K if transpose else R, generator=g).to(torch.bfloat16)
+    y = O.quantized_matmul(x, wq, s, b, transpose, gs, bits, out_dtype=torch.float32)
+    ref = x.double() @ (wd.t() if transpose else wd)
+    assert y.shape == ref.shape
+    assert torch.allclose(y.double(), ref, rtol=1e-6, atol=1e-6)
+
+
+def test_qmm_tiny_python_loop(O):
+    g = torch.Generator().manual_seed(5)
+    R, K, M, gs, bits = 3, 64, 2, 32, 4
+    w = torch.randn(R, K, generator=g)
+    wq, s, b = O.quantize(w, gs, bits)             # f32 scales
+    codes = O.unpack(wq, bits)
+    x = torch.randn(M, K, generator=g)
+    y = O.quantized_matmul(x, wq, s, b, True, gs, bits)
+    for m in range(M):
+        for r in range(R):
+            acc = 0.0
+            for k in range(K):
+                sc, bi = float(s[r, k // gs]), float(b[r, k // gs])
+                wv = float(np.float32(np.float32(sc * int(codes[r, k])) + np.float32(bi)))
+                acc += float(x[m, k]) * wv
+            assert math.isclose(float(y[m, r]), acc, rel_tol=1e-6, abs_tol=1e-6)
+    x2 = torch.randn(M, R, generator=g)
+    y2 = O.quantized_matmul(x2, wq, s, b, False, gs, bits)
+    for m in range(M):
+        for k in range(K):
+            acc = 0.0
+            for r in range(R):
+                sc, bi = float(s[r, k // gs]), float(b[r, k // gs])
+                wv = float(np.float32(np.float32(sc * int(codes[r, k])) + np.float32(bi)))
+                acc += float(x2[m, r]) * wv
+            assert math.isclose(float(y2[m, k]), acc, rel_tol=1e-6, abs_tol=1e-6)
+
+
+def test_quantize_rejects_bad_arguments(O):
+    w = torch.zeros(2, 64)
+    with pytest.raises(ValueError):
+        O.quantize(w, 48, 4)
+    with pytest.raises(ValueError):
+        O.quantize(w, 64, 7)
+    with pytest.raises(ValueError):
+        O.quantize(torch.zeros(2, 96), 64, 4)
