@@ -107,8 +107,9 @@ typedef struct {
 
 /* Several independent decode GEMVs (m <= 16, transpose=True) sharing m, bits,
  * group_size and dtypes.  `problems` is a HOST array of n descriptors; they
- * are copied into kernel arguments, RQ_MAX_GROUPED per launch, so n
- * descriptors cost ceil(n / RQ_MAX_GROUPED) launches. */
+ * are bucketed by cols and copied into kernel arguments, at most
+ * RQ_MAX_GROUPED per launch: one launch per bucket per RQ_MAX_GROUPED
+ * descriptors. */
 #define RQ_MAX_GROUPED 48
 int rq_qmm_grouped(const rq_problem* problems, int n, rq_dtype x_dt, rq_dtype sb_dt,
                    rq_dtype y_dt, int64_t m, int group_size, int bits, void* stream);

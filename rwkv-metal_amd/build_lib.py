@@ -44,8 +44,8 @@ def _units():
     return units
 
 
-def _compile(src, extra, obj):
-    cmd = [HIPCC, *FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", os.path.join(OBJ, obj)]
+def _compile(src, extra, obj, objdir=OBJ):
+    cmd = [HIPCC, *FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", os.path.join(objdir, obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)
@@ -54,31 +54,38 @@ def _compile(src, extra, obj):
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> str:
-    os.makedirs(OBJ, exist_ok=True)
+def build(jobs: int | None = None, verbose: bool = False, defines=(), out: str = LIB,
+          objdir: str = OBJ) -> str:
+    """Compile and link.  `defines` (e.g. ["-DRQ_QMV_NS=6"]) override the
+    kernels' compile-time tuning constants; `out`/`objdir` redirect the
+    products (used to build side-by-side variants)."""
+    os.makedirs(objdir, exist_ok=True)
     jobs = jobs or min(8, os.cpu_count() or 4)
-    units = _units()
+    units = [(src, [*extra, *defines], obj, objdir) for src, extra, obj in _units()]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = [ex.submit(_compile, *u) for u in units]
         for f in cf.as_completed(futs):
             obj = f.result()
             if verbose:
                 print(f"  compiled {obj}", flush=True)
-    objs = [os.path.join(OBJ, u[2]) for u in units]
-    tmp = LIB + ".tmp"
+    objs = [os.path.join(objdir, u[2]) for u in units]
+    tmp = out + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB}", flush=True)
-    return LIB
+        print(f"built {out}", flush=True)
+    return out
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
+    ap.add_argument("-D", action="append", default=[], help="extra -D define")
+    ap.add_argument("-o", default=LIB)
+    ap.add_argument("--objdir", default=OBJ)
     a = ap.parse_args()
-    build(a.j, verbose=True)
+    build(a.j, verbose=True, defines=[f"-D{d}" for d in a.D], out=a.o, objdir=a.objdir)
     sys.exit(0)

@@ -36,14 +36,26 @@
 //        acc += s * D + (b/128 - s) * O  ==  s * sum q x + b * sum x.
 //    8-bit codes use exact bf16(q) operands (q <= 255 has 8 significant
 //    bits) and a constant B of 1.0.
-//  * A block of 4 waves owns 16*RB rows; the waves split the spans of K and
-//    their partial sums meet in LDS at the end.  One launch can cover many
-//    independent problems (rq_qmm_grouped): each block looks its problem up
-//    in a prefix table of block counts.
+//  * Work unit ("task") = 16*RB rows of one problem.  A block of 4 waves
+//    takes 4 consecutive tasks of one problem (KS=1, each wave walks every
+//    span of K for its own rows) or, for small launches, one task whose
+//    spans the 4 waves split and sum in LDS (KS=4).
+//  * The activation rows x[0..M) of the block's problem are staged once in
+//    LDS as bf16; A operands are read from there for every span, so only
+//    packed codes (and their scales) live in registers: a wave issues the
+//    loads of NS spans at once and consumes them in order.  Packed codes use
+//    non-temporal loads (they are read once).
+//    When M*K*2 bytes exceed the LDS budget, A comes from global memory.
+//  * One launch can cover many independent problems (rq_qmm_grouped): a
+//    block finds its problem by binary search in a prefix table of block
+//    counts held in the kernel arguments.
+
 #include "rq_common.h"
 #include "rq_launch.h"
 
 #include <cstring>
+#include <vector>
+#include <type_traits>
 
 #ifndef RQ_BITS
 #error "compile rq_qmv.hip once per bit width with -DRQ_BITS=<bits>"
@@ -54,13 +66,32 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kBlock = 64 * kWaves;
 
+// Compile-time tuning constants (overridable with -D for side-by-side builds).
+#ifndef RQ_QMV_NS
+#define RQ_QMV_NS 4  // rolling pipeline stages (LDS-staged path): NS-1 spans in flight
+#endif
+#ifndef RQ_QMV_BATCH
+#define RQ_QMV_BATCH 8  // spans per batch on the global-scale path
+#endif
+#ifndef RQ_QMV_WAVES_PER_EU
+#define RQ_QMV_WAVES_PER_EU 0  // >0: ask the compiler for this occupancy
+#endif
+#ifndef RQ_QMV_BIG_RB
+#define RQ_QMV_BIG_RB 1  // 16-row blocks per wave for big launches
+#endif
+#if RQ_QMV_WAVES_PER_EU > 0
+#define RQ_QMV_OCC __attribute__((amdgpu_waves_per_eu(RQ_QMV_WAVES_PER_EU)))
+#else
+#define RQ_QMV_OCC
+#endif
+
 struct QmvArgs {
     rq_problem p[RQ_MAX_GROUPED];
-    int block_start[RQ_MAX_GROUPED + 1];
+    int block_start[RQ_MAX_GROUPED + 1];  // prefix sums of blocks per problem
     int n;
     int m;
     int gs_shift;
-    int sb_dt;
+    int x_dt;
     int y_dt;
 };
 
@@ -121,35 +152,138 @@ RQ_DEV void load_x_run_bf16(const void* x, int64_t off, uint32_t* d) {
     }
 }
 
-template <int BITS, int XDT, int NMC, int RB>
-__global__ __launch_bounds__(kBlock) void qmv_kernel(const QmvArgs args) {
+// Streaming load of one run of packed codes (read once: non-temporal).
+template <int BITS>
+RQ_DEV void load_run_stream(const uint32_t* p, uint32_t* words) {
+    if constexpr (BITS == 4) {
+        const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
+        words[0] = v[0]; words[1] = v[1]; words[2] = v[2]; words[3] = v[3];
+    } else if constexpr (BITS == 8) {
+        const u32x4_t v0 = __builtin_nontemporal_load((const u32x4_t*)p);
+        const u32x4_t v1 = __builtin_nontemporal_load((const u32x4_t*)p + 1);
+        words[0] = v0[0]; words[1] = v0[1]; words[2] = v0[2]; words[3] = v0[3];
+        words[4] = v1[0]; words[5] = v1[1]; words[6] = v1[2]; words[7] = v1[3];
+    } else {
+#pragma unroll
+        for (int w = 0; w < BITS; ++w) words[w] = __builtin_nontemporal_load(p + w);
+    }
+}
+
+template <int BITS, int RB>
+struct Stage {
+    uint32_t cw[RB][BITS];   // this lane's run of its row, per row block
+    uint32_t sc[RB], bi[RB];  // raw bits of that run's scale and bias (global-scale path)
+};
+
+// Raw bits of element i of a scales/biases array of dtype SDT.
+template <int SDT>
+RQ_DEV uint32_t load_raw(const void* p, int64_t i) {
+    if constexpr (SDT == RQ_F32) return ((const uint32_t*)p)[i];
+    else return ((const uint16_t*)p)[i];
+}
+template <int SDT>
+RQ_DEV float raw_to_f32(uint32_t r) {
+    if constexpr (SDT == RQ_F32) return __uint_as_float(r);
+    else if constexpr (SDT == RQ_BF16) return bf16_bits_to_f32(r);
+    else return f16_bits_to_f32(r & 0xffffu);
+}
+
+// One (scale, bias) pair as staged in LDS: two 16-bit values in one dword,
+// or two fp32 values.
+template <int SDT>
+struct SBPair {
+    typedef typename std::conditional<SDT == RQ_F32, uint2, uint32_t>::type type;
+};
+
+constexpr int kLdsBudget = 64 * 1024;  // bytes of LDS staging per block
+
+// SLDS=true (fast path): the block's activations AND its rows' scales/biases
+// are staged in LDS once; the span loop then streams only packed codes, with
+// a rolling NS-stage register pipeline (NS-1 spans always in flight).
+// SLDS=false (large M*K or K): activations and scales come from global
+// memory; spans are processed in batches of NS (all loads of a batch issued
+// first).  In both, loads are never predicated: out-of-range rows and runs
+// read clamped, in-bounds addresses and are neutralised at compute time by a
+// zero scale and bias (s*D + (b/128 - s)*O = 0).
+template <int BITS, int SDT, int NMC, int RB, int KS, int NS, bool SLDS>
+__global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs args) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+    typedef typename SBPair<SDT>::type sbp_t;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int bid = blockIdx.x;
-    int p = 0;
-    while (p + 1 < args.n && args.block_start[p + 1] <= bid) ++p;
+    int lo = 0, hi = args.n - 1;  // last problem whose first block <= bid
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (args.block_start[mid] <= bid) lo = mid; else hi = mid - 1;
+    }
+    const int p = lo;
     const void* __restrict__ x = args.p[p].x;
     const uint32_t* __restrict__ wq = args.p[p].w_q;
     const void* __restrict__ scales = args.p[p].scales;
     const void* __restrict__ biases = args.p[p].biases;
     const int64_t R = args.p[p].rows;
     const int64_t K = args.p[p].cols;
-    const int64_t row0 = (int64_t)(bid - args.block_start[p]) * (16 * RB);
+    const int M = args.m;
+    const int x_dt = args.x_dt;
+    const int gsh = args.gs_shift;
+    const int64_t G = K >> gsh;
+    const int64_t lblock = bid - args.block_start[p];
+    constexpr int kRowsPerBlock = (KS == 1 ? kWaves : 1) * 16 * RB;
+    const int64_t blk_row0 = lblock * kRowsPerBlock;
+    const int64_t row0 = blk_row0 + (KS == 1 ? wave * 16 * RB : 0);
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // LDS: 64 zero bytes (the A operand of inactive lanes), x [M][K] bf16,
+    // then the block's (scale, bias) pairs [kRowsPerBlock][G].
+    uint16_t* xzero = lds;
+    uint16_t* xs = lds + 32;
+    sbp_t* sbs = (sbp_t*)(xs + (((int64_t)M * K + 7) & ~7ll));
+    if constexpr (SLDS) {
+        if (threadIdx.x < 4) *(u32x4_t*)&xzero[threadIdx.x * 8] = u32x4_t{0u, 0u, 0u, 0u};
+        // Stage x[0..M) as bf16: 8 elements per thread per step.
+        const int64_t n8 = (int64_t)M * K / 8;
+        for (int64_t e = threadIdx.x; e < n8; e += kBlock) {
+            uint32_t d[4];
+            if (x_dt == RQ_BF16) {
+                const uint4 v = ((const uint4*)x)[e];
+                d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    d[q] = pack_bf16x2(load_dt(x, x_dt, e * 8 + 2 * q),
+                                       load_dt(x, x_dt, e * 8 + 2 * q + 1));
+            }
+            *(u32x4_t*)&xs[e * 8] = u32x4_t{d[0], d[1], d[2], d[3]};
+        }
+        // Stage the block's (scale, bias) pairs; rows past R are zero pairs.
+        const int64_t nsb = (int64_t)kRowsPerBlock * G;
+        for (int64_t e = threadIdx.x; e < nsb; e += kBlock) {
+            const int64_t rl = e / G, g = e - rl * G;
+            const int64_t row = blk_row0 + rl;
+            sbp_t v;
+            if constexpr (SDT == RQ_F32) {
+                v = row < R ? make_uint2(((const uint32_t*)scales)[row * G + g],
+                                         ((const uint32_t*)biases)[row * G + g])
+                            : make_uint2(0u, 0u);
+            } else {
+                v = row < R ? (uint32_t)((const uint16_t*)scales)[row * G + g] |
+                                  ((uint32_t)((const uint16_t*)biases)[row * G + g] << 16)
+                            : 0u;
+            }
+            sbs[e] = v;
+        }
+        __syncthreads();
+    }
+    if (row0 >= R) return;  // a wave past the end of its problem (after the barrier)
+
     const int lg = lane >> 4;  // lane group: run inside the span / k-slice
     const int lr = lane & 15;  // A row m' / weight row inside a 16-row block
-    const int M = args.m;
-    const int gsh = args.gs_shift;
     const int slot_shift = gsh - 5;  // run index -> group index
     const int MC = 16 >> (7 - gsh);  // activation rows per pass
-    const int sb_dt = args.sb_dt;
 
     const int64_t runs_per_row = K >> 5;
     const int64_t wpr = runs_per_row * BITS;  // packed words per row
-    const int64_t G = K >> gsh;
     const int nspans = (int)((runs_per_row + 3) >> 2);
-
-    // A-side role of this lane: activation row (per pass) and slot.
     const bool a_slot_ok = (lr / MC) == (lg >> slot_shift);
 
     constexpr uint32_t kOne = (BITS == 8) ? 0x3F803F80u : 0x43004300u;  // 1.0 or 128.0
@@ -161,38 +295,47 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(const QmvArgs args) {
 #pragma unroll
         for (int c = 0; c < NMC; ++c) acc[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int s = wave; s < nspans; s += kWaves) {
+    auto load = [&](int s, Stage<BITS, RB>& st) {
         const int64_t run = (int64_t)s * 4 + lg;
-        const bool run_ok = run < runs_per_row;
-
-        // B side: this lane's run of its row in every row block.
-        uint32_t cw[RB][BITS];
-        float sc[RB], bi[RB];
+        const int64_t runc = run < runs_per_row ? run : runs_per_row - 1;
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const int64_t row = row0 + rb * 16 + lr;
-            if (run_ok && row < R) {
-                load_run<BITS>(wq + row * wpr + run * BITS, cw[rb]);
-                const int64_t gi = row * G + (run >> slot_shift);
-                sc[rb] = load_dt(scales, sb_dt, gi);
-                bi[rb] = load_dt(biases, sb_dt, gi);
-            } else {
-#pragma unroll
-                for (int w = 0; w < BITS; ++w) cw[rb][w] = 0u;
-                sc[rb] = 0.f;
-                bi[rb] = 0.f;
+            const int64_t rowc = row < R ? row : R - 1;
+            load_run_stream<BITS>(wq + rowc * wpr + runc * BITS, st.cw[rb]);
+            if constexpr (!SLDS) {
+                const int64_t gi = rowc * G + (runc >> slot_shift);
+                st.sc[rb] = load_raw<SDT>(scales, gi);
+                st.bi[rb] = load_raw<SDT>(biases, gi);
             }
         }
+    };
 
-        // A side: activations of this lane's run for each pass.
+    auto compute = [&](int s, const Stage<BITS, RB>& st) {
+        const int64_t run = (int64_t)s * 4 + lg;
+        const bool run_ok = run < runs_per_row;
         bf16x8_t a[NMC][4];
         f32x4_t o[NMC];
 #pragma unroll
         for (int c = 0; c < NMC; ++c) {
             const int m = c * MC + (lr % MC);
             uint32_t xd[16];
-            if (a_slot_ok && run_ok && m < M) {
-                load_x_run_bf16<XDT>(x, (int64_t)m * K + run * 32, xd);
+            const bool active = a_slot_ok && run_ok && m < M;
+            if constexpr (SLDS) {
+                // branch-free: inactive lanes read the zero line
+                const u32x4_t* src =
+                    (const u32x4_t*)(active ? &xs[(int64_t)m * K + run * 32] : xzero);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const u32x4_t v = src[q];
+                    xd[4 * q] = v[0]; xd[4 * q + 1] = v[1]; xd[4 * q + 2] = v[2]; xd[4 * q + 3] = v[3];
+                }
+            } else if (active) {
+                {
+                    if (x_dt == RQ_BF16) load_x_run_bf16<RQ_BF16>(x, (int64_t)m * K + run * 32, xd);
+                    else if (x_dt == RQ_F32) load_x_run_bf16<RQ_F32>(x, (int64_t)m * K + run * 32, xd);
+                    else load_x_run_bf16<RQ_F16>(x, (int64_t)m * K + run * 32, xd);
+                }
             } else {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) xd[i] = 0u;
@@ -208,17 +351,35 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(const QmvArgs args) {
             for (int j = 0; j < 4; ++j)
                 o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c][j], ones, o[c], 0, 0, 0);
         }
-
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             bf16x8_t bop[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 uint32_t pr[4];
-                codes_to_bf16_pairs<BITS>(cw[rb], j, pr);
+                codes_to_bf16_pairs<BITS>(st.cw[rb], j, pr);
                 bop[j] = as_bf16x8(pr[0], pr[1], pr[2], pr[3]);
             }
-            const float cb = (BITS == 8) ? bi[rb] : (bi[rb] * 0.0078125f - sc[rb]);
+            const int64_t row = row0 + rb * 16 + lr;
+            const bool ok = run_ok && row < R;
+            float sc, bi;
+            if constexpr (SLDS) {
+                const int64_t runc = run_ok ? run : runs_per_row - 1;
+                const sbp_t v = sbs[(row - blk_row0) * G + (runc >> slot_shift)];
+                if constexpr (SDT == RQ_F32) {
+                    sc = __uint_as_float(v.x);
+                    bi = __uint_as_float(v.y);
+                } else {
+                    sc = raw_to_f32<SDT>(v & 0xffffu);
+                    bi = raw_to_f32<SDT>(v >> 16);
+                }
+                sc = ok ? sc : 0.f;
+                bi = ok ? bi : 0.f;
+            } else {
+                sc = ok ? raw_to_f32<SDT>(st.sc[rb]) : 0.f;
+                bi = ok ? raw_to_f32<SDT>(st.bi[rb]) : 0.f;
+            }
+            const float cb = (BITS == 8) ? bi : (bi * 0.0078125f - sc);
 #pragma unroll
             for (int c = 0; c < NMC; ++c) {
                 f32x4_t d = {0.f, 0.f, 0.f, 0.f};
@@ -227,60 +388,107 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(const QmvArgs args) {
                     d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c][j], bop[j], d, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    acc[rb][c][i] = fmaf(sc[rb], d[i], fmaf(cb, o[c][i], acc[rb][c][i]));
+                    acc[rb][c][i] = fmaf(sc, d[i], fmaf(cb, o[c][i], acc[rb][c][i]));
+            }
+        }
+    };
+
+    const int s0 = (KS == 1) ? 0 : wave;
+    if constexpr (SLDS) {
+        // Rolling pipeline: span s+(NS-1)*KS is loaded while span s is computed.
+        Stage<BITS, RB> st[NS];
+#pragma unroll
+        for (int i = 0; i < NS - 1; ++i) {
+            load(s0 + i * KS, st[i]);
+            __builtin_amdgcn_sched_barrier(0);  // stage 0 must be the oldest load
+        }
+        for (int s = s0; s < nspans; s += NS * KS) {
+#pragma unroll
+            for (int i = 0; i < NS; ++i) {
+                load(s + (i + NS - 1) * KS, st[(i + NS - 1) % NS]);
+                compute(s + i * KS, st[i]);
+                // keep the loads in issue order: the memory counter retires in
+                // order, so a stage loaded late would make its compute drain
+                // every younger load
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    } else {
+        // Batches of NS spans: all loads first, then consume in order.
+        for (int s = s0; s < nspans; s += NS * KS) {
+            Stage<BITS, RB> st[NS];
+#pragma unroll
+            for (int i = 0; i < NS; ++i) load(s + i * KS, st[i]);
+#pragma unroll
+            for (int i = 0; i < NS; ++i) compute(s + i * KS, st[i]);
+        }
+    }
+
+    if constexpr (KS > 1) {
+        __shared__ float red[KS][RB][NMC][4][64];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int c = 0; c < NMC; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[wave][rb][c][i][lane] = acc[rb][c][i];
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int c = 0; c < NMC; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float v = red[0][rb][c][i][lane];
+#pragma unroll
+                    for (int w = 1; w < KS; ++w) v += red[w][rb][c][i][lane];
+                    acc[rb][c][i] = v;
+                }
+    }
+
+    // Slot combine: D row m' = slot*MC + mm lives in lane group (m'/4), so the
+    // slots of one output meet with xor-shuffles across lane groups.
+    const int slots = 16 / MC;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int64_t row = row0 + rb * 16 + lr;
+#pragma unroll
+        for (int c = 0; c < NMC; ++c) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float v = acc[rb][c][i];
+                if (slots == 4) v += __shfl_xor(v, 16, 64);
+                if (slots >= 2) v += __shfl_xor(v, 32, 64);
+                const int m = c * MC + 4 * lg + i;
+                if (lg < MC / 4 && m < M && row < R)
+                    store_dt(args.p[p].y, args.y_dt, (int64_t)m * R + row, v);
             }
         }
     }
-
-    // Cross-wave sum and slot combine through LDS.
-    __shared__ float red[kWaves][RB][NMC][4][64];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int c = 0; c < NMC; ++c)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) red[wave][rb][c][i][lane] = acc[rb][c][i];
-    __syncthreads();
-
-    const int slots = 1 << (7 - gsh);
-    const int total = RB * 16 * M;
-    for (int idx = threadIdx.x; idx < total; idx += kBlock) {
-        const int rb = idx / (16 * M);
-        const int rem = idx - rb * 16 * M;
-        const int m = rem >> 4;
-        const int n = rem & 15;
-        const int c = m / MC;
-        const int mm = m - c * MC;
-        float sum = 0.f;
-        for (int sl = 0; sl < slots; ++sl) {
-            const int mp = sl * MC + mm;  // D row
-            const int L = n + 16 * (mp >> 2);
-            const int i = mp & 3;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) sum += red[w][rb][c][i][L];
-        }
-        const int64_t row = row0 + rb * 16 + n;
-        if (row < R) store_dt(args.p[p].y, args.y_dt, (int64_t)m * R + row, sum);
-    }
 }
 
-template <int XDT, int NMC, int RB>
-hipError_t launch_one(const QmvArgs& a, int blocks, hipStream_t stream) {
-    hipLaunchKernelGGL((qmv_kernel<RQ_BITS, XDT, NMC, RB>), dim3(blocks), dim3(kBlock), 0, stream,
-                       a);
+template <int SDT, int NMC, int RB, int KS, bool XLDS>
+hipError_t launch_one(const QmvArgs& a, int blocks, size_t lds, hipStream_t stream) {
+    constexpr int NS = XLDS ? RQ_QMV_NS : RQ_QMV_BATCH;
+    hipLaunchKernelGGL((qmv_kernel<RQ_BITS, SDT, NMC, RB, KS, NS, XLDS>), dim3(blocks),
+                       dim3(kBlock), lds, stream, a);
     return hipGetLastError();
 }
 
-template <int RB>
-hipError_t launch_rb(const QmvArgs& a, int x_dt, int nmc, int blocks, hipStream_t stream) {
+template <int RB, int KS>
+hipError_t launch_cfg(const QmvArgs& a, int sb_dt, int nmc, bool xlds, int blocks, size_t lds,
+                      hipStream_t stream) {
     hipError_t e = hipErrorInvalidValue;
-    RQ_DISPATCH_DT(x_dt, XD,
-        switch (nmc) {
-            case 1: e = launch_one<XD, 1, RB>(a, blocks, stream); break;
-            case 2: e = launch_one<XD, 2, RB>(a, blocks, stream); break;
-            case 4: e = launch_one<XD, 4, RB>(a, blocks, stream); break;
-            default: break;
-        });
+#define RQ_QMV_NMC(SD, XL)                                                         \
+    switch (nmc) {                                                                 \
+        case 1: e = launch_one<SD, 1, RB, KS, XL>(a, blocks, lds, stream); break;   \
+        case 2: e = launch_one<SD, 2, RB, KS, XL>(a, blocks, lds, stream); break;   \
+        case 4: e = launch_one<SD, 4, RB, KS, XL>(a, blocks, lds, stream); break;   \
+        default: break;                                                            \
+    }
+    RQ_DISPATCH_DT(sb_dt, SD, if (xlds) { RQ_QMV_NMC(SD, true) } else { RQ_QMV_NMC(SD, false) });
+#undef RQ_QMV_NMC
     return e;
 }
 
@@ -291,19 +499,32 @@ namespace rq {
 #define RQ_CAT2(a, b) a##b
 #define RQ_CAT(a, b) RQ_CAT2(a, b)
 
-hipError_t RQ_CAT(launch_qmv_b, RQ_BITS)(const rq_problem* problems, int n, int x_dt, int sb_dt,
-                                         int y_dt, int64_t m, int gs, hipStream_t stream) {
+// One launch over problems[0..n) that all share cols (so LDS staging is sized
+// exactly for them).
+static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt, int sb_dt,
+                                int y_dt, int64_t m, int gs, hipStream_t stream) {
     const int gs_shift = __builtin_ctz(gs);
     const int MC = 16 >> (7 - gs_shift);
     int nmc = (int)((m + MC - 1) / MC);
     nmc = nmc <= 1 ? 1 : (nmc <= 2 ? 2 : 4);
+    const int64_t K = probs[0]->cols;
 
-    // Total 16-row blocks decide the rows per block: a launch that can keep
-    // every CU busy with 64-row blocks uses them (fewer partial-sum meets),
-    // smaller launches use 16-row blocks for parallelism.
+    // The total number of 16-row blocks picks the organisation: big launches
+    // give every wave RQ_QMV_BIG_RB row blocks of its own, medium ones one,
+    // and small ones let the four waves of a block split K so that more waves
+    // stream at once.
     int64_t rowblocks = 0;
-    for (int i = 0; i < n; ++i) rowblocks += (problems[i].rows + 15) / 16;
-    const int RB = rowblocks >= 4096 ? 4 : 1;
+    for (int i = 0; i < n; ++i) rowblocks += (probs[i]->rows + 15) / 16;
+    const int cfg = rowblocks >= 16384 ? 2 : (rowblocks >= 2048 ? 1 : 0);
+    const int RB = cfg == 2 ? RQ_QMV_BIG_RB : 1;
+    const int rows_per_block = cfg == 0 ? 16 * RB : 16 * RB * kWaves;
+    // LDS staging: a zero line, activations [m][K] as bf16, then the block's
+    // (scale, bias) pairs.
+    const size_t sbsz = sb_dt == RQ_F32 ? 8 : 4;
+    const size_t lds = 64 + (((size_t)m * K * 2 + 15) & ~(size_t)15) +
+                       (size_t)rows_per_block * (K / gs) * sbsz;
+    const bool xlds = lds <= (size_t)kLdsBudget;
+    const size_t dyn = xlds ? lds : 0;
 
     for (int base = 0; base < n; base += RQ_MAX_GROUPED) {
         const int cnt = (n - base) < RQ_MAX_GROUPED ? (n - base) : RQ_MAX_GROUPED;
@@ -311,20 +532,47 @@ hipError_t RQ_CAT(launch_qmv_b, RQ_BITS)(const rq_problem* problems, int n, int 
         std::memset(&a, 0, sizeof(a));
         int64_t blocks = 0;
         for (int i = 0; i < cnt; ++i) {
-            a.p[i] = problems[base + i];
+            a.p[i] = *probs[base + i];
             a.block_start[i] = (int)blocks;
-            blocks += (problems[base + i].rows + 16 * RB - 1) / (16 * RB);
+            blocks += (probs[base + i]->rows + rows_per_block - 1) / rows_per_block;
         }
         a.block_start[cnt] = (int)blocks;
         a.n = cnt;
         a.m = (int)m;
         a.gs_shift = gs_shift;
-        a.sb_dt = sb_dt;
+        a.x_dt = x_dt;
         a.y_dt = y_dt;
         if (blocks == 0) continue;
-        hipError_t e = RB == 4 ? launch_rb<4>(a, x_dt, nmc, (int)blocks, stream)
-                               : launch_rb<1>(a, x_dt, nmc, (int)blocks, stream);
+        hipError_t e;
+        if (cfg == 2) e = launch_cfg<RQ_QMV_BIG_RB, 1>(a, sb_dt, nmc, xlds, (int)blocks, dyn, stream);
+        else if (cfg == 1) e = launch_cfg<1, 1>(a, sb_dt, nmc, xlds, (int)blocks, dyn, stream);
+        else e = launch_cfg<1, kWaves>(a, sb_dt, nmc, xlds, (int)blocks, dyn, stream);
         if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t RQ_CAT(launch_qmv_b, RQ_BITS)(const rq_problem* problems, int n, int x_dt, int sb_dt,
+                                         int y_dt, int64_t m, int gs, hipStream_t stream) {
+    // Problems are bucketed by cols (in order of first appearance): each
+    // bucket is launched with LDS staging sized for its own K.
+    std::vector<const rq_problem*> order;
+    std::vector<int64_t> seen;
+    order.reserve(n);
+    for (int i = 0; i < n; ++i) {
+        bool dup = false;
+        for (int64_t c : seen) dup |= (c == problems[i].cols);
+        if (dup) continue;
+        seen.push_back(problems[i].cols);
+        const size_t start = order.size();
+        for (int k = i; k < n; ++k)
+            if (problems[k].cols == problems[i].cols && problems[k].rows > 0)
+                order.push_back(&problems[k]);
+        if (order.size() > start) {
+            hipError_t e = launch_bucket(order.data() + start, (int)(order.size() - start), x_dt,
+                                         sb_dt, y_dt, m, gs, stream);
+            if (e != hipSuccess) return e;
+        }
     }
     return hipSuccess;
 }

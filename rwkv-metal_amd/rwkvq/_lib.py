@@ -13,7 +13,9 @@ import os
 
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "librwkvq_hip.so")
+# RWKVQ_LIB selects another build of the same ABI (e.g. a tuning variant).
+LIB_PATH = os.environ.get("RWKVQ_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "librwkvq_hip.so")
 
 RQ_BF16, RQ_F16, RQ_F32 = 0, 1, 2
 DTYPE_CODE = {torch.bfloat16: RQ_BF16, torch.float16: RQ_F16, torch.float32: RQ_F32}
