@@ -39,7 +39,10 @@ FLAGS = [
 def _units():
     units = [("rq_quant.hip", [], "rq_quant.o"), ("rq_abi.cpp", ["-x", "hip"], "rq_abi.o")]
     for b in BITS:
-        units.append(("rq_qmv.hip", [f"-DRQ_BITS={b}"], f"rq_qmv_b{b}.o"))
+        # MFMA results straight into VGPRs: the GEMV consumes every MFMA
+        # result with VALU fmas, so accumulator registers only add copies
+        units.append(("rq_qmv.hip", [f"-DRQ_BITS={b}", "-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+                      f"rq_qmv_b{b}.o"))
         units.append(("rq_qmm.hip", [f"-DRQ_BITS={b}"], f"rq_qmm_b{b}.o"))
     return units
 

@@ -93,6 +93,7 @@ struct QmvArgs {
     int gs_shift;
     int x_dt;
     int y_dt;
+    int sb_vec;  // scales and biases are 16-byte aligned (vector staging allowed)
 };
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -103,12 +104,25 @@ RQ_DEV bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
 }
 
 // Eight codes 8j..8j+7 of a run as bf16 pairs (c_i, c_{i+4}), i = 0..3.
+// The mask and the bf16 exponent bits are passed in registers (opaque to the
+// optimiser) so that each pair is one v_and_or_b32 instead of an and plus an
+// or with literal operands.
+struct PairConsts {
+    uint32_t mask, magic;
+};
+RQ_DEV PairConsts pair_consts() {
+    PairConsts c{0x000F000Fu, 0x43004300u};
+    asm volatile("" : "+v"(c.mask), "+v"(c.magic));
+    return c;
+}
+
 template <int BITS>
-RQ_DEV void codes_to_bf16_pairs(const uint32_t* words, int j, uint32_t* out) {
+RQ_DEV void codes_to_bf16_pairs(const uint32_t* words, int j, uint32_t* out,
+                                PairConsts k = PairConsts{0x000F000Fu, 0x43004300u}) {
     if constexpr (BITS == 4) {
         const uint32_t w = words[j];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) out[i] = ((w >> (4 * i)) & 0x000F000Fu) | 0x43004300u;
+        for (int i = 0; i < 4; ++i) out[i] = ((w >> (4 * i)) & k.mask) | k.magic;
     } else if constexpr (BITS == 8) {
         const uint32_t lo = words[2 * j], hi = words[2 * j + 1];
 #pragma unroll
@@ -233,48 +247,6 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
     const int64_t blk_row0 = lblock * kRowsPerBlock;
     const int64_t row0 = blk_row0 + (KS == 1 ? wave * 16 * RB : 0);
 
-    // LDS: 64 zero bytes (the A operand of inactive lanes), x [M][K] bf16,
-    // then the block's (scale, bias) pairs [kRowsPerBlock][G].
-    uint16_t* xzero = lds;
-    uint16_t* xs = lds + 32;
-    sbp_t* sbs = (sbp_t*)(xs + (((int64_t)M * K + 7) & ~7ll));
-    if constexpr (SLDS) {
-        if (threadIdx.x < 4) *(u32x4_t*)&xzero[threadIdx.x * 8] = u32x4_t{0u, 0u, 0u, 0u};
-        // Stage x[0..M) as bf16: 8 elements per thread per step.
-        const int64_t n8 = (int64_t)M * K / 8;
-        for (int64_t e = threadIdx.x; e < n8; e += kBlock) {
-            uint32_t d[4];
-            if (x_dt == RQ_BF16) {
-                const uint4 v = ((const uint4*)x)[e];
-                d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-            } else {
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    d[q] = pack_bf16x2(load_dt(x, x_dt, e * 8 + 2 * q),
-                                       load_dt(x, x_dt, e * 8 + 2 * q + 1));
-            }
-            *(u32x4_t*)&xs[e * 8] = u32x4_t{d[0], d[1], d[2], d[3]};
-        }
-        // Stage the block's (scale, bias) pairs; rows past R are zero pairs.
-        const int64_t nsb = (int64_t)kRowsPerBlock * G;
-        for (int64_t e = threadIdx.x; e < nsb; e += kBlock) {
-            const int64_t rl = e / G, g = e - rl * G;
-            const int64_t row = blk_row0 + rl;
-            sbp_t v;
-            if constexpr (SDT == RQ_F32) {
-                v = row < R ? make_uint2(((const uint32_t*)scales)[row * G + g],
-                                         ((const uint32_t*)biases)[row * G + g])
-                            : make_uint2(0u, 0u);
-            } else {
-                v = row < R ? (uint32_t)((const uint16_t*)scales)[row * G + g] |
-                                  ((uint32_t)((const uint16_t*)biases)[row * G + g] << 16)
-                            : 0u;
-            }
-            sbs[e] = v;
-        }
-        __syncthreads();
-    }
-    if (row0 >= R) return;  // a wave past the end of its problem (after the barrier)
 
     const int lg = lane >> 4;  // lane group: run inside the span / k-slice
     const int lr = lane & 15;  // A row m' / weight row inside a 16-row block
@@ -295,56 +267,172 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
 #pragma unroll
         for (int c = 0; c < NMC; ++c) acc[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+    // Word offsets of this lane's rows (clamped in range); packed weights are
+    // limited to 2^32 words per matrix by the host, so offsets are 32-bit.
+    uint32_t row_off[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int64_t row = row0 + rb * 16 + lr;
+        row_off[rb] = (uint32_t)((row < R ? row : R - 1) * wpr);
+    }
+    const uint32_t last_run = (uint32_t)runs_per_row - 1;
+
     auto load = [&](int s, Stage<BITS, RB>& st) {
-        const int64_t run = (int64_t)s * 4 + lg;
-        const int64_t runc = run < runs_per_row ? run : runs_per_row - 1;
+        const uint32_t run = (uint32_t)s * 4u + (uint32_t)lg;
+        const uint32_t runc = run < last_run ? run : last_run;
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
-            const int64_t row = row0 + rb * 16 + lr;
-            const int64_t rowc = row < R ? row : R - 1;
-            load_run_stream<BITS>(wq + rowc * wpr + runc * BITS, st.cw[rb]);
+            load_run_stream<BITS>(wq + (row_off[rb] + runc * BITS), st.cw[rb]);
             if constexpr (!SLDS) {
-                const int64_t gi = rowc * G + (runc >> slot_shift);
+                const int64_t row = row0 + rb * 16 + lr;
+                const int64_t gi = (row < R ? row : R - 1) * G + (runc >> slot_shift);
                 st.sc[rb] = load_raw<SDT>(scales, gi);
                 st.bi[rb] = load_raw<SDT>(biases, gi);
             }
         }
     };
 
+    // The first NS-1 stages of packed codes are requested before the LDS
+    // staging below, so their latency overlaps it.  (A wave past the end of
+    // its problem loads clamped rows and leaves after the barrier.)
+    const int s0 = (KS == 1) ? 0 : wave;
+    Stage<BITS, RB> st[NS];
+    if constexpr (SLDS) {
+#pragma unroll
+        for (int i = 0; i < NS - 1; ++i) {
+            load(s0 + i * KS, st[i]);
+            __builtin_amdgcn_sched_barrier(0);  // stage 0 must be the oldest load
+        }
+    }
+
+    // LDS: 64 zero bytes (the A operand of inactive lanes), x [M][K] bf16,
+    // then the block's (scale, bias) pairs [kRowsPerBlock][G].
+    uint16_t* xzero = lds;
+    uint16_t* xs = lds + 32;
+    sbp_t* sbs = (sbp_t*)(xs + (((int64_t)M * K + 7) & ~7ll));
+    if constexpr (SLDS) {
+        if (threadIdx.x < 4) *(u32x4_t*)&xzero[threadIdx.x * 8] = u32x4_t{0u, 0u, 0u, 0u};
+        // Stage x[0..M) as bf16: 8 elements per thread per step.
+        const int64_t n8 = (int64_t)M * K / 8;
+        for (int64_t e = threadIdx.x; e < n8; e += kBlock) {
+            uint32_t d[4];
+            if (x_dt == RQ_BF16) {
+                const uint4 v = ((const uint4*)x)[e];
+                d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    d[q] = pack_bf16x2(load_dt(x, x_dt, e * 8 + 2 * q),
+                                       load_dt(x, x_dt, e * 8 + 2 * q + 1));
+            }
+            uint32_t pr[4];  // stored as pairs (x_i, x_{i+4}): the order of the code pairs
+            reorder_pairs(d, pr);
+            *(u32x4_t*)&xs[e * 8] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
+        }
+        // Stage the block's (scale, bias) pairs; rows past R are zero pairs.
+        // With 16-bit scales, 16-byte aligned arrays and G % 8 == 0, eight
+        // pairs per thread per step (two 128-bit loads, two 128-bit LDS
+        // stores); otherwise one pair per step.
+        const int64_t nsb = (int64_t)kRowsPerBlock * G;
+        if (SDT != RQ_F32 && args.sb_vec && (G & 7) == 0) {
+            for (int64_t e8 = threadIdx.x; e8 < nsb / 8; e8 += kBlock) {
+                const int64_t e = e8 * 8;
+                const int64_t rl = e / G, g = e - rl * G;
+                const int64_t row = blk_row0 + rl;
+                u32x4_t sv = {0u, 0u, 0u, 0u}, bv = {0u, 0u, 0u, 0u};
+                if (row < R) {
+                    sv = *(const u32x4_t*)((const uint16_t*)scales + row * G + g);
+                    bv = *(const u32x4_t*)((const uint16_t*)biases + row * G + g);
+                }
+                uint32_t o[8];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    o[2 * q] = (sv[q] & 0xffffu) | (bv[q] << 16);
+                    o[2 * q + 1] = (sv[q] >> 16) | (bv[q] & 0xffff0000u);
+                }
+                u32x4_t* dst = (u32x4_t*)&sbs[e];
+                dst[0] = u32x4_t{o[0], o[1], o[2], o[3]};
+                dst[1] = u32x4_t{o[4], o[5], o[6], o[7]};
+            }
+        } else
+        for (int64_t e = threadIdx.x; e < nsb; e += kBlock) {
+            const int64_t rl = e / G, g = e - rl * G;
+            const int64_t row = blk_row0 + rl;
+            sbp_t v;
+            if constexpr (SDT == RQ_F32) {
+                v = row < R ? make_uint2(((const uint32_t*)scales)[row * G + g],
+                                         ((const uint32_t*)biases)[row * G + g])
+                            : make_uint2(0u, 0u);
+            } else {
+                v = row < R ? (uint32_t)((const uint16_t*)scales)[row * G + g] |
+                                  ((uint32_t)((const uint16_t*)biases)[row * G + g] << 16)
+                            : 0u;
+            }
+            sbs[e] = v;
+        }
+        __syncthreads();
+    }
+    if (row0 >= R) return;  // a wave past the end of its problem (after the barrier)
+
+    const PairConsts kc = pair_consts();
+    // Per-lane constants of the staged path: LDS byte address of this lane's
+    // activation row for each pass (or of the zero line when the lane's A row
+    // is inactive), its row's (scale, bias) base and whether its rows exist.
+    // (Indices are in 16-bit units of the dynamic LDS array: the zero line
+    // is lds[0..32), x row m starts at lds[32 + m*K].)
+    uint32_t a_idx[NMC], a_step[NMC];
+#pragma unroll
+    for (int c = 0; c < NMC; ++c) {
+        const int m = c * MC + (lr % MC);
+        const bool act = a_slot_ok && m < M;
+        a_idx[c] = act ? (uint32_t)(32 + (int64_t)m * K + lg * 32) : 0u;
+        a_step[c] = act ? 4u * 32u : 0u;  // elements per span (4 runs)
+    }
+    uint32_t sb_base[RB];
+    bool row_ok[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int64_t row = row0 + rb * 16 + lr;
+        row_ok[rb] = row < R;
+        sb_base[rb] = (uint32_t)((row < R ? row - blk_row0 : 0) * G);
+    }
+
     auto compute = [&](int s, const Stage<BITS, RB>& st) {
-        const int64_t run = (int64_t)s * 4 + lg;
-        const bool run_ok = run < runs_per_row;
+        const uint32_t run = (uint32_t)s * 4u + (uint32_t)lg;
+        const bool run_ok = run <= last_run;
         bf16x8_t a[NMC][4];
         f32x4_t o[NMC];
 #pragma unroll
         for (int c = 0; c < NMC; ++c) {
             const int m = c * MC + (lr % MC);
             uint32_t xd[16];
-            const bool active = a_slot_ok && run_ok && m < M;
             if constexpr (SLDS) {
-                // branch-free: inactive lanes read the zero line
-                const u32x4_t* src =
-                    (const u32x4_t*)(active ? &xs[(int64_t)m * K + run * 32] : xzero);
+                // Branch-free: inactive lanes and runs past K read the zero
+                // line (a zero scale alone would not cancel Inf/NaN garbage).
+                const uint32_t ai = run_ok ? a_idx[c] + (uint32_t)s * a_step[c] : 0u;
+                const u32x4_t* src = (const u32x4_t*)&lds[ai];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const u32x4_t v = src[q];
                     xd[4 * q] = v[0]; xd[4 * q + 1] = v[1]; xd[4 * q + 2] = v[2]; xd[4 * q + 3] = v[3];
                 }
-            } else if (active) {
-                {
-                    if (x_dt == RQ_BF16) load_x_run_bf16<RQ_BF16>(x, (int64_t)m * K + run * 32, xd);
-                    else if (x_dt == RQ_F32) load_x_run_bf16<RQ_F32>(x, (int64_t)m * K + run * 32, xd);
-                    else load_x_run_bf16<RQ_F16>(x, (int64_t)m * K + run * 32, xd);
-                }
+            } else if (a_slot_ok && run_ok && m < M) {
+                if (x_dt == RQ_BF16) load_x_run_bf16<RQ_BF16>(x, (int64_t)m * K + run * 32, xd);
+                else if (x_dt == RQ_F32) load_x_run_bf16<RQ_F32>(x, (int64_t)m * K + run * 32, xd);
+                else load_x_run_bf16<RQ_F16>(x, (int64_t)m * K + run * 32, xd);
             } else {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) xd[i] = 0u;
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                uint32_t pr[4];
-                reorder_pairs(&xd[4 * j], pr);
-                a[c][j] = as_bf16x8(pr[0], pr[1], pr[2], pr[3]);
+                if constexpr (SLDS) {  // staged already in pair order
+                    a[c][j] = as_bf16x8(xd[4 * j], xd[4 * j + 1], xd[4 * j + 2], xd[4 * j + 3]);
+                } else {
+                    uint32_t pr[4];
+                    reorder_pairs(&xd[4 * j], pr);
+                    a[c][j] = as_bf16x8(pr[0], pr[1], pr[2], pr[3]);
+                }
             }
             o[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -357,15 +445,14 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 uint32_t pr[4];
-                codes_to_bf16_pairs<BITS>(st.cw[rb], j, pr);
+                codes_to_bf16_pairs<BITS>(st.cw[rb], j, pr, kc);
                 bop[j] = as_bf16x8(pr[0], pr[1], pr[2], pr[3]);
             }
-            const int64_t row = row0 + rb * 16 + lr;
-            const bool ok = run_ok && row < R;
+            const bool ok = run_ok && row_ok[rb];
             float sc, bi;
             if constexpr (SLDS) {
-                const int64_t runc = run_ok ? run : runs_per_row - 1;
-                const sbp_t v = sbs[(row - blk_row0) * G + (runc >> slot_shift)];
+                const uint32_t runc = run_ok ? run : last_run;
+                const sbp_t v = sbs[sb_base[rb] + (runc >> slot_shift)];
                 if constexpr (SDT == RQ_F32) {
                     sc = __uint_as_float(v.x);
                     bi = __uint_as_float(v.y);
@@ -393,15 +480,8 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
         }
     };
 
-    const int s0 = (KS == 1) ? 0 : wave;
     if constexpr (SLDS) {
         // Rolling pipeline: span s+(NS-1)*KS is loaded while span s is computed.
-        Stage<BITS, RB> st[NS];
-#pragma unroll
-        for (int i = 0; i < NS - 1; ++i) {
-            load(s0 + i * KS, st[i]);
-            __builtin_amdgcn_sched_barrier(0);  // stage 0 must be the oldest load
-        }
         for (int s = s0; s < nspans; s += NS * KS) {
 #pragma unroll
             for (int i = 0; i < NS; ++i) {
@@ -416,7 +496,6 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
     } else {
         // Batches of NS spans: all loads first, then consume in order.
         for (int s = s0; s < nspans; s += NS * KS) {
-            Stage<BITS, RB> st[NS];
 #pragma unroll
             for (int i = 0; i < NS; ++i) load(s + i * KS, st[i]);
 #pragma unroll
@@ -542,6 +621,9 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
         a.gs_shift = gs_shift;
         a.x_dt = x_dt;
         a.y_dt = y_dt;
+        a.sb_vec = 1;
+        for (int i = 0; i < cnt; ++i)
+            a.sb_vec &= (((uintptr_t)a.p[i].scales | (uintptr_t)a.p[i].biases) & 15) == 0;
         if (blocks == 0) continue;
         hipError_t e;
         if (cfg == 2) e = launch_cfg<RQ_QMV_BIG_RB, 1>(a, sb_dt, nmc, xlds, (int)blocks, dyn, stream);
