@@ -323,6 +323,414 @@ __global__ __launch_bounds__(kBlock) void qmm_n_kernel(
         }
 }
 
+
+// ------------------------------------------------------------- qmm_t_big
+//
+// Large-M forward GEMM.  Block tile 256 (activation rows) x BN (weight rows),
+// 64 contraction elements per stage, four waves in a 2x2 arrangement with a
+// 128 x BN/2 wave tile of 16x16x32 bf16 MFMAs (fp32 accumulators).  BN is
+// chosen per shape so that an M=4096 problem fills the 256 CUs in whole
+// rounds (BN=160 for N in {2560, 10240}, BN=128 otherwise).  Each stage: the block's packed weight tile is dequantized once
+// (fp32 fma of scale, code and bias, rounded to bf16) and written to LDS
+// next to the bf16 activation tile; LDS is double buffered and the next
+// stage's global loads are issued before the current stage's MFMAs.
+// Blocks are assigned to tiles so that each XCD works on a contiguous run of
+// tiles (shared activation rows and weight rows stay in that XCD's L2).
+
+// One run of 32 codes -> 16 dwords of bf16 pairs, ŵ = bf16(scale*code + bias),
+// using byte converts (v_cvt_f32_ubyte*) for 4- and 8-bit codes.
+template <int BITS>
+RQ_DEV void dequant_run_fast(const uint32_t* words, float s, float b, uint32_t* out) {
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t lo = words[w] & 0x0F0F0F0Fu;         // codes 0,2,4,6 of the word
+            const uint32_t hi = (words[w] >> 4) & 0x0F0F0F0Fu;  // codes 1,3,5,7
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float c0 = (float)((lo >> (8 * i)) & 0xffu);
+                const float c1 = (float)((hi >> (8 * i)) & 0xffu);
+                out[4 * w + i] = pack_bf16x2(fmaf(s, c0, b), fmaf(s, c1, b));
+            }
+        }
+    } else if constexpr (BITS == 8) {
+#pragma unroll
+        for (int w = 0; w < 8; ++w)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float c0 = (float)((words[w] >> (16 * i)) & 0xffu);
+                const float c1 = (float)((words[w] >> (16 * i + 8)) & 0xffu);
+                out[2 * w + i] = pack_bf16x2(fmaf(s, c0, b), fmaf(s, c1, b));
+            }
+    } else {
+        dequant_run_bf16<BITS>(words, s, b, out);
+    }
+}
+
+template <int BITS, int XDT, int BN>
+__global__ __launch_bounds__(kBlock, 1) void qmm_t_big(
+    const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
+    const void* __restrict__ biases, int sb_dt, int64_t M, int64_t R, int64_t K, int gs_shift,
+    void* __restrict__ y, int y_dt, int tiles_m, int tiles_n) {
+    constexpr int BM = 256;
+    constexpr int WN = BN / 2;           // wave tile: 128 x WN
+    constexpr int TM = 8, TN = WN / 16;  // 16x16 MFMA tiles per wave
+    constexpr int NRUN = (2 * BN + kBlock - 1) / kBlock;  // weight runs per thread per stage
+    constexpr int TILE_ELEMS = (BM + BN) * LDS_LD;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * TILE_ELEMS];
+
+    // XCD-aware tile order: consecutive block ids go to different XCDs, so
+    // block b works on tile (b % 8) * per_xcd + b / 8.
+    const int ntiles = tiles_m * tiles_n;
+    const int per_xcd = (ntiles + 7) / 8;
+    const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+    if (t >= ntiles) return;
+    const int64_t m0 = (int64_t)(t / tiles_n) * BM, n0 = (int64_t)(t % tiles_n) * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lg = lane >> 4, lr = lane & 15;
+    const int64_t runs_per_row = K >> 5, wpr = runs_per_row * BITS, G = K >> gs_shift;
+    const int nst = (int)((runs_per_row + 1) >> 1);
+
+    // activation tile: 256 rows x 64 k = 2048 16-byte chunks of bf16, 8 per thread
+    uint32_t xa[8][4];
+    uint32_t cw[NRUN][BITS];
+    float sc[NRUN], bi[NRUN];
+
+    auto gload = [&](int st) {
+        const int64_t k0 = (int64_t)st * BK;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = tid + kBlock * i;
+            const int64_t row = m0 + (c >> 3);
+            const int64_t col = k0 + (c & 7) * 8;
+            if (row < M && col < K) {
+                if constexpr (XDT == RQ_BF16) {
+                    const uint4 v = *(const uint4*)((const uint16_t*)x + row * K + col);
+                    xa[i][0] = v.x; xa[i][1] = v.y; xa[i][2] = v.z; xa[i][3] = v.w;
+                } else {
+                    typedef typename dt_traits<XDT>::storage S;
+                    const S* px = (const S*)x + row * K + col;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        xa[i][q] = pack_bf16x2(dt_traits<XDT>::to_f32(px[2 * q]),
+                                               dt_traits<XDT>::to_f32(px[2 * q + 1]));
+                }
+            } else {
+                xa[i][0] = xa[i][1] = xa[i][2] = xa[i][3] = 0u;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NRUN; ++i) {
+            const int r = tid + kBlock * i;
+            const int64_t row = n0 + (r >> 1);
+            const int64_t run = 2 * (int64_t)st + (r & 1);
+            if (r < 2 * BN && row < R && run < runs_per_row) {
+                load_run<BITS>(wq + row * wpr + run * BITS, cw[i]);
+                const int64_t gi = row * G + (run >> (gs_shift - 5));
+                sc[i] = load_dt(scales, sb_dt, gi);
+                bi[i] = load_dt(biases, sb_dt, gi);
+            } else {
+#pragma unroll
+                for (int w = 0; w < BITS; ++w) cw[i][w] = 0u;
+                sc[i] = 0.f;
+                bi[i] = 0.f;
+            }
+        }
+    };
+    auto swrite = [&](int buf) {
+        uint16_t* As = smem + buf * TILE_ELEMS;
+        uint16_t* Bs = As + BM * LDS_LD;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = tid + kBlock * i;
+            *(u32x4_t*)&As[(c >> 3) * LDS_LD + (c & 7) * 8] =
+                u32x4_t{xa[i][0], xa[i][1], xa[i][2], xa[i][3]};
+        }
+#pragma unroll
+        for (int i = 0; i < NRUN; ++i) {
+            const int r = tid + kBlock * i;
+            if (r < 2 * BN) {
+                uint32_t d[16];
+                dequant_run_fast<BITS>(cw[i], sc[i], bi[i], d);
+                store_16dw(&Bs[(r >> 1) * LDS_LD + (r & 1) * 32], d);
+            }
+        }
+    };
+
+    f32x4_t acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    gload(0);
+    swrite(0);
+    __syncthreads();
+    for (int st = 0; st < nst; ++st) {
+        const int buf = st & 1;
+        const uint16_t* As = smem + buf * TILE_ELEMS;
+        const uint16_t* Bs = As + BM * LDS_LD;
+        if (st + 1 < nst) gload(st + 1);
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            bf16x8_t af[TM], bf[TN];
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+                af[a] = lds_frag(&As[(wm * 128 + a * 16 + lr) * LDS_LD + ks * 32 + lg * 8]);
+#pragma unroll
+            for (int b = 0; b < TN; ++b)
+                bf[b] = lds_frag(&Bs[(wn * WN + b * 16 + lr) * LDS_LD + ks * 32 + lg * 8]);
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int b = 0; b < TN; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bf[b], acc[a][b],
+                                                                        0, 0, 0);
+        }
+        if (st + 1 < nst) swrite(buf ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int64_t n = n0 + wn * WN + b * 16 + lr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t m = m0 + wm * 128 + a * 16 + 4 * lg + i;
+                if (m < M && n < R) store_dt(y, y_dt, m * R + n, acc[a][b][i]);
+            }
+        }
+}
+
+
+// ------------------------------------------------------------- qmm_t_dma
+//
+// Large-M forward GEMM for bf16 activations, fed entirely by direct-to-LDS
+// loads (global_load_lds): every stage of 32 contraction elements brings
+//   * the activation tile, 256 rows x 64 bytes, XOR-swizzled by 16-byte chunk
+//     so that MFMA fragment reads are bank-conflict free,
+//   * the packed codes of the BN weight rows (dword-dense [row][word]),
+//   * their scale and bias (one group per row per stage: 32 | group_size),
+// into a 4-slot LDS ring, three stages ahead of the MFMAs, without staging
+// registers.  One stage behind the DMA, threads [0, BN) dequantize the stage
+// (fp32 fma, bf16 round) into a 2-slot bf16 ring; the 4 waves (2x2, wave
+// tile 128 x BN/2, 16x16x32 bf16 MFMAs) consume it.  One workgroup barrier
+// per stage, preceded by an explicit wait for this wave's DMAs two stages
+// back, orders the ring.  Every wave issues the same number of DMAs per
+// stage (out-of-range rows and stages past K load clamped addresses into
+// spare slots), so a single wait count is valid for all waves.
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int BITS, int SDT, int BN>
+struct DmaCfg {
+    static constexpr int BM = 256;
+    static constexpr int NSLOT = 4;                                   // DMA ring depth
+    static constexpr int X_BYTES = BM * 64;                           // 16 KB
+    static constexpr int NX = X_BYTES / (kBlock * 16);                // 4 x-DMAs per thread
+    static constexpr int CODE_DW = BN * BITS;                         // dwords of codes
+    static constexpr int NC = (CODE_DW + kBlock - 1) / kBlock;        // code DMAs per thread
+    static constexpr int C_BYTES = NC * kBlock * 4;
+    static constexpr int SB = SDT == RQ_F32 ? 4 : 2;                  // scale bytes
+    // DMA loads of 4 bytes or fewer land at a 4-byte stride per lane
+    static constexpr int S_BYTES = kBlock * 4;
+    static constexpr int PER_STAGE = NX + NC + 2;                     // DMAs per thread per stage
+    static constexpr int BLD = 40;                                    // bf16 ring row stride (elements)
+    static constexpr int B_BYTES = BN * BLD * 2;
+};
+
+template <int N>
+RQ_DEV void s_wait_vmcnt_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] (7 = no wait) | lgkmcnt[11:8] | vmcnt[5:4] << 14
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+
+template <int BITS, int SDT, int BN>
+__global__ __launch_bounds__(kBlock, 1) void qmm_t_dma(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
+    const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
+    void* __restrict__ y, int y_dt, int tiles_m, int tiles_n) {
+    typedef DmaCfg<BITS, SDT, BN> C;
+    constexpr int BM = C::BM;
+    constexpr int WN = BN / 2;
+    constexpr int TM = 8, TN = WN / 16;
+    // One LDS object per ring slot: the compiler's wait insertion can then
+    // tell a read of one slot from a DMA in flight to another (distinct
+    // objects do not alias) instead of draining every DMA before each read.
+#define RQ_RING(name, bytes)                                                    \
+    __shared__ __attribute__((aligned(16))) uint8_t name##0[bytes];             \
+    __shared__ __attribute__((aligned(16))) uint8_t name##1[bytes];             \
+    __shared__ __attribute__((aligned(16))) uint8_t name##2[bytes];             \
+    __shared__ __attribute__((aligned(16))) uint8_t name##3[bytes];
+    RQ_RING(xr_, C::X_BYTES)
+    RQ_RING(cr_, C::C_BYTES)
+    RQ_RING(sr_, C::S_BYTES)
+    RQ_RING(br_, C::S_BYTES)
+#undef RQ_RING
+    __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * C::BLD];
+    __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * C::BLD];
+    auto xr = [&](int u) -> uint8_t* { return u == 0 ? xr_0 : u == 1 ? xr_1 : u == 2 ? xr_2 : xr_3; };
+    auto cr = [&](int u) -> uint8_t* { return u == 0 ? cr_0 : u == 1 ? cr_1 : u == 2 ? cr_2 : cr_3; };
+    auto sr = [&](int u) -> uint8_t* { return u == 0 ? sr_0 : u == 1 ? sr_1 : u == 2 ? sr_2 : sr_3; };
+    auto br = [&](int u) -> uint8_t* { return u == 0 ? br_0 : u == 1 ? br_1 : u == 2 ? br_2 : br_3; };
+    auto bq = [&](int u) -> uint16_t* { return u == 0 ? bq0 : bq1; };
+
+    const int ntiles = tiles_m * tiles_n;
+    const int per_xcd = (ntiles + 7) / 8;
+    const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+    if (t >= ntiles) return;
+    const int64_t m0 = (int64_t)(t / tiles_n) * BM, n0 = (int64_t)(t % tiles_n) * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lg = lane >> 4, lr = lane & 15;
+    const int64_t runs = K >> 5, wpr = runs * BITS, G = K >> gs_shift;
+    const int nst = (int)runs;
+
+    // Per-thread DMA sources that do not depend on the stage.
+    // x: instruction i of wave w covers tile rows (4w+i)*16 .. +15, 64 B each;
+    // lane l -> row (4w+i)*16 + l/4, stored chunk l%4 holds global chunk
+    // (l%4) ^ ((row/4)%4).
+    const uint16_t* xsrc[C::NX];
+#pragma unroll
+    for (int i = 0; i < C::NX; ++i) {
+        const int row = (wave * C::NX + i) * 16 + (lane >> 2);
+        const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+        int64_t grow = m0 + row;
+        grow = grow < M ? grow : M - 1;
+        xsrc[i] = x + grow * K + chunk * 8;
+    }
+    const uint32_t* csrc[C::NC];
+#pragma unroll
+    for (int i = 0; i < C::NC; ++i) {
+        const int d = tid + kBlock * i;
+        int row = d / BITS;
+        const int word = d - row * BITS;
+        int64_t grow = n0 + (row < BN ? row : BN - 1);
+        grow = grow < R ? grow : R - 1;
+        csrc[i] = wq + grow * wpr + word;
+    }
+    int64_t srow = n0 + (tid < BN ? tid : BN - 1);
+    srow = srow < R ? srow : R - 1;
+    const uint8_t* ssrc = (const uint8_t*)scales + srow * G * C::SB;
+    const uint8_t* bsrc = (const uint8_t*)biases + srow * G * C::SB;
+
+    auto dma = [&](int st, int slot) {
+        const int stc = st < nst ? st : nst - 1;  // past the end: reload the last stage
+#pragma unroll
+        for (int i = 0; i < C::NX; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + (int64_t)stc * 32),
+                                             (lds_void_t*)(xr(slot) + (wave * C::NX + i) * 1024),
+                                             16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < C::NC; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(csrc[i] + (int64_t)stc * BITS),
+                                             (lds_void_t*)(cr(slot) + (i * kBlock + wave * 64) * 4),
+                                             4, 0, 0);
+        const int64_t g = ((int64_t)stc * 32) >> gs_shift;
+        __builtin_amdgcn_global_load_lds((const void*)(ssrc + g * C::SB),
+                                         (lds_void_t*)(sr(slot) + wave * 64 * 4), C::SB, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(bsrc + g * C::SB),
+                                         (lds_void_t*)(br(slot) + wave * 64 * 4), C::SB, 0, 0);
+    };
+
+    // Threads [0, BN) dequantize row tid of a stage into the bf16 ring.
+    auto dequant = [&](int slot, int bslot) {
+        if (tid < BN) {
+            uint32_t words[BITS];
+#pragma unroll
+            for (int w = 0; w < BITS; ++w) words[w] = *(const uint32_t*)(cr(slot) + (tid * BITS + w) * 4);
+            float s, b;
+            if constexpr (SDT == RQ_F32) {
+                s = *(const float*)(sr(slot) + tid * 4);
+                b = *(const float*)(br(slot) + tid * 4);
+            } else {
+                s = dt_traits<SDT>::to_f32(*(const uint16_t*)(sr(slot) + tid * 4));
+                b = dt_traits<SDT>::to_f32(*(const uint16_t*)(br(slot) + tid * 4));
+            }
+            uint32_t d[16];
+            dequant_run_fast<BITS>(words, s, b, d);
+            u32x4_t* dst = (u32x4_t*)(bq(bslot) + tid * C::BLD);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) dst[q] = u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
+        }
+    };
+
+    f32x4_t acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto mfma = [&](int slot, int bslot) {
+        bf16x8_t af[TM], bf[TN];
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+            const int row = wm * 128 + a * 16 + lr;
+            const int pos = lg ^ ((row >> 2) & 3);
+            af[a] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xr(slot) + row * 64 + pos * 16));
+        }
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+            bf[b] = __builtin_bit_cast(bf16x8_t,
+                                       *(const u32x4_t*)(bq(bslot) + (wn * WN + b * 16 + lr) * C::BLD + lg * 8));
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < TN; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bf[b], acc[a][b], 0, 0, 0);
+    };
+
+    // Prologue: stages 0..2 in flight; stage 0 dequantized into bf16 slot 0.
+    dma(0, 0);
+    dma(1, 1);
+    dma(2, 2);
+    s_wait_vmcnt_lgkm0<2 * C::PER_STAGE>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    dequant(0, 0);
+
+    // Main loop, unrolled by the ring size so every slot index is static.
+    // Iteration st: wait for this wave's DMAs of stage st+1 (stage st+2 may
+    // still fly) and for its own LDS traffic; the barrier then makes stage
+    // st+1 (raw) and stage st (bf16) visible and guarantees that every wave
+    // is done with stage st-1, whose ring slot the DMA of stage st+3 reuses.
+    for (int s = 0; s < nst; s += C::NSLOT) {
+#pragma unroll
+        for (int u = 0; u < C::NSLOT; ++u) {
+            const int st = s + u;
+            s_wait_vmcnt_lgkm0<C::PER_STAGE>();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            dma(st + 3, (u + 3) % C::NSLOT);
+            if (st < nst) {
+                dequant((u + 1) % C::NSLOT, (u + 1) & 1);
+                mfma(u, u & 1);
+            }
+        }
+    }
+    s_wait_vmcnt_lgkm0<0>();
+
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int64_t n = n0 + wn * WN + b * 16 + lr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t m = m0 + wm * 128 + a * 16 + 4 * lg + i;
+                if (m < M && n < R) store_dt(y, y_dt, m * R + n, acc[a][b][i]);
+            }
+        }
+}
+
 }  // namespace
 
 namespace rq {
@@ -334,9 +742,37 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
                                       const void* scales, const void* biases, int sb_dt,
                                       int64_t m, int64_t rows, int64_t cols, int gs, void* y,
                                       int y_dt, hipStream_t stream) {
+    const int gs_shift = __builtin_ctz(gs);
+    if (m >= 256 && x_dt == RQ_BF16) {
+        const int bn = rows % 160 == 0 ? 160 : 128;
+        const int tm = (int)((m + 255) / 256);
+        const int tn = (int)((rows + bn - 1) / bn);
+        const int blocks = ((tm * tn + 7) / 8) * 8;
+#define RQ_DMA(BNV)                                                                              \
+    RQ_DISPATCH_DT(sb_dt, SD,                                                                    \
+        hipLaunchKernelGGL((qmm_t_dma<RQ_BITS, SD, BNV>), dim3(blocks), dim3(kBlock), 0, stream, \
+                           (const uint16_t*)x, wq, scales, biases, m, rows, cols, gs_shift, y,   \
+                           y_dt, tm, tn))
+        if (bn == 160) { RQ_DMA(160); } else { RQ_DMA(128); }
+#undef RQ_DMA
+        return hipGetLastError();
+    }
+    if (m >= 256) {
+        // weight-row tile: whole rounds over 256 CUs at M=4096 for the RWKV-7 shapes
+        const int bn = rows % 160 == 0 ? 160 : 128;
+        const int tm = (int)((m + 255) / 256);
+        const int tn = (int)((rows + bn - 1) / bn);
+        const int blocks = ((tm * tn + 7) / 8) * 8;
+#define RQ_BIG(BNV)                                                                          \
+    RQ_DISPATCH_DT(x_dt, XD,                                                                 \
+        hipLaunchKernelGGL((qmm_t_big<RQ_BITS, XD, BNV>), dim3(blocks), dim3(kBlock), 0, stream, \
+                           x, wq, scales, biases, sb_dt, m, rows, cols, gs_shift, y, y_dt, tm, tn))
+        if (bn == 160) { RQ_BIG(160); } else { RQ_BIG(128); }
+#undef RQ_BIG
+        return hipGetLastError();
+    }
     constexpr int BM = 128;
     const dim3 grid((unsigned)((rows + BN - 1) / BN), (unsigned)((m + BM - 1) / BM));
-    const int gs_shift = __builtin_ctz(gs);
     RQ_DISPATCH_DT(x_dt, XD,
         hipLaunchKernelGGL((qmm_t_kernel<RQ_BITS, XD, BM>), grid, dim3(kBlock), 0, stream, x, wq,
                            scales, biases, sb_dt, m, rows, cols, gs_shift, y, y_dt));
