@@ -515,8 +515,8 @@ __global__ __launch_bounds__(kBlock, 1) void qmm_t_big(
 //     so that MFMA fragment reads are bank-conflict free,
 //   * the packed codes of the BN weight rows (dword-dense [row][word]),
 //   * their scale and bias (one group per row per stage: 32 | group_size),
-// into a 4-slot LDS ring, three stages ahead of the MFMAs, without staging
-// registers.  One stage behind the DMA, threads [0, BN) dequantize the stage
+// into an NSLOT-slot LDS ring (6 where LDS allows, else 4), NSLOT-1 stages
+// ahead of the MFMAs, without staging registers.  One stage behind the DMA, threads [0, BN) dequantize the stage
 // (fp32 fma, bf16 round) into a 2-slot bf16 ring; the 4 waves (2x2, wave
 // tile 128 x BN/2, 16x16x32 bf16 MFMAs) consume it.  One workgroup barrier
 // per stage, preceded by an explicit wait for this wave's DMAs two stages
@@ -526,10 +526,12 @@ __global__ __launch_bounds__(kBlock, 1) void qmm_t_big(
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int BITS, int SDT, int BN>
+template <int BITS, int SDT, int BN, int NSLOT_>
 struct DmaCfg {
     static constexpr int BM = 256;
-    static constexpr int NSLOT = 4;                                   // DMA ring depth
+    static constexpr int NSLOT = NSLOT_;                              // DMA ring depth
+    static constexpr int AHEAD = NSLOT_ - 1;                          // stages in flight ahead
+    static_assert(NSLOT_ % 2 == 0, "the bf16 ring index is derived from the slot index");
     static constexpr int X_BYTES = BM * 64;                           // 16 KB
     static constexpr int NX = X_BYTES / (kBlock * 16);                // 4 x-DMAs per thread
     static constexpr int CODE_DW = BN * BITS;                         // dwords of codes
@@ -543,6 +545,12 @@ struct DmaCfg {
     static constexpr int B_BYTES = BN * BLD * 2;
 };
 
+template <int BITS, int SDT, int BN, int NSLOT>
+constexpr int dma_lds_bytes() {
+    typedef DmaCfg<BITS, SDT, BN, NSLOT> C;
+    return NSLOT * (C::X_BYTES + C::C_BYTES + 2 * C::S_BYTES) + 2 * C::B_BYTES;
+}
+
 template <int N>
 RQ_DEV void s_wait_vmcnt_lgkm0() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -550,23 +558,26 @@ RQ_DEV void s_wait_vmcnt_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
 }
 
-template <int BITS, int SDT, int BN>
+template <int BITS, int SDT, int BN, int NSLOT>
 __global__ __launch_bounds__(kBlock, 1) void qmm_t_dma(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
     void* __restrict__ y, int y_dt, int tiles_m, int tiles_n) {
-    typedef DmaCfg<BITS, SDT, BN> C;
+    typedef DmaCfg<BITS, SDT, BN, NSLOT> C;
     constexpr int BM = C::BM;
     constexpr int WN = BN / 2;
     constexpr int TM = 8, TN = WN / 16;
     // One LDS object per ring slot: the compiler's wait insertion can then
     // tell a read of one slot from a DMA in flight to another (distinct
     // objects do not alias) instead of draining every DMA before each read.
+    // (Slots past NSLOT are declared but never referenced: no LDS is used.)
 #define RQ_RING(name, bytes)                                                    \
     __shared__ __attribute__((aligned(16))) uint8_t name##0[bytes];             \
     __shared__ __attribute__((aligned(16))) uint8_t name##1[bytes];             \
     __shared__ __attribute__((aligned(16))) uint8_t name##2[bytes];             \
-    __shared__ __attribute__((aligned(16))) uint8_t name##3[bytes];
+    __shared__ __attribute__((aligned(16))) uint8_t name##3[bytes];             \
+    __shared__ __attribute__((aligned(16))) uint8_t name##4[bytes];             \
+    __shared__ __attribute__((aligned(16))) uint8_t name##5[bytes];
     RQ_RING(xr_, C::X_BYTES)
     RQ_RING(cr_, C::C_BYTES)
     RQ_RING(sr_, C::S_BYTES)
@@ -574,10 +585,13 @@ __global__ __launch_bounds__(kBlock, 1) void qmm_t_dma(
 #undef RQ_RING
     __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * C::BLD];
     __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * C::BLD];
-    auto xr = [&](int u) -> uint8_t* { return u == 0 ? xr_0 : u == 1 ? xr_1 : u == 2 ? xr_2 : xr_3; };
-    auto cr = [&](int u) -> uint8_t* { return u == 0 ? cr_0 : u == 1 ? cr_1 : u == 2 ? cr_2 : cr_3; };
-    auto sr = [&](int u) -> uint8_t* { return u == 0 ? sr_0 : u == 1 ? sr_1 : u == 2 ? sr_2 : sr_3; };
-    auto br = [&](int u) -> uint8_t* { return u == 0 ? br_0 : u == 1 ? br_1 : u == 2 ? br_2 : br_3; };
+#define RQ_PICK(name) \
+    [&](int u) -> uint8_t* { return u == 0 ? name##0 : u == 1 ? name##1 : u == 2 ? name##2 : u == 3 ? name##3 : u == 4 ? name##4 : name##5; }
+    auto xr = RQ_PICK(xr_);
+    auto cr = RQ_PICK(cr_);
+    auto sr = RQ_PICK(sr_);
+    auto br = RQ_PICK(br_);
+#undef RQ_PICK
     auto bq = [&](int u) -> uint16_t* { return u == 0 ? bq0 : bq1; };
 
     const int ntiles = tiles_m * tiles_n;
@@ -686,37 +700,269 @@ __global__ __launch_bounds__(kBlock, 1) void qmm_t_dma(
                 acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bf[b], acc[a][b], 0, 0, 0);
     };
 
-    // Prologue: stages 0..2 in flight; stage 0 dequantized into bf16 slot 0.
-    dma(0, 0);
-    dma(1, 1);
-    dma(2, 2);
-    s_wait_vmcnt_lgkm0<2 * C::PER_STAGE>();
+    // Prologue: stages 0..AHEAD-1 in flight; stage 0 dequantized into bf16 slot 0.
+#pragma unroll
+    for (int i = 0; i < C::AHEAD; ++i) dma(i, i);
+    s_wait_vmcnt_lgkm0<(C::AHEAD - 1) * C::PER_STAGE>();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     dequant(0, 0);
 
     // Main loop, unrolled by the ring size so every slot index is static.
-    // Iteration st: wait for this wave's DMAs of stage st+1 (stage st+2 may
-    // still fly) and for its own LDS traffic; the barrier then makes stage
-    // st+1 (raw) and stage st (bf16) visible and guarantees that every wave
-    // is done with stage st-1, whose ring slot the DMA of stage st+3 reuses.
+    // Iteration st: wait for this wave's DMAs of stage st+1 (stages st+2 ..
+    // st+AHEAD-1 may still fly) and for its own LDS traffic; the barrier then
+    // makes stage st+1 (raw) and stage st (bf16) visible and guarantees that
+    // every wave is done with stage st-1, whose ring slot the DMA of stage
+    // st+AHEAD reuses.
     for (int s = 0; s < nst; s += C::NSLOT) {
 #pragma unroll
         for (int u = 0; u < C::NSLOT; ++u) {
             const int st = s + u;
-            s_wait_vmcnt_lgkm0<C::PER_STAGE>();
+            s_wait_vmcnt_lgkm0<(C::AHEAD - 2) * C::PER_STAGE>();
             asm volatile("" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            dma(st + 3, (u + 3) % C::NSLOT);
+            dma(st + C::AHEAD, (u + C::AHEAD) % C::NSLOT);
             if (st < nst) {
-                dequant((u + 1) % C::NSLOT, (u + 1) & 1);
+                dequant((u + 1) % C::NSLOT, (u + 1) & 1);  // NSLOT is even
                 mfma(u, u & 1);
             }
         }
     }
     s_wait_vmcnt_lgkm0<0>();
+
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int64_t n = n0 + wn * WN + b * 16 + lr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t m = m0 + wm * 128 + a * 16 + 4 * lg + i;
+                if (m < M && n < R) store_dt(y, y_dt, m * R + n, acc[a][b][i]);
+            }
+        }
+}
+
+
+// -------------------------------------------------------------- qmm_t_ws
+//
+// Warp-specialised form of the DMA-fed GEMM (bf16 activations, M >= 256):
+// 8 waves per block.  Waves 0-3 only run MFMAs (2x2, wave tile 128 x BN/2,
+// fp32 accumulators); waves 4-7 ("producers") issue every direct-to-LDS load
+// of the ring and dequantize one stage ahead.  Each SIMD holds one wave of
+// each kind, so the hardware interleaves the producers' VALU work with the
+// consumers' matrix instructions.  One workgroup barrier per stage of 32
+// contraction elements orders the rings:
+//   producers: wait own DMAs of stage st+1 and own LDS writes; barrier;
+//              DMA stage st+AHEAD; dequantize stage st+1 into bf16 slot.
+//   consumers: wait own LDS reads; barrier; MFMAs on stage st.
+constexpr int kWsBlock = 512;
+
+template <int BITS, int SDT, int BN, int NSLOT>
+struct WsCfg {
+    static constexpr int BM = 256;
+    static constexpr int AHEAD = NSLOT - 1;
+    static constexpr int NP = 256;                              // producer threads
+    static constexpr int X_BYTES = BM * 64;                     // 16 KB activation stage
+    static constexpr int NX = X_BYTES / (NP * 16);              // 4 x-DMAs per producer
+    static constexpr int CODE_DW = BN * BITS;
+    static constexpr int NC = (CODE_DW + NP - 1) / NP;          // code DMAs per producer
+    static constexpr int C_BYTES = NC * NP * 4;
+    static constexpr int SB = SDT == RQ_F32 ? 4 : 2;
+    static constexpr int S_BYTES = NP * 4;                      // 4-byte lane stride
+    static constexpr int PER_STAGE = NX + NC + 2;
+    static constexpr int BLD = 40;                              // bf16 ring row stride
+    static constexpr int B_BYTES = BN * BLD * 2;
+    static_assert(NSLOT % 2 == 0, "the bf16 ring index is derived from the slot index");
+    static_assert(BN <= NP, "one producer thread dequantizes one weight row");
+};
+
+template <int BITS, int SDT, int BN, int NSLOT>
+__global__ __launch_bounds__(kWsBlock, 1) void qmm_t_ws(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
+    const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
+    void* __restrict__ y, int y_dt, int tiles_m, int tiles_n) {
+    typedef WsCfg<BITS, SDT, BN, NSLOT> C;
+    constexpr int BM = C::BM;
+    constexpr int WN = BN / 2;
+    constexpr int TM = 8, TN = WN / 16;
+#define RQ_RING(name, bytes)                                                    \
+    __shared__ __attribute__((aligned(16))) uint8_t name##0[bytes];             \
+    __shared__ __attribute__((aligned(16))) uint8_t name##1[bytes];             \
+    __shared__ __attribute__((aligned(16))) uint8_t name##2[bytes];             \
+    __shared__ __attribute__((aligned(16))) uint8_t name##3[bytes];
+    RQ_RING(xr_, C::X_BYTES)
+    RQ_RING(cr_, C::C_BYTES)
+    RQ_RING(sr_, C::S_BYTES)
+    RQ_RING(br_, C::S_BYTES)
+#undef RQ_RING
+    static_assert(NSLOT == 4, "four ring slots are declared");
+    __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * C::BLD];
+    __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * C::BLD];
+#define RQ_PICK(name) \
+    [&](int u) -> uint8_t* { return u == 0 ? name##0 : u == 1 ? name##1 : u == 2 ? name##2 : name##3; }
+    auto xr = RQ_PICK(xr_);
+    auto cr = RQ_PICK(cr_);
+    auto sr = RQ_PICK(sr_);
+    auto br = RQ_PICK(br_);
+#undef RQ_PICK
+    auto bq = [&](int u) -> uint16_t* { return u == 0 ? bq0 : bq1; };
+
+    const int ntiles = tiles_m * tiles_n;
+    const int per_xcd = (ntiles + 7) / 8;
+    const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+    if (t >= ntiles) return;
+    const int64_t m0 = (int64_t)(t / tiles_n) * BM, n0 = (int64_t)(t % tiles_n) * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool producer = wave >= 4;
+    const int pt = tid - 256;   // producer thread index
+    const int pw = wave - 4;    // producer wave index
+    const int64_t runs = K >> 5, wpr = runs * BITS, G = K >> gs_shift;
+    const int nst = (int)runs;
+
+    if (producer) {
+        // ---------------------------------------------------------- producers
+        // Per-lane source byte offsets relative to uniform per-stage bases.
+        uint32_t xoff[C::NX];
+#pragma unroll
+        for (int i = 0; i < C::NX; ++i) {
+            const int row = (pw * C::NX + i) * 16 + (lane >> 2);
+            const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+            int64_t grow = m0 + row;
+            grow = grow < M ? grow : M - 1;
+            xoff[i] = (uint32_t)((grow - m0) * K * 2 + chunk * 16);
+        }
+        uint32_t coff[C::NC];
+#pragma unroll
+        for (int i = 0; i < C::NC; ++i) {
+            const int d = pt + C::NP * i;
+            const int row = d / BITS;
+            const int word = d - row * BITS;
+            int64_t grow = n0 + (row < BN ? row : BN - 1);
+            grow = grow < R ? grow : R - 1;
+            coff[i] = (uint32_t)(((grow - n0) * wpr + word) * 4);
+        }
+        int64_t srow = n0 + (pt < BN ? pt : BN - 1);
+        srow = srow < R ? srow : R - 1;
+        const uint32_t soff = (uint32_t)((srow - n0) * G * C::SB);
+        const uint8_t* xbase = (const uint8_t*)(x + m0 * K);
+        const uint8_t* cbase = (const uint8_t*)(wq + n0 * wpr);
+        const uint8_t* sbase = (const uint8_t*)scales + n0 * G * C::SB;
+        const uint8_t* bbase = (const uint8_t*)biases + n0 * G * C::SB;
+
+        auto dma = [&](int st, int slot) {
+            const int64_t stc = st < nst ? st : nst - 1;  // past the end: reload the last stage
+            const uint8_t* xb = xbase + stc * 64;
+            const uint8_t* cb = cbase + stc * BITS * 4;
+            const int64_t gb = ((stc * 32) >> gs_shift) * C::SB;
+#pragma unroll
+            for (int i = 0; i < C::NX; ++i)
+                __builtin_amdgcn_global_load_lds((const void*)(xb + xoff[i]),
+                                                 (lds_void_t*)(xr(slot) + (pw * C::NX + i) * 1024),
+                                                 16, 0, 0);
+#pragma unroll
+            for (int i = 0; i < C::NC; ++i)
+                __builtin_amdgcn_global_load_lds((const void*)(cb + coff[i]),
+                                                 (lds_void_t*)(cr(slot) + (i * C::NP + pw * 64) * 4),
+                                                 4, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(sbase + gb + soff),
+                                             (lds_void_t*)(sr(slot) + pw * 64 * 4), C::SB, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(bbase + gb + soff),
+                                             (lds_void_t*)(br(slot) + pw * 64 * 4), C::SB, 0, 0);
+        };
+        auto dequant = [&](int slot, int bslot) {
+            if (pt < BN) {
+                uint32_t words[BITS];
+#pragma unroll
+                for (int w = 0; w < BITS; ++w) words[w] = *(const uint32_t*)(cr(slot) + (pt * BITS + w) * 4);
+                float s, b;
+                if constexpr (SDT == RQ_F32) {
+                    s = *(const float*)(sr(slot) + pt * 4);
+                    b = *(const float*)(br(slot) + pt * 4);
+                } else {
+                    s = dt_traits<SDT>::to_f32(*(const uint16_t*)(sr(slot) + pt * 4));
+                    b = dt_traits<SDT>::to_f32(*(const uint16_t*)(br(slot) + pt * 4));
+                }
+                uint32_t d[16];
+                dequant_run_fast<BITS>(words, s, b, d);
+                u32x4_t* dst = (u32x4_t*)(bq(bslot) + pt * C::BLD);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) dst[q] = u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
+            }
+        };
+
+#pragma unroll
+        for (int i = 0; i < C::AHEAD; ++i) dma(i, i);
+        s_wait_vmcnt_lgkm0<(C::AHEAD - 1) * C::PER_STAGE>();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // barrier 0: stage 0 has landed
+        asm volatile("" ::: "memory");
+        dequant(0, 0);
+        for (int s = 0; s < nst; s += NSLOT) {
+#pragma unroll
+            for (int u = 0; u < NSLOT; ++u) {
+                const int st = s + u;
+                s_wait_vmcnt_lgkm0<(C::AHEAD - 2) * C::PER_STAGE>();
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                dma(st + C::AHEAD, (u + C::AHEAD) % NSLOT);
+                if (st < nst) dequant((u + 1) % NSLOT, (u + 1) & 1);
+            }
+        }
+        s_wait_vmcnt_lgkm0<0>();
+        return;
+    }
+
+    // -------------------------------------------------------------- consumers
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lg = lane >> 4, lr = lane & 15;
+    f32x4_t acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // LDS byte offsets of this lane's fragments (slot-relative)
+    uint32_t aoff[TM];
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+        const int row = wm * 128 + a * 16 + lr;
+        aoff[a] = (uint32_t)(row * 64 + ((lg ^ ((row >> 2) & 3)) * 16));
+    }
+    const uint32_t boff = (uint32_t)((wn * WN + lr) * C::BLD + lg * 8);
+
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // barrier 0
+    asm volatile("" ::: "memory");
+    for (int s = 0; s < nst; s += NSLOT) {
+#pragma unroll
+        for (int u = 0; u < NSLOT; ++u) {
+            const int st = s + u;
+            s_wait_vmcnt_lgkm0<0>();  // own LDS reads of the previous stage are done
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (st < nst) {
+                bf16x8_t af[TM], bf[TN];
+#pragma unroll
+                for (int a = 0; a < TM; ++a)
+                    af[a] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xr(u) + aoff[a]));
+#pragma unroll
+                for (int b = 0; b < TN; ++b)
+                    bf[b] = __builtin_bit_cast(bf16x8_t,
+                                               *(const u32x4_t*)(bq(u & 1) + boff + b * 16 * C::BLD));
+#pragma unroll
+                for (int a = 0; a < TM; ++a)
+#pragma unroll
+                    for (int b = 0; b < TN; ++b)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bf[b], acc[a][b],
+                                                                            0, 0, 0);
+            }
+        }
+    }
 
 #pragma unroll
     for (int a = 0; a < TM; ++a)
@@ -750,9 +996,9 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
         const int blocks = ((tm * tn + 7) / 8) * 8;
 #define RQ_DMA(BNV)                                                                              \
     RQ_DISPATCH_DT(sb_dt, SD,                                                                    \
-        hipLaunchKernelGGL((qmm_t_dma<RQ_BITS, SD, BNV>), dim3(blocks), dim3(kBlock), 0, stream, \
-                           (const uint16_t*)x, wq, scales, biases, m, rows, cols, gs_shift, y,   \
-                           y_dt, tm, tn))
+        hipLaunchKernelGGL((qmm_t_ws<RQ_BITS, SD, BNV, 4>), dim3(blocks), dim3(kWsBlock), 0,     \
+                           stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,        \
+                           gs_shift, y, y_dt, tm, tn))
         if (bn == 160) { RQ_DMA(160); } else { RQ_DMA(128); }
 #undef RQ_DMA
         return hipGetLastError();
