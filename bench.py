@@ -15,6 +15,12 @@ GEMM (RWKV-7 2.9B shapes, M=4096) in TFLOP/s, and the CPU
 oracle's GEMV timed on the host cores on a bounded sample.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+
+HBM traffic of the headline kernel (`roofline.traffic`) comes from two
+rocprofv3 counter passes over `--pmc-workload` (the headline plan run three
+times, then three plain 1 GiB copies that calibrate the counters), reduced by
+`--pmc-report FETCH_DIR WRITE_DIR`; the reduced figures are kept in
+profiles/qmv_config2_sweep_m1_traffic.txt and read back here.
 """
 from __future__ import annotations
 
@@ -50,32 +56,117 @@ def parse():
                     help="bounded CPU-baseline sample length")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline sweep only")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run the headline plan 3x then 3 calibration copies, print nothing")
+    ap.add_argument("--pmc-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="reduce two rocprofv3 --pmc csv outputs of --pmc-workload")
     return ap.parse_args()
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmv_config2_sweep_m1_traffic.txt")
+PMC_RUNS, COPY_BYTES, COPY_RUNS = 3, 1 << 30, 3
+HEAD_KERNEL = "qmv_kernel"
+
+
+def pmc_workload(torch, rq, dev):
+    """What the counter passes profile: the headline plan PMC_RUNS times,
+    then COPY_RUNS copies of COPY_BYTES (read COPY_BYTES, write COPY_BYTES)
+    as the last dispatches of the process."""
+    probs, _ = make_sweep(rq, torch, dev, M=1)
+    plan = rq.GroupedQmv([x for _, x, _ in probs], [w for _, _, w in probs], 64, 4)
+    for _ in range(PMC_RUNS):
+        plan.run()
+    torch.cuda.synchronize()
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(COPY_RUNS):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def _pmc_rows(d):
+    import csv
+    import glob
+    files = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    # one value per dispatch (counters are summed over the per-dispatch rows)
+    per = {}
+    for did, name, v in rows:
+        n, acc = per.get(did, (name, 0.0))
+        per[did] = (n, acc + v)
+    return [(did, *per[did]) for did in sorted(per)]
+
+
+def pmc_report(fetch_dir, write_dir):
+    """Print the calibrated HBM traffic of the headline kernel per step and
+    per launch.  FETCH_SIZE / WRITE_SIZE are KiB per dispatch; the factor that
+    turns them into bytes is COPY_BYTES over what the calibration copies read
+    (resp. wrote)."""
+    out = {}
+    for tag, d in (("fetch", fetch_dir), ("write", write_dir)):
+        rows = _pmc_rows(d)
+        copies = rows[-COPY_RUNS:]
+        head = [r for r in rows if HEAD_KERNEL in r[1]]
+        if len(head) % PMC_RUNS:
+            raise SystemExit(f"{tag}: {len(head)} {HEAD_KERNEL} dispatches, not a multiple of "
+                             f"{PMC_RUNS}")
+        copy_kib = sum(r[2] for r in copies) / len(copies)
+        factor = COPY_BYTES / copy_kib
+        out[tag] = {"copy_kernel": copies[0][1][:80], "copy_kib": copy_kib, "factor": factor,
+                    "launches_per_step": len(head) // PMC_RUNS,
+                    "bytes_per_step": sum(r[2] for r in head) / PMC_RUNS * factor}
+    launches = out["fetch"]["launches_per_step"]
+    step = out["fetch"]["bytes_per_step"] + out["write"]["bytes_per_step"]
+    for tag in ("fetch", "write"):
+        o = out[tag]
+        print(f"{tag}: calibration copy {o['copy_kernel']!r} reads/writes {COPY_BYTES} B, "
+              f"counter {o['copy_kib']:.1f} KiB -> factor {o['factor']:.4f} B per counted KiB")
+        print(f"{tag}_bytes_per_step: {o['bytes_per_step']:.0f}")
+    print(f"launches_per_step: {launches}")
+    print(f"traffic_bytes_per_step: {step:.0f}")
+    print(f"traffic_bytes_per_launch: {step / launches:.0f}")
+
+
+def read_traffic():
+    """traffic_bytes_per_launch from the committed counter summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def make_sweep(rq, torch, dev, M, bits=4, gs=64):
-    """Quantize the config-2 weights on the GPU (seed per layer/projection)."""
+    """Quantize the config-2 weights on the GPU (seed per layer/projection).
+    Also returns the quantize kernel's GB/s on the head weight (R*K*2 bytes
+    read + packed bytes written), timed as one region of repeated calls."""
     probs = []
-    qtime = 0.0
-    qbytes = 0
+    qgbs = None
     for layer in range(LAYERS + 1):
         items = PROJ if layer < LAYERS else [("head", VOCAB, D)]
         for name, R, K in items:
             seed = 2_000_000 + 1000 * layer + PROJ_ID[name]
             g = torch.Generator(device=dev).manual_seed(seed)
             w = (torch.randn(R, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
             wq, s, b = rq.quantize(w, gs, bits)
-            e1.record()
-            e1.synchronize()
-            qtime += e0.elapsed_time(e1) / 1e3
-            qbytes += R * K * 2 + weight_bytes(R, K, bits, gs)
+            if name == "head":
+                t = time_region(torch, lambda: rq.quantize(w, gs, bits), 10, 2)
+                qgbs = (R * K * 2 + weight_bytes(R, K, bits, gs)) / t / 1e9
             del w
             gx = torch.Generator(device=dev).manual_seed(seed + 500)
             x = torch.randn(M, K, generator=gx, device=dev).to(torch.bfloat16)
             probs.append((name, x, (wq, s, b)))
-    return probs, qbytes / qtime / 1e9
+    return probs, qgbs
 
 
 def time_region(torch, fn, steps, warmup):
@@ -91,22 +182,19 @@ def time_region(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / 1e3 / steps
 
 
-def launch_durations(torch, fns, reps=5):
-    """HIP-event duration of each launch in `fns` (one event pair per launch,
-    on the stream the kernels run on), averaged over reps."""
-    tot = [0.0] * len(fns)
+def call_duration(torch, fn, reps):
+    """Mean HIP-event duration of one fn() call, one event pair per call,
+    recorded on torch's current stream -- the stream the library launches
+    on -- with a synchronisation between calls so that no two overlap."""
+    tot = 0.0
     for _ in range(reps):
-        evs = []
-        for f in fns:
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            f()
-            b.record()
-            evs.append((a, b))
-        torch.cuda.synchronize()
-        for i, (a, b) in enumerate(evs):
-            tot[i] += a.elapsed_time(b) / 1e3
-    return [t / reps for t in tot]
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        b.synchronize()
+        tot += a.elapsed_time(b) / 1e3
+    return tot / reps
 
 
 def cpu_baseline(torch, seconds):
@@ -142,6 +230,9 @@ def cpu_baseline(torch, seconds):
 
 def main():
     args = parse()
+    if args.pmc_report:
+        pmc_report(*args.pmc_report)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(the sharding design is described in DESIGN.md)"}))
@@ -152,6 +243,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     bits, gs = 4, 64
+    if args.pmc_workload:
+        pmc_workload(torch, rwkvq, dev)
+        return
 
     # ---------------- headline: config-2 decode sweep, M=1, grouped launches
     probs, quant_gbs = make_sweep(rwkvq, torch, dev, M=1)
@@ -164,14 +258,16 @@ def main():
     t_step = time_region(torch, plan.run, args.steps, args.warmup)
     value = total_wbytes / t_step / 1e9
 
-    # per-launch HIP-event durations of the grouped GEMV kernel
-    chunks = [(xs[i:i + 48], ws[i:i + 48], outs[i:i + 48]) for i in range(0, len(xs), 48)]
-    fns = [rwkvq.GroupedQmv(c[0], c[1], gs, bits, out=c[2]).run for c in chunks]
-    durs = launch_durations(torch, fns)
-    chunk_bytes = [sum(weight_bytes(w[0].shape[0], x.shape[1]) for x, w in zip(c[0], c[1]))
-                   for c in chunks]
-    kernel_time = sum(durs)
-    achieved = sum(chunk_bytes) / kernel_time / 1e9
+    # The step is one rq_qmm_grouped call; the library buckets the 145
+    # problems by K and issues ceil(bucket/48) launches of qmv_kernel per
+    # bucket (K=2048: 121 problems -> 3, K=8192: 24 -> 1), back to back on
+    # one stream.  Average launch = event time of the call / launches.
+    n2048 = sum(1 for x in xs if x.shape[1] == D)
+    launches = -(-n2048 // 48) + -(-(len(xs) - n2048) // 48)
+    call_t = call_duration(torch, plan.run, max(5, args.steps))
+    avg_launch = call_t / launches
+    bytes_per_launch = total_wbytes / launches
+    achieved = bytes_per_launch / avg_launch / 1e9
     result = {
         "metric": "q4 GEMV effective HBM GB/s (% of peak) + prefill qmm TFLOP/s, RWKV-7 1.5B",
         "value": round(value, 2),
@@ -191,13 +287,14 @@ def main():
                          "[65536,2048], M=1, 4-bit g64 bf16 scales/biases, grouped launch"),
             "weight_bytes_per_step": total_wbytes,
             "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-            "launches_per_step": len(chunks),
+            "launches_per_step": launches,
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "qmv_kernel<4,bf16,NMC=1,RB=4>",
-                     "avg_launch_us": round(kernel_time / len(durs) * 1e6, 2),
-                     "bytes_per_launch": int(sum(chunk_bytes) / len(chunk_bytes))},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic(),
+                     "kernel": "qmv_kernel<BITS=4, scales bf16, NMC=1, RB=1, KS=1, NS=4, SLDS>",
+                     "avg_launch_us": round(avg_launch * 1e6, 2),
+                     "bytes_per_launch": int(bytes_per_launch)},
     }
 
     if not args.no_extra:
