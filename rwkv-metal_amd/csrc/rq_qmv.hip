@@ -30,12 +30,16 @@
 //    so D row m' sums exactly one group and the lane's per-row scale can be
 //    applied to it.  M up to MC per pass; larger M uses NMC passes that
 //    share the loaded codes.
-//  * The +128 offset is removed with a second MFMA per span on a constant
-//    B (all 128.0): O[m'][n] = 128 * sum_{k in slot} x[m][k], in the same
-//    accumulator layout as D.  Then
-//        acc += s * D + (b/128 - s) * O  ==  s * sum q x + b * sum x.
+//  * The +128 offset is removed with the per-group sums of the activations,
+//    X[m][g] = sum_{k in g} x[m][k], computed once per block while x is
+//    staged (in LDS next to it):
+//        acc += s * D + (b - 128 s) * X  ==  s * sum q x + b * sum x.
 //    8-bit codes use exact bf16(q) operands (q <= 255 has 8 significant
-//    bits) and a constant B of 1.0.
+//    bits) and acc += s * D + b * X.  Without LDS staging the sums come from
+//    a second MFMA per span on a constant B (all 128.0, or 1.0 at 8 bits).
+//  * A lane's accumulator holds D rows m' = 4*(lane/16) + i; at small M only
+//    i < MI can be a real activation row (MI = min(M, 4) rounded up to a
+//    power of two), so only those are updated and stored.
 //  * Work unit ("task") = 16*RB rows of one problem.  A block of 4 waves
 //    takes 4 consecutive tasks of one problem (KS=1, each wave walks every
 //    span of K for its own rows) or, for small launches, one task whose
@@ -78,6 +82,9 @@ constexpr int kBlock = 64 * kWaves;
 #endif
 #ifndef RQ_QMV_BIG_RB
 #define RQ_QMV_BIG_RB 1  // 16-row blocks per wave for big launches
+#endif
+#ifndef RQ_QMV_BIG_MIN
+#define RQ_QMV_BIG_MIN 16384  // 16-row blocks in a launch from which RQ_QMV_BIG_RB applies
 #endif
 #if RQ_QMV_WAVES_PER_EU > 0
 #define RQ_QMV_OCC __attribute__((amdgpu_waves_per_eu(RQ_QMV_WAVES_PER_EU)))
@@ -230,7 +237,7 @@ constexpr int kLdsBudget = 64 * 1024;  // bytes of LDS staging per block
 // first).  In both, loads are never predicated: out-of-range rows and runs
 // read clamped, in-bounds addresses and are neutralised at compute time by a
 // zero scale and bias (s*D + (b/128 - s)*O = 0).
-template <int BITS, int SDT, int NMC, int RB, int KS, int NS, bool SLDS>
+template <int BITS, int SDT, int NMC, int MI, int RB, int KS, int NS, bool SLDS>
 __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs args) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
     typedef typename SBPair<SDT>::type sbp_t;
@@ -316,11 +323,14 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
         }
     }
 
-    // LDS: 64 zero bytes (the A operand of inactive lanes), x [M][K] bf16,
-    // then the block's (scale, bias) pairs [kRowsPerBlock][G].
+    // LDS: 64 zero bytes (the A operand of inactive lanes, and a zero group
+    // sum), x [M][K] bf16, the group sums X [M][G] fp32, then the block's
+    // (scale, bias) pairs [kRowsPerBlock][G].
     uint16_t* xzero = lds;
     uint16_t* xs = lds + 32;
-    sbp_t* sbs = (sbp_t*)(xs + (((int64_t)M * K + 7) & ~7ll));
+    const uint32_t xsum_f = (uint32_t)((64 + (((int64_t)M * K * 2 + 15) & ~15ll)) >> 2);
+    float* xsum = (float*)lds + xsum_f;
+    sbp_t* sbs = (sbp_t*)(xsum + (((int64_t)M * G + 3) & ~3ll));
     if constexpr (SLDS) {
         if (threadIdx.x < 4) *(u32x4_t*)&xzero[threadIdx.x * 8] = u32x4_t{0u, 0u, 0u, 0u};
         // Stage x[0..M) as bf16: 8 elements per thread per step.
@@ -339,6 +349,15 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
             uint32_t pr[4];  // stored as pairs (x_i, x_{i+4}): the order of the code pairs
             reorder_pairs(d, pr);
             *(u32x4_t*)&xs[e * 8] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
+            // Group sums of the bf16 values the MFMAs see.  A group is
+            // gs/8 consecutive e, i.e. consecutive lanes of one wave (K and
+            // the loop stride are multiples of gs/8), all active together.
+            float sum = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                sum += __uint_as_float(d[q] << 16) + __uint_as_float(d[q] & 0xffff0000u);
+            for (int w = 1; w < (1 << (gsh - 3)); w <<= 1) sum += __shfl_xor(sum, w, 64);
+            if ((e & ((1 << (gsh - 3)) - 1)) == 0) xsum[e >> (gsh - 3)] = sum;
         }
         // Stage the block's (scale, bias) pairs; rows past R are zero pairs.
         // With 16-bit scales, 16-byte aligned arrays and G % 8 == 0, eight
@@ -399,6 +418,20 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
         a_idx[c] = act ? (uint32_t)(32 + (int64_t)m * K + lg * 32) : 0u;
         a_step[c] = act ? 4u * 32u : 0u;  // elements per span (4 runs)
     }
+    // LDS float index of the group sum for D row 4*lg+i in pass c (0, a zero,
+    // when that row carries no activation row), and its step per span.
+    constexpr int kMI = SLDS ? MI : 1;
+    uint32_t g_idx[NMC][kMI], g_step[NMC][kMI];
+    const int slots_per_span = 4 >> slot_shift;
+#pragma unroll
+    for (int c = 0; c < NMC; ++c)
+#pragma unroll
+        for (int i = 0; i < kMI; ++i) {
+            const int m = c * MC + ((4 * lg + i) % MC);
+            const bool act = m < M;
+            g_idx[c][i] = act ? xsum_f + (uint32_t)(m * G + (lg >> slot_shift)) : 0u;
+            g_step[c][i] = act ? (uint32_t)slots_per_span : 0u;
+        }
     uint32_t sb_base[RB];
     bool row_ok[RB];
 #pragma unroll
@@ -413,6 +446,7 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
         const bool run_ok = run <= last_run;
         bf16x8_t a[NMC][4];
         f32x4_t o[NMC];
+        float xg[NMC][kMI];
 #pragma unroll
         for (int c = 0; c < NMC; ++c) {
             const int m = c * MC + (lr % MC);
@@ -426,6 +460,11 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
                 for (int q = 0; q < 4; ++q) {
                     const u32x4_t v = src[q];
                     xd[4 * q] = v[0]; xd[4 * q + 1] = v[1]; xd[4 * q + 2] = v[2]; xd[4 * q + 3] = v[3];
+                }
+#pragma unroll
+                for (int i = 0; i < kMI; ++i) {
+                    const uint32_t gi = run_ok ? g_idx[c][i] + (uint32_t)s * g_step[c][i] : 0u;
+                    xg[c][i] = ((const float*)lds)[gi];
                 }
             } else if (a_slot_ok && run_ok && m < M) {
                 if (x_dt == RQ_BF16) load_x_run_bf16<RQ_BF16>(x, (int64_t)m * K + run * 32, xd);
@@ -445,10 +484,12 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
                     a[c][j] = as_bf16x8(pr[0], pr[1], pr[2], pr[3]);
                 }
             }
-            o[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            if constexpr (!SLDS) {
+                o[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c][j], ones, o[c], 0, 0, 0);
+                for (int j = 0; j < 4; ++j)
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c][j], ones, o[c], 0, 0, 0);
+            }
         }
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
@@ -459,9 +500,11 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
                 codes_to_bf16_pairs<BITS>(st.cw[rb], j, pr, kc);
                 bop[j] = as_bf16x8(pr[0], pr[1], pr[2], pr[3]);
             }
-            const bool ok = run_ok && row_ok[rb];
             float sc, bi;
             if constexpr (SLDS) {
+                // Rows past R have zero pairs in LDS; runs past K have zero
+                // activations and group sums, so their (clamped, finite)
+                // scale multiplies zeros.
                 const uint32_t runc = run_ok ? run : last_run;
                 const sbp_t v = sbs[sb_base[rb] + (runc >> slot_shift)];
                 if constexpr (SDT == RQ_F32) {
@@ -471,22 +514,29 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
                     sc = raw_to_f32<SDT>(v & 0xffffu);
                     bi = raw_to_f32<SDT>(v >> 16);
                 }
-                sc = ok ? sc : 0.f;
-                bi = ok ? bi : 0.f;
             } else {
+                const bool ok = run_ok && row_ok[rb];
                 sc = ok ? raw_to_f32<SDT>(st.sc[rb]) : 0.f;
                 bi = ok ? raw_to_f32<SDT>(st.bi[rb]) : 0.f;
             }
-            const float cb = (BITS == 8) ? bi : (bi * 0.0078125f - sc);
+            // coefficient of the group sum (LDS path) or of O = 128 * sum
+            const float cb = (BITS == 8) ? bi
+                           : (SLDS ? fmaf(sc, -128.f, bi) : (bi * 0.0078125f - sc));
 #pragma unroll
             for (int c = 0; c < NMC; ++c) {
                 f32x4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[c][j], bop[j], d, 0, 0, 0);
+                if constexpr (SLDS) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[rb][c][i] = fmaf(sc, d[i], fmaf(cb, o[c][i], acc[rb][c][i]));
+                    for (int i = 0; i < kMI; ++i)
+                        acc[rb][c][i] = fmaf(sc, d[i], fmaf(cb, xg[c][i], acc[rb][c][i]));
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[rb][c][i] = fmaf(sc, d[i], fmaf(cb, o[c][i], acc[rb][c][i]));
+                }
             }
         }
     };
@@ -546,7 +596,7 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
 #pragma unroll
         for (int c = 0; c < NMC; ++c) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < (SLDS ? kMI : 4); ++i) {
                 float v = acc[rb][c][i];
                 if (slots == 4) v += __shfl_xor(v, 16, 64);
                 if (slots >= 2) v += __shfl_xor(v, 32, 64);
@@ -558,10 +608,10 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
     }
 }
 
-template <int SDT, int NMC, int RB, int KS, bool XLDS>
+template <int SDT, int NMC, int MI, int RB, int KS, bool XLDS>
 hipError_t launch_one(const QmvArgs& a, int blocks, size_t lds, hipStream_t stream) {
     constexpr int NS = XLDS ? RQ_QMV_NS : RQ_QMV_BATCH;
-    hipLaunchKernelGGL((qmv_kernel<RQ_BITS, SDT, NMC, RB, KS, NS, XLDS>), dim3(blocks),
+    hipLaunchKernelGGL((qmv_kernel<RQ_BITS, SDT, NMC, MI, RB, KS, NS, XLDS>), dim3(blocks),
                        dim3(kBlock), lds, stream, a);
     return hipGetLastError();
 }
@@ -570,12 +620,16 @@ template <int RB, int KS>
 hipError_t launch_cfg(const QmvArgs& a, int sb_dt, int nmc, bool xlds, int blocks, size_t lds,
                       hipStream_t stream) {
     hipError_t e = hipErrorInvalidValue;
-#define RQ_QMV_NMC(SD, XL)                                                         \
-    switch (nmc) {                                                                 \
-        case 1: e = launch_one<SD, 1, RB, KS, XL>(a, blocks, lds, stream); break;   \
-        case 2: e = launch_one<SD, 2, RB, KS, XL>(a, blocks, lds, stream); break;   \
-        case 4: e = launch_one<SD, 4, RB, KS, XL>(a, blocks, lds, stream); break;   \
-        default: break;                                                            \
+    // MI: accumulator rows that can carry activations (see the kernel)
+    const int mi = a.m >= 3 ? 4 : a.m;
+#define RQ_QMV_NMC(SD, XL)                                                                \
+    switch (nmc * 8 + (nmc == 1 ? mi : 4)) {                                              \
+        case 9: e = launch_one<SD, 1, 1, RB, KS, XL>(a, blocks, lds, stream); break;       \
+        case 10: e = launch_one<SD, 1, 2, RB, KS, XL>(a, blocks, lds, stream); break;      \
+        case 12: e = launch_one<SD, 1, 4, RB, KS, XL>(a, blocks, lds, stream); break;      \
+        case 20: e = launch_one<SD, 2, 4, RB, KS, XL>(a, blocks, lds, stream); break;      \
+        case 36: e = launch_one<SD, 4, 4, RB, KS, XL>(a, blocks, lds, stream); break;      \
+        default: break;                                                                   \
     }
     RQ_DISPATCH_DT(sb_dt, SD, if (xlds) { RQ_QMV_NMC(SD, true) } else { RQ_QMV_NMC(SD, false) });
 #undef RQ_QMV_NMC
@@ -605,13 +659,14 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
     // stream at once.
     int64_t rowblocks = 0;
     for (int i = 0; i < n; ++i) rowblocks += (probs[i]->rows + 15) / 16;
-    const int cfg = rowblocks >= 16384 ? 2 : (rowblocks >= 2048 ? 1 : 0);
+    const int cfg = rowblocks >= RQ_QMV_BIG_MIN ? 2 : (rowblocks >= 2048 ? 1 : 0);
     const int RB = cfg == 2 ? RQ_QMV_BIG_RB : 1;
     const int rows_per_block = cfg == 0 ? 16 * RB : 16 * RB * kWaves;
-    // LDS staging: a zero line, activations [m][K] as bf16, then the block's
-    // (scale, bias) pairs.
+    // LDS staging: a zero line, activations [m][K] as bf16, their group sums
+    // [m][K/gs] fp32, then the block's (scale, bias) pairs.
     const size_t sbsz = sb_dt == RQ_F32 ? 8 : 4;
     const size_t lds = 64 + (((size_t)m * K * 2 + 15) & ~(size_t)15) +
+                       (((size_t)m * (K / gs) * 4 + 15) & ~(size_t)15) +
                        (size_t)rows_per_block * (K / gs) * sbsz;
     const bool xlds = lds <= (size_t)kLdsBudget;
     const size_t dyn = xlds ? lds : 0;
