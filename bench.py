@@ -60,6 +60,8 @@ def parse():
                     help="run the headline plan 3x then 3 calibration copies, print nothing")
     ap.add_argument("--pmc-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="reduce two rocprofv3 --pmc csv outputs of --pmc-workload")
+    ap.add_argument("--kt-report", metavar="DIR",
+                    help="print rocprofv3 --kernel-trace --stats csv output as a table")
     return ap.parse_args()
 
 
@@ -132,6 +134,43 @@ def pmc_report(fetch_dir, write_dir):
     print(f"launches_per_step: {launches}")
     print(f"traffic_bytes_per_step: {step:.0f}")
     print(f"traffic_bytes_per_launch: {step / launches:.0f}")
+
+
+def kt_report(d):
+    """Markdown table of the kernel statistics rocprofv3 wrote under `d`
+    (*kernel_stats.csv), plus per-grid-size medians of the library's kernels
+    from *kernel_trace.csv."""
+    import csv
+    import glob
+    import statistics
+    stats = sorted(glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True))
+    if not stats:
+        raise SystemExit(f"no *kernel_stats.csv under {d}")
+    print("| kernel | calls | avg us | min us | max us | % time |")
+    print("|---|---|---|---|---|---|")
+    with open(stats[0], newline="") as fh:
+        for r in csv.DictReader(fh):
+            name = r["Name"].replace("(anonymous namespace)::", "")
+            name = name.split("(")[0] if not name.startswith("void (") else name
+            print(f"| `{name[:110]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                  f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                  f"{float(r['Percentage']):.2f} |")
+    traces = sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True))
+    if traces:
+        per = {}
+        with open(traces[0], newline="") as fh:
+            for r in csv.DictReader(fh):
+                if not any(k in r["Kernel_Name"] for k in ("qmv_kernel", "qmm_", "quantize_kernel")):
+                    continue
+                key = (r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0],
+                       int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])))
+                per.setdefault(key, []).append(
+                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        print()
+        print("| kernel | workgroups | dispatches | median us |")
+        print("|---|---|---|---|")
+        for (name, wg), v in sorted(per.items()):
+            print(f"| `{name[:100]}` | {wg} | {len(v)} | {statistics.median(v):.2f} |")
 
 
 def read_traffic():
@@ -232,6 +271,9 @@ def main():
     args = parse()
     if args.pmc_report:
         pmc_report(*args.pmc_report)
+        return
+    if args.kt_report:
+        kt_report(args.kt_report)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
