@@ -21,6 +21,8 @@
  *   rq_qmm_grouped <- several independent mx.quantized_matmul(transpose=True) nodes of one
  *                     lazy MLX graph evaluated together (e.g. tmix r/k/v projections,
  *                     rwkv_metal/model/rwkv7_x070.py:142-144); one launch for all of them
+ *   rq_grouped_plan_* <- the same, with the launch schedule kept in device memory so that
+ *                     any number of problems runs as one launch per call
  *
  * Layout (identical to MLX's): W is [rows, cols], cols (= in_features) is the
  * grouped and packed axis.  w_q is uint32[rows, cols*bits/32], each row an
@@ -35,7 +37,9 @@
  * Return codes: RQ_OK (0); RQ_EINVAL (-1): bits not in {2,3,4,5,6,8},
  * group_size not in {32,64,128}, cols % group_size != 0, a negative size, a
  * NULL pointer or an unknown dtype; RQ_EALIGN (-2): a pointer not 16-byte
- * aligned; RQ_ELAUNCH (-3): the HIP launch failed.  rq_last_error() returns a
+ * aligned; RQ_ELAUNCH (-3): the HIP launch failed; RQ_EUNSUPPORTED (-4): valid
+ * arguments outside what the called entry point covers (the message names the
+ * entry point that does).  rq_last_error() returns a
  * thread-local message describing the last non-zero return.
  *
  * Reentrant: calls from several host threads on different streams are safe.
@@ -53,7 +57,7 @@ extern "C" {
 
 typedef enum { RQ_BF16 = 0, RQ_F16 = 1, RQ_F32 = 2 } rq_dtype;
 
-enum { RQ_OK = 0, RQ_EINVAL = -1, RQ_EALIGN = -2, RQ_ELAUNCH = -3 };
+enum { RQ_OK = 0, RQ_EINVAL = -1, RQ_EALIGN = -2, RQ_ELAUNCH = -3, RQ_EUNSUPPORTED = -4 };
 
 /* ABI version of the loaded library (RWKVQ_ABI_VERSION). */
 int rq_abi_version(void);
@@ -113,6 +117,33 @@ typedef struct {
 #define RQ_MAX_GROUPED 48
 int rq_qmm_grouped(const rq_problem* problems, int n, rq_dtype x_dt, rq_dtype sb_dt,
                    rq_dtype y_dt, int64_t m, int group_size, int bits, void* stream);
+
+/* Planned grouped decode GEMV: the schedule of a fixed set of problems (the
+ * projections one decode step runs, re-run every step with new activations
+ * in the same buffers) is written once into caller-owned device memory, and
+ * each run is ONE kernel launch however many problems there are.  Same
+ * semantics as rq_qmm_grouped.  Like rq_qmm_grouped it has no single MLX
+ * counterpart: it evaluates several independent mx.quantized_matmul
+ * (transpose=True) nodes of one lazy graph (rwkv_metal/model/rwkv7_x070.py:142-144,
+ * the 24-layer decode sweep of the benchmark).
+ *
+ * rq_grouped_plan_table_bytes: device bytes the table needs (or < 0 on error).
+ * rq_grouped_plan_init: validates, orders the problems longest contraction
+ *   first, uploads the table to `table` and SYNCHRONISES `stream` (the host
+ *   staging copy does not outlive the call).  Returns RQ_EUNSUPPORTED for
+ *   problems outside the planned kernel (scales must be 16-bit and 16-byte
+ *   aligned, cols % 512 == 0, m*cols*2 bytes of activations within the LDS
+ *   budget); rq_qmm_grouped covers those.
+ * rq_grouped_plan_run: one launch on `stream`.  The table and every pointer
+ *   of the problems must stay valid for as long as the plan is run. */
+typedef struct {
+    int64_t opaque[8];
+} rq_grouped_plan;
+int64_t rq_grouped_plan_table_bytes(const rq_problem* problems, int n);
+int rq_grouped_plan_init(const rq_problem* problems, int n, rq_dtype x_dt, rq_dtype sb_dt,
+                         rq_dtype y_dt, int64_t m, int group_size, int bits, void* table,
+                         int64_t table_bytes, rq_grouped_plan* plan, void* stream);
+int rq_grouped_plan_run(const rq_grouped_plan* plan, void* stream);
 
 #ifdef __cplusplus
 }

@@ -40,7 +40,8 @@ def lib() -> ctypes.CDLL:
         L.rqo_pack.argtypes = [vp, i64, i64, i32, vp]
         L.rqo_unpack.argtypes = [vp, i64, i64, i32, vp]
         L.rqo_dequantize.argtypes = [vp, vp, vp, i32, i64, i64, i32, i32, vp, i32]
-        L.rqo_qmm.argtypes = [vp, i32, vp, vp, vp, i32, i64, i64, i64, i32, i32, i32, vp, i32, i32]
+        L.rqo_qmm.argtypes = [vp, i32, vp, vp, vp, i32, i64, i64, i64, i32, i32, i32, vp, i32, i32,
+                              i32]
         L.rqo_qmv_bf16.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, vp, i32]
         L.rqo_round_bf16.argtypes = [ctypes.c_float]
         L.rqo_round_bf16.restype = ctypes.c_float
@@ -102,7 +103,15 @@ def dequantize(wq, scales, biases, group_size=64, bits=4, out_dtype=None):
 
 
 def quantized_matmul(x, wq, scales, biases, transpose=True, group_size=64, bits=4,
-                     out_dtype=None, nthreads=0):
+                     out_dtype=None, nthreads=0, weights="mlx"):
+    """weights="mlx": the weights are dequantize()'s values (each of s*q and
+    +b rounded to the promoted dtype, as MLX's tiled qmm dequantizes);
+    weights="exact": s*q + b in double, unrounded (what MLX's qmv computes by
+    applying s and b to per-group sums).  For N(0, 0.02) weights the two
+    differ by up to ~1% relative: the bias is several times the weight, so
+    rounding s*q to bf16 costs more than rounding w."""
+    if weights not in ("mlx", "exact"):
+        raise ValueError("weights must be 'mlx' or 'exact'")
     x, wq, scales, biases = x.contiguous(), wq.contiguous(), scales.contiguous(), biases.contiguous()
     R, W = wq.shape
     K = W * 32 // bits
@@ -117,7 +126,7 @@ def quantized_matmul(x, wq, scales, biases, transpose=True, group_size=64, bits=
     y = torch.empty(*lead, n_out, dtype=out_dtype)
     rc = lib().rqo_qmm(_p(x), DT[x.dtype], _p(wq), _p(scales), _p(biases), DT[scales.dtype], m,
                        R, K, group_size, bits, 1 if transpose else 0, _p(y), DT[out_dtype],
-                       nthreads)
+                       nthreads, 1 if weights == "exact" else 0)
     if rc != 0:
         raise ValueError(f"oracle qmm rejected arguments (rc={rc})")
     return y

@@ -26,8 +26,12 @@
  *                      (rwkvq_native.py:119-122, the VJP w.r.t. x for the QLoRA
  *                      backward is the transpose=False form).  Operands are
  *                      promoted to a common dtype T as MLX does; the weights
- *                      used are exactly rqo_dequantize's values in T; products
- *                      are accumulated in double.
+ *                      are either exactly rqo_dequantize's values in T (the
+ *                      form of MLX's tiled qmm, which dequantizes into T) or,
+ *                      with exact_w, scale*code + bias evaluated in double
+ *                      with no rounding (the form of MLX's qmv, which applies
+ *                      scale and bias to per-group sums of x*code and x);
+ *                      products are accumulated in double.
  *
  * Build: oracle/Makefile (gcc, -ffp-contract=off so no FMA contraction changes
  * the quantize arithmetic).
@@ -287,12 +291,41 @@ int rqo_dequantize(const uint32_t* wq, const void* scales, const void* biases, i
 
 /* ------------------------------------------------------------------- qmm */
 
+/* Row r of the weights in double: the dequantized values in T (exact_w = 0),
+ * or scale*code + bias with scale and bias cast to T and no rounding after
+ * (exact_w = 1). */
+static void weight_row_f64(const uint32_t* wq, const void* scales, const void* biases, int sb_dt,
+                           int T, int64_t r, int64_t K, int gs, int bits, int exact_w,
+                           float* tmp, double* out) {
+    if (!exact_w) {
+        dequant_rows_f32(wq, scales, biases, sb_dt, T, r, K, gs, bits, tmp);
+        for (int64_t k = 0; k < K; ++k) out[k] = (double)tmp[k];
+        return;
+    }
+    const int64_t G = K / gs;
+    const uint32_t* in = wq + r * (K * bits / 32);
+    const uint32_t mask = (1u << bits) - 1u;
+    for (int64_t g = 0; g < G; ++g) {
+        const double sc = (double)round_to(T, load_el(scales, sb_dt, r * G + g));
+        const double bi = (double)round_to(T, load_el(biases, sb_dt, r * G + g));
+        for (int j = 0; j < gs; ++j) {
+            const int64_t k = g * gs + j;
+            const int64_t bit = k * bits;
+            const int64_t w = bit >> 5;
+            const int off = (int)(bit & 31);
+            uint64_t win = in[w];
+            if (off + bits > 32) win |= (uint64_t)in[w + 1] << 32;
+            out[k] = sc * (double)(uint32_t)((win >> off) & mask) + bi;
+        }
+    }
+}
+
 /* transpose=1: y[m, rows] = x[m, cols] . W^T ; transpose=0: y[m, cols] = x[m, rows] . W.
  * T = promote(x_dt, sb_dt); x and the scales are cast to T, the weights are
- * the dequantized values in T, the sum runs in double and is cast to y_dt. */
+ * weight_row_f64's values, the sum runs in double and is cast to y_dt. */
 int rqo_qmm(const void* x, int x_dt, const uint32_t* wq, const void* scales, const void* biases,
             int sb_dt, int64_t m, int64_t rows, int64_t cols, int gs, int bits, int transpose,
-            void* y, int y_dt, int nthreads) {
+            void* y, int y_dt, int nthreads, int exact_w) {
     if (!valid_bits(bits) || !valid_gs(gs) || !valid_dt(x_dt) || !valid_dt(sb_dt) ||
         !valid_dt(y_dt))
         return -1;
@@ -309,18 +342,20 @@ int rqo_qmm(const void* x, int x_dt, const uint32_t* wq, const void* scales, con
         for (int64_t i = 0; i < m * K; ++i) xf[i] = round_to(T, load_el(x, x_dt, i));
 #pragma omp parallel
         {
-            float* wrow = (float*)malloc(sizeof(float) * (size_t)K);
+            float* tmp = (float*)malloc(sizeof(float) * (size_t)K);
+            double* wrow = (double*)malloc(sizeof(double) * (size_t)K);
 #pragma omp for schedule(static)
             for (int64_t r = 0; r < rows; ++r) {
-                dequant_rows_f32(wq, scales, biases, sb_dt, T, r, K, gs, bits, wrow);
+                weight_row_f64(wq, scales, biases, sb_dt, T, r, K, gs, bits, exact_w, tmp, wrow);
                 for (int64_t i = 0; i < m; ++i) {
                     const float* xr = xf + i * K;
                     double acc = 0.0;
-                    for (int64_t k = 0; k < K; ++k) acc += (double)xr[k] * (double)wrow[k];
+                    for (int64_t k = 0; k < K; ++k) acc += (double)xr[k] * wrow[k];
                     store_el(y, y_dt, i * rows + r, (float)acc);
                 }
             }
             free(wrow);
+            free(tmp);
         }
         free(xf);
     } else {
@@ -332,7 +367,8 @@ int rqo_qmm(const void* x, int x_dt, const uint32_t* wq, const void* scales, con
          * dequantizes every row but writes only its slice. */
 #pragma omp parallel
         {
-            float* wrow = (float*)malloc(sizeof(float) * (size_t)K);
+            float* tmp = (float*)malloc(sizeof(float) * (size_t)K);
+            double* wrow = (double*)malloc(sizeof(double) * (size_t)K);
             int nt = 1, tid = 0;
 #ifdef _OPENMP
             nt = omp_get_num_threads();
@@ -344,15 +380,17 @@ int rqo_qmm(const void* x, int x_dt, const uint32_t* wq, const void* scales, con
             for (int64_t r = 0; r < R; ++r) {
                 if (k1 > k0) {
                     /* dequantize the whole row: simple, the slice is what is used */
-                    dequant_rows_f32(wq, scales, biases, sb_dt, T, r, K, gs, bits, wrow);
+                    weight_row_f64(wq, scales, biases, sb_dt, T, r, K, gs, bits, exact_w, tmp,
+                                   wrow);
                     for (int64_t i = 0; i < m; ++i) {
                         double xv = xf[i * R + r];
                         double* ar = acc + i * K;
-                        for (int64_t k = k0; k < k1; ++k) ar[k] += xv * (double)wrow[k];
+                        for (int64_t k = k0; k < k1; ++k) ar[k] += xv * wrow[k];
                     }
                 }
             }
             free(wrow);
+            free(tmp);
         }
         for (int64_t i = 0; i < m * K; ++i) store_el(y, y_dt, i, (float)acc[i]);
         free(acc);

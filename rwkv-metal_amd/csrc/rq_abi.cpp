@@ -6,9 +6,11 @@
 // thread-local buffer read by rq_last_error().
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <vector>
 
 #include "../../include/rwkvq.h"
 #include "rq_launch.h"
@@ -22,6 +24,28 @@ namespace rq {
                                  int, int64_t, int64_t, int64_t, int, void*, int, hipStream_t); \
     hipError_t launch_qmm_n_b##B(const void*, int, const uint32_t*, const void*, const void*,    \
                                  int, int64_t, int64_t, int64_t, int, void*, int, hipStream_t);
+#define RQ_DECLARE_TABLE(B)                                                                    \
+    hipError_t launch_qmv_table_b##B(const QmvTable&, int, int, int, size_t, hipStream_t);
+RQ_DECLARE_TABLE(2)
+RQ_DECLARE_TABLE(3)
+RQ_DECLARE_TABLE(4)
+RQ_DECLARE_TABLE(5)
+RQ_DECLARE_TABLE(6)
+RQ_DECLARE_TABLE(8)
+
+hipError_t launch_qmv_table(const QmvTable& t, int blocks, int sb_dt, int gs, int bits,
+                            size_t lds, hipStream_t stream) {
+    switch (bits) {
+        case 2: return launch_qmv_table_b2(t, blocks, sb_dt, gs, lds, stream);
+        case 3: return launch_qmv_table_b3(t, blocks, sb_dt, gs, lds, stream);
+        case 4: return launch_qmv_table_b4(t, blocks, sb_dt, gs, lds, stream);
+        case 5: return launch_qmv_table_b5(t, blocks, sb_dt, gs, lds, stream);
+        case 6: return launch_qmv_table_b6(t, blocks, sb_dt, gs, lds, stream);
+        case 8: return launch_qmv_table_b8(t, blocks, sb_dt, gs, lds, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 RQ_DECLARE_BITS(2)
 RQ_DECLARE_BITS(3)
 RQ_DECLARE_BITS(4)
@@ -179,25 +203,137 @@ int rq_qmm(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales
     return launch_status(e, "rq_qmm");
 }
 
-int rq_qmm_grouped(const rq_problem* problems, int n, rq_dtype x_dt, rq_dtype sb_dt,
-                   rq_dtype y_dt, int64_t m, int group_size, int bits, void* stream) {
-    if (n < 0 || (n > 0 && !problems)) return fail(RQ_EINVAL, "rq_qmm_grouped: bad problem list");
+static int check_grouped(const char* what, const rq_problem* problems, int n, rq_dtype x_dt,
+                         rq_dtype sb_dt, rq_dtype y_dt, int64_t m, int group_size, int bits) {
+    if (n < 0 || (n > 0 && !problems)) return fail(RQ_EINVAL, "%s: bad problem list", what);
     if (!valid_dt(x_dt) || !valid_dt(sb_dt) || !valid_dt(y_dt)) return fail(RQ_EINVAL, "unsupported dtype");
-    if (m < 1 || m > 16) return fail(RQ_EINVAL, "rq_qmm_grouped: m must be in [1, 16] (got %lld)", (long long)m);
+    if (m < 1 || m > 16) return fail(RQ_EINVAL, "%s: m must be in [1, 16] (got %lld)", what, (long long)m);
     for (int i = 0; i < n; ++i) {
         const rq_problem& p = problems[i];
         if (int rc = check_common(p.rows, p.cols, group_size, bits)) return rc;
         if (p.cols == 0 && p.rows > 0)
-            return fail(RQ_EINVAL, "rq_qmm_grouped: problem %d has an empty contraction", i);
+            return fail(RQ_EINVAL, "%s: problem %d has an empty contraction", what, i);
         if (p.rows > 0 && (!p.x || !p.w_q || !p.scales || !p.biases || !p.y))
-            return fail(RQ_EINVAL, "rq_qmm_grouped: NULL pointer in problem %d", i);
+            return fail(RQ_EINVAL, "%s: NULL pointer in problem %d", what, i);
         if (!aligned16(p.x) || !aligned16(p.w_q))
-            return fail(RQ_EALIGN, "rq_qmm_grouped: problem %d: x and w_q must be 16-byte aligned", i);
+            return fail(RQ_EALIGN, "%s: problem %d: x and w_q must be 16-byte aligned", what, i);
     }
+    return RQ_OK;
+}
+
+int rq_qmm_grouped(const rq_problem* problems, int n, rq_dtype x_dt, rq_dtype sb_dt,
+                   rq_dtype y_dt, int64_t m, int group_size, int bits, void* stream) {
+    if (int rc = check_grouped("rq_qmm_grouped", problems, n, x_dt, sb_dt, y_dt, m, group_size, bits))
+        return rc;
     if (n == 0) return ok();
     return launch_status(rq::launch_qmv(problems, n, x_dt, sb_dt, y_dt, m, group_size, bits,
                                         (hipStream_t)stream),
                          "rq_qmm_grouped");
+}
+
+// ---------------------------------------------------------------- plans
+// Table layout in device memory: rq_problem descs[n] (sorted by cols,
+// descending; 16-byte padded), then uint32 blocks[nblocks] with
+// problem << 16 | 64-row block of that problem, longest blocks first.
+static const int64_t kPlanMagic = 0x5251504c414e31ll;  // "RQPLAN1"
+
+static int64_t plan_blocks(const rq_problem* problems, int n) {
+    int64_t b = 0;
+    for (int i = 0; i < n; ++i)
+        b += (problems[i].rows + rq::kQmvRowsPerBlock - 1) / rq::kQmvRowsPerBlock;
+    return b;
+}
+
+static int64_t plan_desc_bytes(int n) { return ((int64_t)n * (int64_t)sizeof(rq_problem) + 15) & ~15ll; }
+
+int64_t rq_grouped_plan_table_bytes(const rq_problem* problems, int n) {
+    if (n < 0 || (n > 0 && !problems)) return fail(RQ_EINVAL, "rq_grouped_plan_table_bytes: bad problem list");
+    return plan_desc_bytes(n) + 4 * plan_blocks(problems, n);
+}
+
+int rq_grouped_plan_init(const rq_problem* problems, int n, rq_dtype x_dt, rq_dtype sb_dt,
+                         rq_dtype y_dt, int64_t m, int group_size, int bits, void* table,
+                         int64_t table_bytes, rq_grouped_plan* plan, void* stream) {
+    if (!plan) return fail(RQ_EINVAL, "rq_grouped_plan_init: NULL plan");
+    std::memset(plan, 0, sizeof(*plan));
+    if (int rc = check_grouped("rq_grouped_plan_init", problems, n, x_dt, sb_dt, y_dt, m,
+                               group_size, bits))
+        return rc;
+    std::vector<int> order;
+    for (int i = 0; i < n; ++i) {
+        if (problems[i].rows == 0) continue;
+        if (!rq::qmv_stream_covers(problems[i], sb_dt, m, group_size))
+            return fail(RQ_EUNSUPPORTED,
+                        "rq_grouped_plan_init: problem %d is outside the planned GEMV (needs "
+                        "16-bit scales, cols %% 512 == 0, 16-byte aligned scales/biases, "
+                        "m*cols*2 bytes of activations within the LDS budget); use rq_qmm_grouped",
+                        i);
+        if ((problems[i].rows + rq::kQmvRowsPerBlock - 1) / rq::kQmvRowsPerBlock > 65536)
+            return fail(RQ_EUNSUPPORTED, "rq_grouped_plan_init: problem %d has too many rows", i);
+        order.push_back(i);
+    }
+    if (order.size() > 65535) return fail(RQ_EUNSUPPORTED, "rq_grouped_plan_init: too many problems");
+    // longest contraction first: the last blocks to start are the shortest
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int a, int b) { return problems[a].cols > problems[b].cols; });
+    const int nn = (int)order.size();
+    std::vector<rq_problem> descs(nn);
+    size_t lds = 0;
+    for (int i = 0; i < nn; ++i) {
+        descs[i] = problems[order[i]];
+        lds = std::max(lds, rq::qmv_stream_lds(m, descs[i].cols, group_size));
+    }
+    const int64_t nblocks = plan_blocks(descs.data(), nn);
+    const int64_t dbytes = plan_desc_bytes(nn);
+    const int64_t need = dbytes + 4 * nblocks;
+    if (nn > 0) {
+        if (!table) return fail(RQ_EINVAL, "rq_grouped_plan_init: NULL table");
+        if (!aligned16(table)) return fail(RQ_EALIGN, "rq_grouped_plan_init: table must be 16-byte aligned");
+        if (table_bytes < need)
+            return fail(RQ_EINVAL, "rq_grouped_plan_init: table has %lld bytes, needs %lld",
+                        (long long)table_bytes, (long long)need);
+        std::vector<uint8_t> host((size_t)need, 0);
+        std::memcpy(host.data(), descs.data(), (size_t)nn * sizeof(rq_problem));
+        uint32_t* blk = (uint32_t*)(host.data() + dbytes);
+        int64_t b = 0;
+        for (int i = 0; i < nn; ++i) {
+            const int64_t nb = (descs[i].rows + rq::kQmvRowsPerBlock - 1) / rq::kQmvRowsPerBlock;
+            for (int64_t j = 0; j < nb; ++j) blk[b++] = ((uint32_t)i << 16) | (uint32_t)j;
+        }
+        hipStream_t s = (hipStream_t)stream;
+        hipError_t e = hipMemcpyAsync(table, host.data(), (size_t)need, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);  // the host copy dies with this call
+        if (e != hipSuccess)
+            return fail(RQ_ELAUNCH, "rq_grouped_plan_init: table upload failed: %s", hipGetErrorString(e));
+    }
+    plan->opaque[0] = (int64_t)(uintptr_t)table;
+    plan->opaque[1] = nblocks;
+    plan->opaque[2] = m;
+    plan->opaque[3] = group_size;
+    plan->opaque[4] = bits;
+    plan->opaque[5] = (int64_t)x_dt | ((int64_t)sb_dt << 8) | ((int64_t)y_dt << 16) | ((int64_t)nn << 24);
+    plan->opaque[6] = (int64_t)lds;
+    plan->opaque[7] = kPlanMagic;
+    return ok();
+}
+
+int rq_grouped_plan_run(const rq_grouped_plan* plan, void* stream) {
+    if (!plan || plan->opaque[7] != kPlanMagic)
+        return fail(RQ_EINVAL, "rq_grouped_plan_run: not an initialised plan");
+    const int64_t nblocks = plan->opaque[1];
+    if (nblocks == 0) return ok();
+    const int nn = (int)(plan->opaque[5] >> 24);
+    rq::QmvTable t;
+    t.descs = (const rq_problem*)(uintptr_t)plan->opaque[0];
+    t.blocks = (const uint32_t*)((const uint8_t*)t.descs + plan_desc_bytes(nn));
+    t.m = (int)plan->opaque[2];
+    t.x_dt = (int)(plan->opaque[5] & 0xff);
+    t.y_dt = (int)((plan->opaque[5] >> 16) & 0xff);
+    const int sb_dt = (int)((plan->opaque[5] >> 8) & 0xff);
+    return launch_status(rq::launch_qmv_table(t, (int)nblocks, sb_dt, (int)plan->opaque[3],
+                                              (int)plan->opaque[4], (size_t)plan->opaque[6],
+                                              (hipStream_t)stream),
+                         "rq_grouped_plan_run");
 }
 
 }  // extern "C"

@@ -26,6 +26,22 @@ hipError_t launch_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bit
 hipError_t launch_qmv(const rq_problem* problems, int n, int x_dt, int sb_dt, int y_dt,
                       int64_t m, int gs, int bits, hipStream_t stream);
 
+// Streamed decode GEMV over a device-side schedule (rq_grouped_plan_*).
+struct QmvTable {
+    const rq_problem* descs;  // device: problem descriptors, longest K first
+    const uint32_t* blocks;   // device: per block, problem << 16 | 64-row block of that problem
+    int m, x_dt, y_dt;
+};
+constexpr int kQmvLdsBudget = 64 * 1024;  // LDS bytes a GEMV block may stage
+constexpr int kQmvRowsPerBlock = 64;      // rows of one streamed-GEMV block
+// LDS bytes of a streamed-GEMV block for one problem shape.
+size_t qmv_stream_lds(int64_t m, int64_t cols, int gs);
+// Whether the streamed GEMV covers a problem (16-bit scales, cols % 512 == 0,
+// 16-byte aligned scales/biases, staging within budget).
+bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs);
+hipError_t launch_qmv_table(const QmvTable& t, int blocks, int sb_dt, int gs, int bits,
+                            size_t lds, hipStream_t stream);
+
 // MFMA GEMM, transpose=True: y[m, rows] = x[m, cols] . W^T.
 hipError_t launch_qmm_t(const void* x, int x_dt, const uint32_t* wq, const void* scales,
                         const void* biases, int sb_dt, int64_t m, int64_t rows, int64_t cols,

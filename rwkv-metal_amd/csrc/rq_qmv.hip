@@ -83,6 +83,9 @@ constexpr int kBlock = 64 * kWaves;
 #ifndef RQ_QMV_BIG_RB
 #define RQ_QMV_BIG_RB 1  // 16-row blocks per wave for big launches
 #endif
+#ifndef RQ_QMV_STREAM
+#define RQ_QMV_STREAM 1  // 0: never use the streamed-scale GEMV
+#endif
 #ifndef RQ_QMV_BIG_MIN
 #define RQ_QMV_BIG_MIN 16384  // 16-row blocks in a launch from which RQ_QMV_BIG_RB applies
 #endif
@@ -227,7 +230,7 @@ struct SBPair {
     typedef typename std::conditional<SDT == RQ_F32, uint2, uint32_t>::type type;
 };
 
-constexpr int kLdsBudget = 64 * 1024;  // bytes of LDS staging per block
+constexpr int kLdsBudget = rq::kQmvLdsBudget;  // bytes of LDS staging per block
 
 // SLDS=true (fast path): the block's activations AND its rows' scales/biases
 // are staged in LDS once; the span loop then streams only packed codes, with
@@ -636,6 +639,345 @@ hipError_t launch_cfg(const QmvArgs& a, int sb_dt, int nmc, bool xlds, int block
     return e;
 }
 
+
+// ------------------------------------------------------------ streamed GEMV
+//
+// qmv_stream_*: the decode GEMV for the common layout -- 16-bit scales with
+// 16-byte aligned arrays and K a multiple of 512 -- built around full cache
+// lines and streamed (scale, bias) pairs:
+//
+//  * A "stage" is 256 codes of 16 weight rows.  Lane L takes the two
+//    consecutive runs 2g, 2g+1 (g = L/16) of row L%16: 64 contiguous codes,
+//    so one wave-load covers 16 rows x 128 B, whole cache lines (measured:
+//    +18% streaming rate over 16 rows x 64 B per load).  Stage s+3 is in
+//    flight while stage s is computed.
+//  * Each lane group owns a different k-slice of the MFMA, so the 16 A rows
+//    are split into 4 slots (A row m' carries x[m'%4] on lane group m'/4's
+//    slice only): D row 4g+i sums exactly lane group g's codes, i.e. one
+//    group (two at gs=32: the stage's two MFMA halves are kept apart), and
+//    lane L's accumulator rows need only its own row's (scale, bias) and
+//    the activation sums X of its own group(s).  M > 4 runs ceil(M/4)
+//    passes over the same codes.
+//  * Every 4 stages a wave loads the (scale, bias) values of those stages
+//    for its 16 rows with one vector load per lane (lane groups 0/2 take
+//    scales, 1/3 biases), one iteration ahead, and parks them in its own LDS
+//    window (wave-private, no barrier).
+//  * Only x (pair-permuted bf16) and its sums X over 32-element (gs=32) or
+//    64-element slices -- a lane group's k-slice never spans two groups and
+//    at gs=128 covers half of one -- are staged per block, behind one
+//    barrier.  acc += s * D + (b - 128 s) * X (8-bit: b * X).
+//  * qmv_stream_table reads its problem from a device-side table (one entry
+//    per block: problem << 16 | 64-row block of that problem), so one launch
+//    covers any number of problems; blocks are ordered longest first by the
+//    host.  qmv_stream_inline takes up to RQ_MAX_GROUPED problems in its
+//    arguments.
+constexpr int kZeroElems = 64;  // zero line at the start of LDS: 128 B (8 A fragments)
+
+template <int GSH>
+struct StreamWin {
+    static constexpr int GPS = 256 >> GSH;             // groups per stage: 8, 4, 2
+    static constexpr int GPI = 4 * GPS;                // groups per iteration: 32, 16, 8
+    static constexpr int WB = GPI * 2;                 // bytes per array per row per iteration
+    static constexpr int LB = WB / 2;                  // bytes one lane loads: 32, 16, 8
+    static constexpr int ROWB = GSH == 5 ? 144 : (GSH == 6 ? 80 : 48);  // LDS row stride
+    static constexpr int WAVE_BYTES = 16 * ROWB;
+};
+
+template <int N>
+struct Words {
+    uint32_t w[N];
+};
+
+template <int BITS>
+RQ_DEV void load_two_runs(const uint32_t* p, uint32_t* out) {
+    // 2*BITS contiguous words; 16-byte aligned for even BITS, 8-byte for odd
+    if constexpr ((BITS & 1) == 0) {
+#pragma unroll
+        for (int q = 0; q < BITS / 2; ++q) {
+            const u32x4_t v = ld_code((const u32x4_t*)p + q);
+            out[4 * q] = v[0]; out[4 * q + 1] = v[1]; out[4 * q + 2] = v[2]; out[4 * q + 3] = v[3];
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < BITS; ++q) {
+            const uint2 v = ld_code((const uint2*)p + q);
+            out[2 * q] = v.x; out[2 * q + 1] = v.y;
+        }
+    }
+}
+
+template <int BITS, int SDT, int NMC, int MI, int GSH>
+RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, int y_dt) {
+    static_assert(SDT != RQ_F32, "streamed scales are 16-bit");
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+    typedef StreamWin<GSH> W;
+    constexpr int NS = 4;  // stages per iteration; NS-1 stages of codes in flight
+    typedef typename std::conditional<W::LB == 32, Words<8>,
+            typename std::conditional<W::LB == 16, Words<4>, Words<2>>::type>::type win_t;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lg = lane >> 4, lr = lane & 15;
+    const int64_t R = P.rows, K = P.cols;
+    const int G = (int)(K >> GSH);
+    const int nst = (int)(K >> 8);
+    const int niter = (nst + NS - 1) / NS;
+    const int64_t row0 = (int64_t)lblock * 64 + wave * 16;
+    const int64_t rowc = (row0 + lr) < R ? (row0 + lr) : R - 1;
+    const int64_t wpr = (K >> 5) * BITS;
+
+    // ---- first loads: window 0, then codes of stages 0..NS-2
+    const uint16_t* __restrict__ sbrow =
+        (const uint16_t*)((lg & 1) ? P.biases : P.scales) + rowc * G;
+    const int part = (lg >> 1) * (W::GPI / 2);
+    auto load_win = [&](int it) -> win_t {
+        int g0 = it * W::GPI + part;
+        g0 = g0 < G - W::GPI / 2 ? g0 : G - W::GPI / 2;  // past the last stage: any valid data
+        win_t v;
+        const uint16_t* src = sbrow + g0;
+        if constexpr (W::LB == 32) {
+            const u32x4_t a = *(const u32x4_t*)src, b = *((const u32x4_t*)src + 1);
+            v.w[0] = a[0]; v.w[1] = a[1]; v.w[2] = a[2]; v.w[3] = a[3];
+            v.w[4] = b[0]; v.w[5] = b[1]; v.w[6] = b[2]; v.w[7] = b[3];
+        } else if constexpr (W::LB == 16) {
+            const u32x4_t a = *(const u32x4_t*)src;
+            v.w[0] = a[0]; v.w[1] = a[1]; v.w[2] = a[2]; v.w[3] = a[3];
+        } else {
+            const uint2 a = *(const uint2*)src;
+            v.w[0] = a.x; v.w[1] = a.y;
+        }
+        return v;
+    };
+    const uint32_t* __restrict__ wqr = P.w_q + rowc * wpr + lg * 2 * BITS;
+    auto load_codes = [&](int st, uint32_t* words) {
+        const int sc = st < nst ? st : nst - 1;
+        load_two_runs<BITS>(wqr + sc * (8 * BITS), words);
+    };
+    win_t wv = load_win(0);
+    uint32_t cw[NS][2 * BITS];
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i) {
+        load_codes(i, cw[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- stage x [M][K] (bf16, pair order) and its group sums; zero line
+    uint16_t* xs = lds + kZeroElems;
+    constexpr int XSH = GSH < 6 ? GSH : 6;  // activation sums over 2^XSH elements
+    const int GX = (int)(K >> XSH);
+    const uint32_t xsum_f = (uint32_t)((2 * kZeroElems + (((int64_t)M * K * 2 + 15) & ~15ll)) >> 2);
+    float* xsum = (float*)lds + xsum_f;
+    uint8_t* win = (uint8_t*)(xsum + (((int64_t)M * GX + 3) & ~3ll)) + wave * W::WAVE_BYTES;
+    if (threadIdx.x < kZeroElems / 8) *(u32x4_t*)&lds[threadIdx.x * 8] = u32x4_t{0u, 0u, 0u, 0u};
+    {
+        const void* __restrict__ x = P.x;
+        const int64_t n8 = (int64_t)M * K / 8;
+        for (int64_t e = threadIdx.x; e < n8; e += kBlock) {
+            uint32_t d[4];
+            if (x_dt == RQ_BF16) {
+                const uint4 v = ((const uint4*)x)[e];
+                d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    d[q] = pack_bf16x2(load_dt(x, x_dt, e * 8 + 2 * q),
+                                       load_dt(x, x_dt, e * 8 + 2 * q + 1));
+            }
+            uint32_t pr[4];
+            reorder_pairs(d, pr);
+            *(u32x4_t*)&xs[e * 8] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
+            float sum = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                sum += __uint_as_float(d[q] << 16) + __uint_as_float(d[q] & 0xffff0000u);
+#pragma unroll
+            for (int w = 1; w < (1 << (XSH - 3)); w <<= 1) sum += __shfl_xor(sum, w, 64);
+            if ((e & ((1 << (XSH - 3)) - 1)) == 0) xsum[e >> (XSH - 3)] = sum;
+        }
+    }
+    __syncthreads();
+    if (row0 >= R) return;  // no rows for this wave (after the barrier)
+
+    // ---- per-lane constants
+    const PairConsts kc = pair_consts();
+    // A: lane (lr, lg) supplies row m' = lr on lane group lg's k-slice; that
+    // row carries x[c*4 + lr%4] when its slot lr/4 is lg.
+    uint32_t a_idx[NMC], a_step[NMC];
+#pragma unroll
+    for (int c = 0; c < NMC; ++c) {
+        const int m = c * 4 + (lr & 3);
+        const bool act = (lr >> 2) == lg && m < M;
+        a_idx[c] = act ? (uint32_t)(kZeroElems + (int64_t)m * K + lg * 64) : 0u;
+        a_step[c] = act ? 256u : 0u;
+    }
+    // activation sums of this lane's k-slice for its D rows m = c*4 + i
+    constexpr int GL = GSH == 5 ? 2 : 1;                 // groups per lane per stage
+    const int glane = GSH == 5 ? 2 * lg : (GSH == 6 ? lg : (lg >> 1));
+    const int xlane = GSH == 5 ? 2 * lg : lg;
+    uint32_t g_idx[NMC][MI], g_step[NMC][MI];
+#pragma unroll
+    for (int c = 0; c < NMC; ++c)
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            const int m = c * 4 + i;
+            const bool act = m < M;
+            g_idx[c][i] = act ? xsum_f + (uint32_t)(m * GX + xlane) : 0u;
+            g_step[c][i] = act ? (uint32_t)(256 >> XSH) : 0u;
+        }
+    uint8_t* win_w = win + lr * W::ROWB + (lg & 1) * W::WB + (lg >> 1) * W::LB;
+    const uint8_t* win_r = win + lr * W::ROWB + glane * 2;
+
+    f32x4_t acc[NMC];
+#pragma unroll
+    for (int c = 0; c < NMC; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int it = 0; it < niter; ++it) {
+        // this iteration's (scale, bias) window into LDS, the next one into registers
+        *(win_t*)win_w = wv;  // read below by other lanes of this wave (LDS runs in order)
+        __builtin_amdgcn_wave_barrier();
+        wv = load_win(it + 1);
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            const int st = it * NS + t;
+            load_codes(st + NS - 1, cw[(t + NS - 1) % NS]);
+            if (st < nst) {
+                // scales and biases of this lane's group(s) at this stage
+                float sc[GL], cb[GL];
+#pragma unroll
+                for (int q = 0; q < GL; ++q) {
+                    const uint16_t sr = *(const uint16_t*)(win_r + (t * W::GPS + q) * 2);
+                    const uint16_t br = *(const uint16_t*)(win_r + W::WB + (t * W::GPS + q) * 2);
+                    sc[q] = raw_to_f32<SDT>(sr);
+                    const float bi = raw_to_f32<SDT>(br);
+                    cb[q] = (BITS == 8) ? bi : fmaf(sc[q], -128.f, bi);
+                }
+                f32x4_t d[NMC][2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    bf16x8_t bop[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        uint32_t pr[4];
+                        codes_to_bf16_pairs<BITS>(cw[t] + h * BITS, j, pr, kc);
+                        bop[j] = as_bf16x8(pr[0], pr[1], pr[2], pr[3]);
+                    }
+#pragma unroll
+                    for (int c = 0; c < NMC; ++c) {
+                        const u32x4_t* src =
+                            (const u32x4_t*)&lds[a_idx[c] + (uint32_t)st * a_step[c] + h * 32];
+                        d[c][h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const u32x4_t v = src[j];
+                            d[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                as_bf16x8(v[0], v[1], v[2], v[3]), bop[j], d[c][h], 0, 0, 0);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < NMC; ++c)
+#pragma unroll
+                    for (int i = 0; i < MI; ++i) {
+                        const float* xg = (const float*)lds + g_idx[c][i] + (uint32_t)st * g_step[c][i];
+                        if constexpr (GL == 2) {
+                            acc[c][i] = fmaf(sc[0], d[c][0][i], fmaf(cb[0], xg[0], acc[c][i]));
+                            acc[c][i] = fmaf(sc[1], d[c][1][i], fmaf(cb[1], xg[1], acc[c][i]));
+                        } else {
+                            acc[c][i] = fmaf(sc[0], d[c][0][i] + d[c][1][i],
+                                             fmaf(cb[0], xg[0], acc[c][i]));
+                        }
+                    }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // sum the four slots (lane groups), then lane group 0 stores rows < R
+    const int64_t row = row0 + lr;
+#pragma unroll
+    for (int c = 0; c < NMC; ++c)
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            float v = acc[c][i];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            const int m = c * 4 + i;
+            if (lg == 0 && m < M && row < R) store_dt(P.y, y_dt, (int64_t)m * R + row, v);
+        }
+}
+
+template <int BITS, int SDT, int NMC, int MI, int GSH>
+__global__ __launch_bounds__(kBlock) void qmv_stream_inline(const QmvArgs args) {
+    const int bid = blockIdx.x;
+    int lo = 0, hi = args.n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (args.block_start[mid] <= bid) lo = mid; else hi = mid - 1;
+    }
+    qmv_stream_body<BITS, SDT, NMC, MI, GSH>(args.p[lo], bid - args.block_start[lo], args.m,
+                                             args.x_dt, args.y_dt);
+}
+
+template <int BITS, int SDT, int NMC, int MI, int GSH>
+__global__ __launch_bounds__(kBlock) void qmv_stream_table(const rq::QmvTable a) {
+    const uint32_t e = a.blocks[blockIdx.x];
+    const rq_problem P = a.descs[e >> 16];
+    qmv_stream_body<BITS, SDT, NMC, MI, GSH>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
+}
+
+// Template dispatch shared by both launch forms: F is called with
+// integral_constant-typed (SDT, NMC, MI, GSH).
+template <typename F>
+hipError_t stream_dispatch(int sb_dt, int64_t m, int gs, F&& f) {
+    const int gsh = __builtin_ctz(gs);
+    int nmc = (int)((m + 3) / 4);  // four activation rows per pass
+    nmc = nmc <= 1 ? 1 : (nmc <= 2 ? 2 : 4);
+    const int mi = nmc > 1 ? 4 : (m >= 3 ? 4 : (int)m);
+    typedef std::integral_constant<int, RQ_BF16> BF;
+    typedef std::integral_constant<int, RQ_F16> FH;
+#define RQ_S_GSH(SD, N, I)                                                                        \
+    switch (gsh) {                                                                                \
+        case 5: return f(SD(), std::integral_constant<int, N>(), std::integral_constant<int, I>(), \
+                         std::integral_constant<int, 5>());                                       \
+        case 6: return f(SD(), std::integral_constant<int, N>(), std::integral_constant<int, I>(), \
+                         std::integral_constant<int, 6>());                                       \
+        case 7: return f(SD(), std::integral_constant<int, N>(), std::integral_constant<int, I>(), \
+                         std::integral_constant<int, 7>());                                       \
+        default: return hipErrorInvalidValue;                                                     \
+    }
+#define RQ_S_NMI(SD)                                 \
+    switch (nmc * 8 + mi) {                          \
+        case 9: RQ_S_GSH(SD, 1, 1)                   \
+        case 10: RQ_S_GSH(SD, 1, 2)                  \
+        case 12: RQ_S_GSH(SD, 1, 4)                  \
+        case 20: RQ_S_GSH(SD, 2, 4)                  \
+        case 36: RQ_S_GSH(SD, 4, 4)                  \
+        default: return hipErrorInvalidValue;        \
+    }
+    if (sb_dt == RQ_BF16) { RQ_S_NMI(BF) }
+    RQ_S_NMI(FH)
+#undef RQ_S_NMI
+#undef RQ_S_GSH
+}
+
+hipError_t launch_stream_inline(const QmvArgs& a, int blocks, int sb_dt, int gs, size_t lds,
+                                hipStream_t stream) {
+    return stream_dispatch(sb_dt, a.m, gs, [&](auto sd, auto nmc, auto mi, auto gsh) {
+        hipLaunchKernelGGL((qmv_stream_inline<RQ_BITS, decltype(sd)::value, decltype(nmc)::value,
+                                              decltype(mi)::value, decltype(gsh)::value>),
+                           dim3(blocks), dim3(kBlock), lds, stream, a);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_stream_table(const rq::QmvTable& a, int blocks, int sb_dt, int gs, size_t lds,
+                               hipStream_t stream) {
+    return stream_dispatch(sb_dt, a.m, gs, [&](auto sd, auto nmc, auto mi, auto gsh) {
+        hipLaunchKernelGGL((qmv_stream_table<RQ_BITS, decltype(sd)::value, decltype(nmc)::value,
+                                             decltype(mi)::value, decltype(gsh)::value>),
+                           dim3(blocks), dim3(kBlock), lds, stream, a);
+        return hipGetLastError();
+    });
+}
 }  // namespace
 
 namespace rq {
@@ -660,6 +1002,32 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
     int64_t rowblocks = 0;
     for (int i = 0; i < n; ++i) rowblocks += (probs[i]->rows + 15) / 16;
     const int cfg = rowblocks >= RQ_QMV_BIG_MIN ? 2 : (rowblocks >= 2048 ? 1 : 0);
+    bool streamed = cfg >= 1 && RQ_QMV_STREAM;
+    for (int i = 0; i < n && streamed; ++i) streamed = qmv_stream_covers(*probs[i], sb_dt, m, gs);
+    if (streamed) {
+        const size_t lds = qmv_stream_lds(m, K, gs);
+        for (int base = 0; base < n; base += RQ_MAX_GROUPED) {
+            const int cnt = (n - base) < RQ_MAX_GROUPED ? (n - base) : RQ_MAX_GROUPED;
+            QmvArgs a;
+            std::memset(&a, 0, sizeof(a));
+            int64_t blocks = 0;
+            for (int i = 0; i < cnt; ++i) {
+                a.p[i] = *probs[base + i];
+                a.block_start[i] = (int)blocks;
+                blocks += (probs[base + i]->rows + kQmvRowsPerBlock - 1) / kQmvRowsPerBlock;
+            }
+            a.block_start[cnt] = (int)blocks;
+            a.n = cnt;
+            a.m = (int)m;
+            a.gs_shift = gs_shift;
+            a.x_dt = x_dt;
+            a.y_dt = y_dt;
+            if (blocks == 0) continue;
+            hipError_t e = launch_stream_inline(a, (int)blocks, sb_dt, gs, lds, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     const int RB = cfg == 2 ? RQ_QMV_BIG_RB : 1;
     const int rows_per_block = cfg == 0 ? 16 * RB : 16 * RB * kWaves;
     // LDS staging: a zero line, activations [m][K] as bf16, their group sums
@@ -698,6 +1066,26 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+#if RQ_BITS == 4  // bit-width independent helpers: defined in one unit only
+size_t qmv_stream_lds(int64_t m, int64_t cols, int gs) {
+    const int wave_bytes = gs == 32 ? StreamWin<5>::WAVE_BYTES
+                         : (gs == 64 ? StreamWin<6>::WAVE_BYTES : StreamWin<7>::WAVE_BYTES);
+    const int xg = gs < 64 ? gs : 64;  // elements per activation sum
+    return 2 * kZeroElems + (((size_t)m * cols * 2 + 15) & ~(size_t)15) +
+           (((size_t)m * (cols / xg) * 4 + 15) & ~(size_t)15) + 4 * (size_t)wave_bytes;
+}
+bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs) {
+    return sb_dt != RQ_F32 && p.cols % 512 == 0 && p.rows <= (int64_t)65536 * kQmvRowsPerBlock &&
+           (((uintptr_t)p.scales | (uintptr_t)p.biases) & 15) == 0 &&
+           qmv_stream_lds(m, p.cols, gs) <= (size_t)kQmvLdsBudget;
+}
+#endif
+
+hipError_t RQ_CAT(launch_qmv_table_b, RQ_BITS)(const QmvTable& t, int blocks, int sb_dt, int gs,
+                                               size_t lds, hipStream_t stream) {
+    return launch_stream_table(t, blocks, sb_dt, gs, lds, stream);
 }
 
 hipError_t RQ_CAT(launch_qmv_b, RQ_BITS)(const rq_problem* problems, int n, int x_dt, int sb_dt,

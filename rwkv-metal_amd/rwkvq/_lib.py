@@ -38,6 +38,12 @@ class RqProblem(ctypes.Structure):
     ]
 
 
+class RqGroupedPlan(ctypes.Structure):
+    """Mirror of rq_grouped_plan."""
+
+    _fields_ = [("opaque", _i64 * 8)]
+
+
 SIGNATURES = {
     "rq_abi_version": ([], _i32),
     "rq_last_error": ([], ctypes.c_char_p),
@@ -49,7 +55,12 @@ SIGNATURES = {
     "rq_unpack": ([_vp, _i64, _i64, _i32, _vp, _vp], _i32),
     "rq_qmm_grouped": ([ctypes.POINTER(RqProblem), _i32, _i32, _i32, _i32, _i64, _i32, _i32, _vp],
                        _i32),
+    "rq_grouped_plan_table_bytes": ([ctypes.POINTER(RqProblem), _i32], _i64),
+    "rq_grouped_plan_init": ([ctypes.POINTER(RqProblem), _i32, _i32, _i32, _i32, _i64, _i32, _i32,
+                              _vp, _i64, ctypes.POINTER(RqGroupedPlan), _vp], _i32),
+    "rq_grouped_plan_run": ([ctypes.POINTER(RqGroupedPlan), _vp], _i32),
 }
+RQ_EUNSUPPORTED = -4
 
 ABI_VERSION = 1
 MAX_GROUPED = 48

@@ -28,7 +28,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
-from ._lib import DTYPE_CODE, RqProblem, check, lib
+from ._lib import DTYPE_CODE, RQ_EUNSUPPORTED, RqGroupedPlan, RqProblem, check, lib
 
 VALID_BITS = (2, 3, 4, 5, 6, 8)
 VALID_GROUP_SIZES = (32, 64, 128)
@@ -238,8 +238,9 @@ def quantized_matmul(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor,
 
 class GroupedQmv:
     """A validated set of independent decode products y_i = x_i @ W_i^T
-    (m <= 16) run by rq_qmm_grouped: one ctypes call per run(), as few kernel
-    launches as the C ABI allows.  All x_i share m and dtype; all W_i share
+    (m <= 16): one ctypes call and, where the planned kernel covers the
+    problems (rq_grouped_plan_*), one kernel launch per run(); otherwise
+    rq_qmm_grouped's launches.  All x_i share m and dtype; all W_i share
     bits, group size and the scales dtype.  The plan keeps references to every
     tensor, so run() may be called repeatedly (e.g. one decode step each)."""
 
@@ -279,11 +280,31 @@ class GroupedQmv:
         self.n, self.m, self.device = len(xs), m, x0.device
         self.codes = (DTYPE_CODE[x0.dtype], DTYPE_CODE[sdt], DTYPE_CODE[ydt])
         self.group_size, self.bits = group_size, bits
+        # A device-side schedule (one launch per run) where the planned kernel
+        # covers every problem; otherwise the host-array entry point.
+        self.plan, self._table = None, None
+        L = lib()
+        nbytes = L.rq_grouped_plan_table_bytes(self.probs, self.n)
+        check(nbytes if nbytes < 0 else 0, "grouped_qmv plan")
+        table = torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=self.device)
+        plan = RqGroupedPlan()
+        with torch.cuda.device(self.device):
+            rc = L.rq_grouped_plan_init(self.probs, self.n, *self.codes, self.m, group_size, bits,
+                                        table.data_ptr(), table.numel(), ctypes.byref(plan),
+                                        torch.cuda.current_stream(self.device).cuda_stream)
+        if rc == RQ_EUNSUPPORTED:
+            return
+        check(rc, "grouped_qmv plan")
+        self.plan, self._table = plan, table
 
     def run(self) -> List[Tensor]:
         with torch.cuda.device(self.device):
-            rc = lib().rq_qmm_grouped(self.probs, self.n, *self.codes, self.m, self.group_size,
-                                      self.bits, torch.cuda.current_stream(self.device).cuda_stream)
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            if self.plan is not None:
+                rc = lib().rq_grouped_plan_run(ctypes.byref(self.plan), stream)
+            else:
+                rc = lib().rq_qmm_grouped(self.probs, self.n, *self.codes, self.m,
+                                          self.group_size, self.bits, stream)
         check(rc, "grouped_qmv")
         return self.outs
 

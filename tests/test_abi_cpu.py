@@ -26,7 +26,8 @@ def L():
 def test_header_declares_the_expected_surface():
     assert declared_functions() == sorted([
         "rq_abi_version", "rq_last_error", "rq_quantize", "rq_dequantize", "rq_qmm",
-        "rq_pack", "rq_unpack", "rq_qmm_grouped"])
+        "rq_pack", "rq_unpack", "rq_qmm_grouped", "rq_grouped_plan_table_bytes",
+        "rq_grouped_plan_init", "rq_grouped_plan_run"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -75,3 +76,46 @@ def test_grouped_rejects_large_m(L):
     probs = (RqProblem * 1)()
     assert L.rq_qmm_grouped(probs, 1, 0, 0, 0, 17, 64, 4, None) == -1
     assert "m must be" in _err(L)
+
+
+def _problems(shapes, sb_align=0):
+    from rwkvq._lib import RqProblem
+    probs = (RqProblem * len(shapes))()
+    for i, (R, K) in enumerate(shapes):
+        probs[i] = RqProblem(0x1000, 0x2000, 0x3000 + sb_align, 0x4000, 0x5000, R, K)
+    return probs
+
+
+def test_plan_table_bytes(L):
+    # descriptors (56 B each, padded to 16) + one uint32 per 64-row block
+    probs = _problems([(2048, 2048), (65536, 2048), (100, 512)])
+    assert L.rq_grouped_plan_table_bytes(probs, 3) == 176 + 4 * (32 + 1024 + 2)
+
+
+def test_plan_rejections_before_any_device_work(L):
+    from ctypes import byref
+    from rwkvq._lib import RQ_EUNSUPPORTED, RqGroupedPlan
+    plan = RqGroupedPlan()
+    probs = _problems([(2048, 2048)])
+    # fp32 scales are outside the planned kernel
+    assert L.rq_grouped_plan_init(probs, 1, 0, 2, 2, 1, 64, 4, 0x10000, 1 << 20, byref(plan),
+                                  None) == RQ_EUNSUPPORTED
+    assert "rq_qmm_grouped" in _err(L)
+    # cols not a multiple of 512
+    probs = _problems([(2048, 768)])
+    assert L.rq_grouped_plan_init(probs, 1, 0, 0, 0, 1, 64, 4, 0x10000, 1 << 20, byref(plan),
+                                  None) == RQ_EUNSUPPORTED
+    # misaligned scales
+    probs = _problems([(2048, 2048)], sb_align=2)
+    assert L.rq_grouped_plan_init(probs, 1, 0, 0, 0, 1, 64, 4, 0x10000, 1 << 20, byref(plan),
+                                  None) == RQ_EUNSUPPORTED
+    # table too small
+    probs = _problems([(2048, 2048)])
+    assert L.rq_grouped_plan_init(probs, 1, 0, 0, 0, 1, 64, 4, 0x10000, 16, byref(plan),
+                                  None) == -1
+    assert "needs" in _err(L)
+    # a plan that was never initialised does not run
+    assert L.rq_grouped_plan_run(byref(RqGroupedPlan()), None) == -1
+    # an empty set is a valid plan whose run is a no-op
+    assert L.rq_grouped_plan_init(None, 0, 0, 0, 0, 1, 64, 4, None, 0, byref(plan), None) == 0
+    assert L.rq_grouped_plan_run(byref(plan), None) == 0

@@ -5,7 +5,10 @@ Bar: quantize codes/words, scales and biases bit-exact; pack/unpack
 bit-exact; dequantize bit-exact to the oracle's MLX arithmetic (multiply and
 add each rounded in the scales dtype); quantized_matmul within rel-err 1e-2
 (bf16 operands, fp32 accumulation) -- Frobenius-relative and elementwise
-against the largest reference magnitude.
+against the largest reference magnitude -- of the oracle's product with the
+weights s*q + b unrounded (weights="exact", the form of MLX's qmv).  The
+oracle's other form, with dequantize()'s bf16-rounded weights, sits up to ~1%
+from it on N(0, 0.02) weights (tests/test_oracle.py pins both).
 """
 import pytest
 import torch
@@ -133,7 +136,7 @@ def test_qmv_parity_bf16(O, rq, dev, bits, gs, M):
     x = acts(M, K, M + bits)
     say(f"qmv bits={bits} gs={gs} M={M}")
     y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
-    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32)
+    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
     assert y.dtype == torch.bfloat16
     rel_check(y, ref, what=f"qmv b{bits} g{gs} M{M}")
 
@@ -153,7 +156,7 @@ def test_qmv_parity_dtypes(O, rq, dev, bits, gs, xdt, sdt):
     y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
     want = xdt if xdt == sdt else torch.float32
     assert y.dtype == want
-    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32)
+    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
     rel_check(y, ref, what="qmv dtypes")
 
 
@@ -166,7 +169,7 @@ def test_qmv_edge_shapes(O, rq, dev):
         x = acts(M, K, R)
         say(f"qmv edge R={R} K={K} gs={gs} bits={bits} M={M}")
         y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
-        ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32)
+        ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
         rel_check(y, ref, what=f"edge {R}x{K}")
 
 
@@ -182,7 +185,7 @@ def test_qmm_t_parity(O, rq, dev, bits, gs, M):
     x = acts(M, K, M)
     say(f"qmm_t bits={bits} gs={gs} M={M}")
     y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
-    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32)
+    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
     rel_check(y, ref, what=f"qmm_t b{bits} g{gs} M{M}")
 
 
@@ -197,7 +200,7 @@ def test_qmm_n_parity(O, rq, dev, bits, gs, M):
     dy = acts(M, R, M + 1)
     say(f"qmm_n bits={bits} gs={gs} M={M}")
     y = rq.quantized_matmul(dy.to(dev), wq.to(dev), s.to(dev), b.to(dev), False, gs, bits)
-    ref = O.quantized_matmul(dy, wq, s, b, False, gs, bits, out_dtype=torch.float32)
+    ref = O.quantized_matmul(dy, wq, s, b, False, gs, bits, out_dtype=torch.float32, weights="exact")
     rel_check(y, ref, what=f"qmm_n b{bits} g{gs} M{M}")
 
 
@@ -211,7 +214,7 @@ def test_qmm_n_unaligned_rows(O, rq, dev, R):
         dy = acts(45, R, R, xdt)
         say(f"qmm_n unaligned R={R} x={xdt}")
         y = rq.quantized_matmul(dy.to(dev), wq.to(dev), s.to(dev), b.to(dev), False, gs, bits)
-        ref = O.quantized_matmul(dy, wq, s, b, False, gs, bits, out_dtype=torch.float32)
+        ref = O.quantized_matmul(dy, wq, s, b, False, gs, bits, out_dtype=torch.float32, weights="exact")
         rel_check(y, ref, what=f"qmm_n R{R}")
 
 
@@ -223,7 +226,7 @@ def test_qmm_t_other_dtypes(O, rq, dev, xdt):
     x = acts(M, K, 2, xdt)
     say(f"qmm_t x={xdt}")
     y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
-    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32)
+    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
     rel_check(y, ref, what="qmm_t dtypes")
 
 
@@ -241,7 +244,7 @@ def test_config1_roundtrip_and_matmul(O, rq, dev, M):
     assert torch.equal(rq.unpack_codes(wq, 4).cpu(), O.unpack(owq, 4))
     assert bits_equal(rq.dequantize(wq, s, b, 64, 4), O.dequantize(owq, os_, ob, 64, 4))
     y = rq.quantized_matmul(x.to(dev), wq, s, b, True, 64, 4)
-    rel_check(y, O.quantized_matmul(x, owq, os_, ob, True, 64, 4, out_dtype=torch.float32))
+    rel_check(y, O.quantized_matmul(x, owq, os_, ob, True, 64, 4, out_dtype=torch.float32, weights="exact"))
 
 
 CONFIG2 = {"r": (2048, 2048), "ffn_key": (8192, 2048), "ffn_value": (2048, 8192),
@@ -257,12 +260,16 @@ def test_config2_decode_shapes(O, rq, dev, name, M):
     x = acts(M, K, 2_000_000 + 6)
     say(f"config2 {name} M={M}")
     y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
-    ref = O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32)
+    ref = O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32, weights="exact")
     rel_check(y, ref, what=f"config2 {name}")
 
 
 def _gpu_dense_ref(rq, x, wq, s, b, gs, bits, transpose):
-    wd = rq.dequantize(wq, s, b, gs, bits).float()   # bit-exact to the oracle (tested above)
+    """fp32 dense product with the weights s*q + b from the (bit-exact)
+    unpacked codes -- the oracle's weights="exact" form, at sizes the CPU
+    oracle is too slow for."""
+    q = rq.unpack_codes(wq, bits).float()
+    wd = q * s.float().repeat_interleave(gs, 1) + b.float().repeat_interleave(gs, 1)
     return x.float() @ (wd.t() if transpose else wd)
 
 
@@ -288,7 +295,7 @@ def test_config3_oracle_small_m(O, rq, dev):
     x = acts(M, K, 3_000_512)
     say("config3 oracle M=512")
     y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
-    rel_check(y, O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32))
+    rel_check(y, O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32, weights="exact"))
 
 
 @pytest.mark.parametrize("shape", [(2048, 2048), (8192, 2048), (2048, 8192)])
@@ -316,7 +323,7 @@ def test_config5_mixed_bits(O, rq, dev, name, R, K, bits):
     assert torch.equal(gq.cpu(), wq) and bits_equal(gs_, s) and bits_equal(gb, b)
     x1 = acts(1, K, 5_000_500)
     y1 = rq.quantized_matmul(x1.to(dev), gq, gs_, gb, True, 64, bits)
-    rel_check(y1, O.quantized_matmul(x1, wq, s, b, True, 64, bits, out_dtype=torch.float32))
+    rel_check(y1, O.quantized_matmul(x1, wq, s, b, True, 64, bits, out_dtype=torch.float32, weights="exact"))
     x = acts(2048, K, 5_000_501).to(dev)
     y = rq.quantized_matmul(x, gq, gs_, gb, True, 64, bits)
     rel_check(y, _gpu_dense_ref(rq, x, gq, gs_, gb, 64, bits, True), what=f"config5 {name}")
@@ -333,7 +340,7 @@ def test_grouped_matches_single_calls(O, rq, dev):
         x = acts(8, K, 60 + i)
         xs.append(x.to(dev))
         ws.append((wq.to(dev), s.to(dev), b.to(dev)))
-        refs.append(O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32))
+        refs.append(O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32, weights="exact"))
     say("grouped qmv")
     ys = rq.grouped_qmv(xs, ws, 64, 4)
     for y, ref, x, (wq, s, b) in zip(ys, refs, xs, ws):
@@ -351,10 +358,80 @@ def test_grouped_more_problems_than_one_launch(O, rq, dev):
         x = acts(1, 256, 900 + i)
         xs.append(x.to(dev))
         ws.append((wq.to(dev), s.to(dev), b.to(dev)))
-        refs.append(O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32))
+        refs.append(O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32, weights="exact"))
     say("grouped qmv, 70 problems")
     for y, ref in zip(rq.grouped_qmv(xs, ws, 64, 4), refs):
         rel_check(y, ref, what="grouped70")
+
+
+# ------------------------------------------- planned (one-launch) grouped GEMV
+
+PLAN_SHAPES = [(100, 512), (64, 1024), (17, 2048)]
+
+
+def _planned(O, rq, dev, shapes, M, gs, bits, seed, xdt=torch.bfloat16, sdt=torch.bfloat16):
+    xs, ws, refs = [], [], []
+    for i, (R, K) in enumerate(shapes):
+        w = weights(R, K, seed + i, sdt)
+        wq, s, b = O.quantize(w, gs, bits)
+        x = acts(M, K, seed + i, xdt)
+        xs.append(x.to(dev))
+        ws.append((wq.to(dev), s.to(dev), b.to(dev)))
+        refs.append(O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact"))
+    plan = rq.GroupedQmv(xs, ws, gs, bits)
+    assert plan.plan is not None, "expected the planned kernel to cover these problems"
+    return plan, refs, xs, ws
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 8, 16])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_planned_qmv_parity(O, rq, dev, bits, gs, M):
+    say(f"planned qmv bits={bits} gs={gs} M={M}")
+    # activations are staged whole: M*K*2 bytes must stay within the 64 KB budget
+    shapes = [(R, K) for R, K in PLAN_SHAPES if M * K * 2 <= 48 * 1024]
+    plan, refs, _, _ = _planned(O, rq, dev, shapes, M, gs, bits, 5000 + 10 * bits + gs)
+    for y, ref in zip(plan.run(), refs):
+        rel_check(y, ref, what=f"planned b{bits} g{gs} M{M}")
+
+
+@pytest.mark.parametrize("xdt,sdt", [(torch.float32, torch.bfloat16), (torch.float16, torch.float16),
+                                     (torch.bfloat16, torch.float16)])
+def test_planned_qmv_dtypes(O, rq, dev, xdt, sdt):
+    say(f"planned qmv x={xdt} s={sdt}")
+    plan, refs, _, _ = _planned(O, rq, dev, PLAN_SHAPES, 5, 64, 4, 5900, xdt, sdt)
+    for y, ref in zip(plan.run(), refs):
+        rel_check(y, ref, what=f"planned {xdt} {sdt}")
+
+
+def test_planned_many_problems_one_launch(O, rq, dev):
+    """150 problems of three contraction sizes (> RQ_MAX_GROUPED): one launch,
+    blocks ordered longest first; run twice with new activations in place."""
+    shapes = [(64 + 16 * (i % 5), (512, 1024, 2048)[i % 3]) for i in range(150)]
+    say("planned qmv, 150 problems")
+    plan, refs, xs, ws = _planned(O, rq, dev, shapes, 1, 64, 4, 6000)
+    for y, ref in zip(plan.run(), refs):
+        rel_check(y, ref, what="planned150")
+    # new activations in the same buffers, same plan
+    for i, x in enumerate(xs):
+        x.copy_(acts(1, x.shape[-1], 7000 + i).to(dev))
+    for i, y in enumerate(plan.run()):
+        wq, s, b = (t.cpu() for t in ws[i])
+        ref = O.quantized_matmul(xs[i].cpu(), wq, s, b, True, 64, 4, out_dtype=torch.float32, weights="exact")
+        rel_check(y, ref, what=f"planned150 rerun {i}")
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_streamed_single_launch_path(O, rq, dev, M):
+    """A single problem big enough (>= 2048 16-row blocks) for the streamed
+    kernel through rq_qmm itself."""
+    R, K = 32768 + 40, 1024
+    w = weights(R, K, 8100)
+    wq, s, b = O.quantize(w, 64, 4)
+    x = acts(M, K, 8100)
+    say(f"streamed single M={M}")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
+    rel_check(y, O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32, weights="exact"))
 
 
 # ---------------------------------------------- autograd / modules / LoRA
@@ -368,7 +445,7 @@ def test_autograd_dx_is_transposed_qmm(O, rq, dev):
     y = rq.quantized_matmul(x, wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
     g = acts(M, R, 45)
     y.backward(g.to(dev))
-    ref = O.quantized_matmul(g, wq, s, b, False, 64, 4, out_dtype=torch.float32)
+    ref = O.quantized_matmul(g, wq, s, b, False, 64, 4, out_dtype=torch.float32, weights="exact")
     rel_check(x.grad, ref, what="dX")
 
 
@@ -447,12 +524,12 @@ def test_empty_and_unaligned_inputs(O, rq, dev):
     x = big[:, 1:]                      # storage offset 1 element: not 16-byte aligned
     y = rq.quantized_matmul(x, wq, s, b, True, 64, 4)
     ref = O.quantized_matmul(x.cpu().contiguous(), wq.cpu(), s.cpu(), b.cpu(), True, 64, 4,
-                             out_dtype=torch.float32)
+                             out_dtype=torch.float32, weights="exact")
     rel_check(y, ref, what="unaligned x")
     xt = acts(256, 3, 4).to(dev).t()    # non-contiguous view
     y = rq.quantized_matmul(xt, wq, s, b, True, 64, 4)
     ref = O.quantized_matmul(xt.cpu().contiguous(), wq.cpu(), s.cpu(), b.cpu(), True, 64, 4,
-                             out_dtype=torch.float32)
+                             out_dtype=torch.float32, weights="exact")
     rel_check(y, ref, what="transposed view x")
 
 

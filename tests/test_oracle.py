@@ -186,6 +186,30 @@ def test_qmm_matches_dense_float64(O, transpose, bits, gs):
     assert torch.allclose(y.double(), ref, rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("transpose", [True, False])
+@pytest.mark.parametrize("bits", [3, 4, 8])
+def test_qmm_exact_weights_match_dense_float64(O, transpose, bits):
+    """weights="exact": s*q + b from the unpacked codes (torch.bitwise
+    extraction below, independent of the C code) in float64."""
+    g = torch.Generator().manual_seed(300 + bits)
+    R, K, M, gs = 40, 256, 3, 64
+    w = (torch.randn(R, K, generator=g) * 0.02).to(torch.bfloat16)
+    wq, s, b = O.quantize(w, gs, bits)
+    words = wq.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    bitstream = [sum(int(words[r, i]) << (32 * i) for i in range(words.shape[1])) for r in range(R)]
+    codes = torch.tensor([[(row >> (k * bits)) & ((1 << bits) - 1) for k in range(K)]
+                          for row in bitstream], dtype=torch.float64)
+    we = codes * s.double().repeat_interleave(gs, 1) + b.double().repeat_interleave(gs, 1)
+    x = torch.randn(M, K if transpose else R, generator=g).to(torch.bfloat16)
+    y = O.quantized_matmul(x, wq, s, b, transpose, gs, bits, out_dtype=torch.float32,
+                           weights="exact")
+    ref = x.double() @ (we.t() if transpose else we)
+    assert torch.allclose(y.double(), ref, rtol=1e-6, atol=1e-6)
+    # the two weight forms differ only by the bf16 rounding of s*q and +b
+    ym = O.quantized_matmul(x, wq, s, b, transpose, gs, bits, out_dtype=torch.float32).double()
+    assert ((ym - ref).norm() / ref.norm()).item() < 1.5e-2
+
+
 def test_qmm_tiny_python_loop(O):
     g = torch.Generator().manual_seed(5)
     R, K, M, gs, bits = 3, 64, 2, 32, 4
