@@ -688,20 +688,29 @@ struct Words {
     uint32_t w[N];
 };
 
+// Pointers into global memory.  The problem descriptors of a table launch
+// are loaded from memory, so without the address space the compiler emits
+// FLAT loads, which also count as LDS operations: every wait for an LDS
+// read would then wait for all code loads in flight.
+#define RQ_GLOBAL __attribute__((address_space(1)))
+typedef const RQ_GLOBAL uint32_t* gptr_u32;
+typedef const RQ_GLOBAL uint16_t* gptr_u16;
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
 template <int BITS>
-RQ_DEV void load_two_runs(const uint32_t* p, uint32_t* out) {
+RQ_DEV void load_two_runs(gptr_u32 p, uint32_t* out) {
     // 2*BITS contiguous words; 16-byte aligned for even BITS, 8-byte for odd
     if constexpr ((BITS & 1) == 0) {
 #pragma unroll
         for (int q = 0; q < BITS / 2; ++q) {
-            const u32x4_t v = ld_code((const u32x4_t*)p + q);
+            const u32x4_t v = *((const RQ_GLOBAL u32x4_t*)p + q);
             out[4 * q] = v[0]; out[4 * q + 1] = v[1]; out[4 * q + 2] = v[2]; out[4 * q + 3] = v[3];
         }
     } else {
 #pragma unroll
         for (int q = 0; q < BITS; ++q) {
-            const uint2 v = ld_code((const uint2*)p + q);
-            out[2 * q] = v.x; out[2 * q + 1] = v.y;
+            const u32x2_t v = *((const RQ_GLOBAL u32x2_t*)p + q);
+            out[2 * q] = v[0]; out[2 * q + 1] = v[1];
         }
     }
 }
@@ -726,28 +735,27 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
     const int64_t wpr = (K >> 5) * BITS;
 
     // ---- first loads: window 0, then codes of stages 0..NS-2
-    const uint16_t* __restrict__ sbrow =
-        (const uint16_t*)((lg & 1) ? P.biases : P.scales) + rowc * G;
+    const gptr_u16 sbrow = (gptr_u16)((lg & 1) ? P.biases : P.scales) + rowc * G;
     const int part = (lg >> 1) * (W::GPI / 2);
     auto load_win = [&](int it) -> win_t {
         int g0 = it * W::GPI + part;
         g0 = g0 < G - W::GPI / 2 ? g0 : G - W::GPI / 2;  // past the last stage: any valid data
         win_t v;
-        const uint16_t* src = sbrow + g0;
+        const gptr_u16 src = sbrow + g0;
         if constexpr (W::LB == 32) {
-            const u32x4_t a = *(const u32x4_t*)src, b = *((const u32x4_t*)src + 1);
+            const u32x4_t a = *(const RQ_GLOBAL u32x4_t*)src, b = *((const RQ_GLOBAL u32x4_t*)src + 1);
             v.w[0] = a[0]; v.w[1] = a[1]; v.w[2] = a[2]; v.w[3] = a[3];
             v.w[4] = b[0]; v.w[5] = b[1]; v.w[6] = b[2]; v.w[7] = b[3];
         } else if constexpr (W::LB == 16) {
-            const u32x4_t a = *(const u32x4_t*)src;
+            const u32x4_t a = *(const RQ_GLOBAL u32x4_t*)src;
             v.w[0] = a[0]; v.w[1] = a[1]; v.w[2] = a[2]; v.w[3] = a[3];
         } else {
-            const uint2 a = *(const uint2*)src;
-            v.w[0] = a.x; v.w[1] = a.y;
+            const u32x2_t a = *(const RQ_GLOBAL u32x2_t*)src;
+            v.w[0] = a[0]; v.w[1] = a[1];
         }
         return v;
     };
-    const uint32_t* __restrict__ wqr = P.w_q + rowc * wpr + lg * 2 * BITS;
+    const gptr_u32 wqr = (gptr_u32)P.w_q + rowc * wpr + lg * 2 * BITS;
     auto load_codes = [&](int st, uint32_t* words) {
         const int sc = st < nst ? st : nst - 1;
         load_two_runs<BITS>(wqr + sc * (8 * BITS), words);
@@ -774,13 +782,19 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
         for (int64_t e = threadIdx.x; e < n8; e += kBlock) {
             uint32_t d[4];
             if (x_dt == RQ_BF16) {
-                const uint4 v = ((const uint4*)x)[e];
-                d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+                const u32x4_t v = ((const RQ_GLOBAL u32x4_t*)x)[e];
+                d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+            } else if (x_dt == RQ_F32) {
+                const RQ_GLOBAL f32x4_t* xf = (const RQ_GLOBAL f32x4_t*)x + 2 * e;
+                const f32x4_t lo = xf[0], hi = xf[1];
+                d[0] = pack_bf16x2(lo[0], lo[1]); d[1] = pack_bf16x2(lo[2], lo[3]);
+                d[2] = pack_bf16x2(hi[0], hi[1]); d[3] = pack_bf16x2(hi[2], hi[3]);
             } else {
+                const u32x4_t v = ((const RQ_GLOBAL u32x4_t*)x)[e];
+                const uint32_t h[4] = {v[0], v[1], v[2], v[3]};
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
-                    d[q] = pack_bf16x2(load_dt(x, x_dt, e * 8 + 2 * q),
-                                       load_dt(x, x_dt, e * 8 + 2 * q + 1));
+                    d[q] = pack_bf16x2(f16_bits_to_f32(h[q] & 0xffffu), f16_bits_to_f32(h[q] >> 16));
             }
             uint32_t pr[4];
             reorder_pairs(d, pr);
