@@ -131,9 +131,11 @@ int rq_qmm_grouped(const rq_problem* problems, int n, rq_dtype x_dt, rq_dtype sb
  * rq_grouped_plan_init: validates, orders the problems longest contraction
  *   first, uploads the table to `table` and SYNCHRONISES `stream` (the host
  *   staging copy does not outlive the call).  Returns RQ_EUNSUPPORTED for
- *   problems outside the planned kernel (scales must be 16-bit and 16-byte
- *   aligned, cols % 512 == 0, m*cols*2 bytes of activations within the LDS
- *   budget); rq_qmm_grouped covers those.
+ *   problems outside the planned kernel (m <= 4; scales must be 16-bit and
+ *   16-byte aligned, cols % 512 == 0, m*cols*2 bytes of activations within
+ *   the LDS budget); rq_qmm_grouped covers those.  Small sets (fewer than
+ *   about 1024 blocks of 64 rows) run faster on rq_qmm_grouped, which splits
+ *   them along K. 
  * rq_grouped_plan_run: one launch on `stream`.  The table and every pointer
  *   of the problems must stay valid for as long as the plan is run. */
 typedef struct {

@@ -265,7 +265,7 @@ int rq_grouped_plan_init(const rq_problem* problems, int n, rq_dtype x_dt, rq_dt
         if (!rq::qmv_stream_covers(problems[i], sb_dt, m, group_size))
             return fail(RQ_EUNSUPPORTED,
                         "rq_grouped_plan_init: problem %d is outside the planned GEMV (needs "
-                        "16-bit scales, cols %% 512 == 0, 16-byte aligned scales/biases, "
+                        "m <= 4, 16-bit scales, cols %% 512 == 0, 16-byte aligned scales/biases, "
                         "m*cols*2 bytes of activations within the LDS budget); use rq_qmm_grouped",
                         i);
         if ((problems[i].rows + rq::kQmvRowsPerBlock - 1) / rq::kQmvRowsPerBlock > 65536)

@@ -919,8 +919,17 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
         }
 }
 
+#ifndef RQ_QMV_STREAM_WPE
+#define RQ_QMV_STREAM_WPE 0  // >0: occupancy (waves per SIMD) requested for the streamed GEMV
+#endif
+#if RQ_QMV_STREAM_WPE > 0
+#define RQ_STREAM_OCC __attribute__((amdgpu_waves_per_eu(RQ_QMV_STREAM_WPE)))
+#else
+#define RQ_STREAM_OCC
+#endif
+
 template <int BITS, int SDT, int NMC, int MI, int GSH>
-__global__ __launch_bounds__(kBlock) void qmv_stream_inline(const QmvArgs args) {
+__global__ __launch_bounds__(kBlock) RQ_STREAM_OCC void qmv_stream_inline(const QmvArgs args) {
     const int bid = blockIdx.x;
     int lo = 0, hi = args.n - 1;
     while (lo < hi) {
@@ -932,7 +941,7 @@ __global__ __launch_bounds__(kBlock) void qmv_stream_inline(const QmvArgs args) 
 }
 
 template <int BITS, int SDT, int NMC, int MI, int GSH>
-__global__ __launch_bounds__(kBlock) void qmv_stream_table(const rq::QmvTable a) {
+__global__ __launch_bounds__(kBlock) RQ_STREAM_OCC void qmv_stream_table(const rq::QmvTable a) {
     const uint32_t e = a.blocks[blockIdx.x];
     const rq_problem P = a.descs[e >> 16];
     qmv_stream_body<BITS, SDT, NMC, MI, GSH>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
@@ -1091,7 +1100,10 @@ size_t qmv_stream_lds(int64_t m, int64_t cols, int gs) {
            (((size_t)m * (cols / xg) * 4 + 15) & ~(size_t)15) + 4 * (size_t)wave_bytes;
 }
 bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs) {
-    return sb_dt != RQ_F32 && p.cols % 512 == 0 && p.rows <= (int64_t)65536 * kQmvRowsPerBlock &&
+    // m > 4 takes ceil(m/4) passes of 4 slots here; the LDS-staged kernel's
+    // 8-row slots (gs 64) do less MFMA work there
+    return m <= 4 && sb_dt != RQ_F32 && p.cols % 512 == 0 &&
+           p.rows <= (int64_t)65536 * kQmvRowsPerBlock &&
            (((uintptr_t)p.scales | (uintptr_t)p.biases) & 15) == 0 &&
            qmv_stream_lds(m, p.cols, gs) <= (size_t)kQmvLdsBudget;
 }

@@ -244,8 +244,11 @@ class GroupedQmv:
     bits, group size and the scales dtype.  The plan keeps references to every
     tensor, so run() may be called repeatedly (e.g. one decode step each)."""
 
+    PLAN_MIN_BLOCKS = 1024  # below this many 64-row blocks the K-split launches are faster
+
     def __init__(self, xs: Sequence[Tensor], ws: Sequence[Tuple[Tensor, Tensor, Tensor]],
-                 group_size: int = 64, bits: int = 4, out: Sequence[Tensor] | None = None):
+                 group_size: int = 64, bits: int = 4, out: Sequence[Tensor] | None = None,
+                 planned: bool | None = None):
         _check_args(group_size, bits)
         if len(xs) != len(ws):
             raise ValueError("need one weight triple per activation")
@@ -281,8 +284,12 @@ class GroupedQmv:
         self.codes = (DTYPE_CODE[x0.dtype], DTYPE_CODE[sdt], DTYPE_CODE[ydt])
         self.group_size, self.bits = group_size, bits
         # A device-side schedule (one launch per run) where the planned kernel
-        # covers every problem; otherwise the host-array entry point.
+        # covers every problem and the set is large enough (planned=None), or
+        # always (True: an uncovered set raises) or never (False).
         self.plan, self._table = None, None
+        blocks = sum((w[0].shape[0] + 63) // 64 for w in ws)
+        if planned is False or (planned is None and blocks < self.PLAN_MIN_BLOCKS):
+            return
         L = lib()
         nbytes = L.rq_grouped_plan_table_bytes(self.probs, self.n)
         check(nbytes if nbytes < 0 else 0, "grouped_qmv plan")
@@ -292,7 +299,7 @@ class GroupedQmv:
             rc = L.rq_grouped_plan_init(self.probs, self.n, *self.codes, self.m, group_size, bits,
                                         table.data_ptr(), table.numel(), ctypes.byref(plan),
                                         torch.cuda.current_stream(self.device).cuda_stream)
-        if rc == RQ_EUNSUPPORTED:
+        if rc == RQ_EUNSUPPORTED and not planned:
             return
         check(rc, "grouped_qmv plan")
         self.plan, self._table = plan, table

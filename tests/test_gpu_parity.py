@@ -378,19 +378,17 @@ def _planned(O, rq, dev, shapes, M, gs, bits, seed, xdt=torch.bfloat16, sdt=torc
         xs.append(x.to(dev))
         ws.append((wq.to(dev), s.to(dev), b.to(dev)))
         refs.append(O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact"))
-    plan = rq.GroupedQmv(xs, ws, gs, bits)
-    assert plan.plan is not None, "expected the planned kernel to cover these problems"
+    plan = rq.GroupedQmv(xs, ws, gs, bits, planned=True)
+    assert plan.plan is not None
     return plan, refs, xs, ws
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 8, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 @pytest.mark.parametrize("gs", GROUPS)
 @pytest.mark.parametrize("bits", BITS)
 def test_planned_qmv_parity(O, rq, dev, bits, gs, M):
     say(f"planned qmv bits={bits} gs={gs} M={M}")
-    # activations are staged whole: M*K*2 bytes must stay within the 64 KB budget
-    shapes = [(R, K) for R, K in PLAN_SHAPES if M * K * 2 <= 48 * 1024]
-    plan, refs, _, _ = _planned(O, rq, dev, shapes, M, gs, bits, 5000 + 10 * bits + gs)
+    plan, refs, _, _ = _planned(O, rq, dev, PLAN_SHAPES, M, gs, bits, 5000 + 10 * bits + gs)
     for y, ref in zip(plan.run(), refs):
         rel_check(y, ref, what=f"planned b{bits} g{gs} M{M}")
 
@@ -399,9 +397,20 @@ def test_planned_qmv_parity(O, rq, dev, bits, gs, M):
                                      (torch.bfloat16, torch.float16)])
 def test_planned_qmv_dtypes(O, rq, dev, xdt, sdt):
     say(f"planned qmv x={xdt} s={sdt}")
-    plan, refs, _, _ = _planned(O, rq, dev, PLAN_SHAPES, 5, 64, 4, 5900, xdt, sdt)
+    plan, refs, _, _ = _planned(O, rq, dev, PLAN_SHAPES, 3, 64, 4, 5900, xdt, sdt)
     for y, ref in zip(plan.run(), refs):
         rel_check(y, ref, what=f"planned {xdt} {sdt}")
+
+
+def test_planned_rejects_uncovered_sets(O, rq, dev):
+    """m > 4 or a cols not multiple of 512: planned=True raises, auto falls back."""
+    from rwkvq._lib import RwkvqError
+    w = weights(64, 768, 1)
+    wq, s, b = (t.to(dev) for t in O.quantize(w, 64, 4))
+    x = acts(1, 768, 1).to(dev)
+    with pytest.raises(RwkvqError):
+        rq.GroupedQmv([x], [(wq, s, b)], 64, 4, planned=True)
+    assert rq.GroupedQmv([x], [(wq, s, b)], 64, 4).plan is None
 
 
 def test_planned_many_problems_one_launch(O, rq, dev):
