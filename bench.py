@@ -5,8 +5,8 @@ sweep -- 24 layers x {r, k, v, o [2048,2048], FFN key [8192,2048], FFN value
 [2048,8192]} + head [65536,2048], 4-bit g64 with bf16 scales/biases, weights
 ~N(0,0.02) with a distinct seed per layer and projection (755 MB of packed
 weights, larger than the 256 MB MALL), bf16 activations ~N(0,1), M=1.
-One step = the whole sweep, run by rq_qmm_grouped (145 independent GEMVs in
-ceil(145/48) launches).  `value` = effective weight-stream GB/s:
+One step = the whole sweep: one planned grouped call (rq_grouped_plan_run),
+a single launch over the 145 independent GEMVs.  `value` = effective weight-stream GB/s:
 (R*K*bits/8 + 2*R*(K/gs)*2 bytes summed over the sweep) / step time, with all
 inputs resident in HBM.
 
@@ -67,13 +67,13 @@ def parse():
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmv_config2_sweep_m1_traffic.txt")
 PMC_RUNS, COPY_BYTES, COPY_RUNS = 3, 1 << 30, 3
-HEAD_KERNEL = "qmv_kernel"
+HEAD_KERNEL = "qmv_stream_table"
 
 
 def pmc_workload(torch, rq, dev):
-    """What the counter passes profile: the headline plan PMC_RUNS times,
-    then COPY_RUNS copies of COPY_BYTES (read COPY_BYTES, write COPY_BYTES)
-    as the last dispatches of the process."""
+    """What the counter passes profile: the headline plan (one launch) PMC_RUNS
+    times, then COPY_RUNS copies of COPY_BYTES (read COPY_BYTES, write
+    COPY_BYTES) as the last dispatches of the process."""
     probs, _ = make_sweep(rq, torch, dev, M=1)
     plan = rq.GroupedQmv([x for _, x, _ in probs], [w for _, _, w in probs], 64, 4)
     for _ in range(PMC_RUNS):
@@ -160,7 +160,7 @@ def kt_report(d):
         per = {}
         with open(traces[0], newline="") as fh:
             for r in csv.DictReader(fh):
-                if not any(k in r["Kernel_Name"] for k in ("qmv_kernel", "qmm_", "quantize_kernel")):
+                if not any(k in r["Kernel_Name"] for k in ("qmv_", "qmm_", "quantize_kernel")):
                     continue
                 key = (r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0],
                        int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])))
@@ -224,10 +224,14 @@ def time_region(torch, fn, steps, warmup):
 def call_duration(torch, fn, reps):
     """Mean HIP-event duration of one fn() call, one event pair per call,
     recorded on torch's current stream -- the stream the library launches
-    on -- with a synchronisation between calls so that no two overlap."""
+    on.  Each measured call follows an unmeasured one, so the GPU is busy
+    while the host enqueues the first event, the call and the second event:
+    the pair then brackets the kernel, not the host's submission latency.
+    A synchronisation between rounds keeps the rounds apart."""
     tot = 0.0
     for _ in range(reps):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        fn()
         a.record()
         fn()
         b.record()
@@ -300,12 +304,11 @@ def main():
     t_step = time_region(torch, plan.run, args.steps, args.warmup)
     value = total_wbytes / t_step / 1e9
 
-    # The step is one rq_qmm_grouped call; the library buckets the 145
-    # problems by K and issues ceil(bucket/48) launches of qmv_kernel per
-    # bucket (K=2048: 121 problems -> 3, K=8192: 24 -> 1), back to back on
-    # one stream.  Average launch = event time of the call / launches.
-    n2048 = sum(1 for x in xs if x.shape[1] == D)
-    launches = -(-n2048 // 48) + -(-(len(xs) - n2048) // 48)
+    # The step is one planned grouped call (rq_grouped_plan_run): ONE launch
+    # of qmv_stream_table over all 145 problems (3168 blocks of 64 rows,
+    # K=8192 blocks first).  Average launch = event time of the call.
+    assert plan.plan is not None, "the config-2 sweep must run on the planned GEMV"
+    launches = 1
     call_t = call_duration(torch, plan.run, max(5, args.steps))
     avg_launch = call_t / launches
     bytes_per_launch = total_wbytes / launches
@@ -334,7 +337,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic(),
-                     "kernel": "qmv_kernel<BITS=4, scales bf16, NMC=1, RB=1, KS=1, NS=4, SLDS>",
+                     "kernel": "qmv_stream_table<BITS=4, scales bf16, NMC=1, MI=1, GSH=6>",
                      "avg_launch_us": round(avg_launch * 1e6, 2),
                      "bytes_per_launch": int(bytes_per_launch)},
     }
