@@ -759,8 +759,20 @@ __global__ __launch_bounds__(kBlock, 1) void qmm_t_dma(
 //              DMA stage st+AHEAD; dequantize stage st+1 into bf16 slot.
 //   consumers: wait own LDS reads; barrier; MFMAs on stage st.
 constexpr int kWsBlock = 512;
+#ifndef RQ_GEMM_K64
+#define RQ_GEMM_K64 1  // 1: 64-wide stages with whole-line loads (qmm_t_k64) where they apply
+#endif
+#ifndef RQ_GEMM_REG
+#define RQ_GEMM_REG 0  // 1: register-staged producers (qmm_t_wsr); 0: DMA ring (qmm_t_ws)
+#endif
+#ifndef RQ_GEMM_DEPTH
+#define RQ_GEMM_DEPTH 4  // stages of loads in flight per producer thread (even)
+#endif
+#ifndef RQ_WS_SLOTS
+#define RQ_WS_SLOTS 6  // DMA ring slots of qmm_t_ws (4 or 6): RQ_WS_SLOTS-1 stages in flight
+#endif
 
-template <int BITS, int SDT, int BN, int NSLOT>
+template <int BITS, int SDT, int BN, int NSLOT, bool SBP>
 struct WsCfg {
     static constexpr int BM = 256;
     static constexpr int AHEAD = NSLOT - 1;
@@ -771,38 +783,71 @@ struct WsCfg {
     static constexpr int NC = (CODE_DW + NP - 1) / NP;          // code DMAs per producer
     static constexpr int C_BYTES = NC * NP * 4;
     static constexpr int SB = SDT == RQ_F32 ? 4 : 2;
-    static constexpr int S_BYTES = NP * 4;                      // 4-byte lane stride
-    static constexpr int PER_STAGE = NX + NC + 2;
+    // SBP: the (scale, bias) values of 8 groups per row arrive with one
+    // 16-byte DMA each per 8 groups, one period ahead, and are copied to the
+    // buffer the dequantisation reads at the period start; otherwise one 2-
+    // or 4-byte DMA each per stage.
+    static constexpr int S_BYTES = SBP ? 16 : NP * 4;           // 4-byte lane stride
+    static constexpr int PER_STAGE = NX + NC + (SBP ? 0 : 2);
+    static constexpr int SBP_BYTES = SBP ? BN * 16 : 16;        // per row and buffer: 8 values
     static constexpr int BLD = 40;                              // bf16 ring row stride
     static constexpr int B_BYTES = BN * BLD * 2;
     static_assert(NSLOT % 2 == 0, "the bf16 ring index is derived from the slot index");
     static_assert(BN <= NP, "one producer thread dequantizes one weight row");
 };
 
-template <int BITS, int SDT, int BN, int NSLOT>
+// LDS bytes of qmm_t_ws (the slot arrays, the bf16 ring and the scale buffers).
+template <int BITS, int SDT, int BN, int NSLOT, bool SBP>
+constexpr size_t ws_lds_bytes() {
+    typedef WsCfg<BITS, SDT, BN, NSLOT, SBP> C;
+    return (size_t)NSLOT * (C::X_BYTES + C::C_BYTES + 2 * C::S_BYTES) + (6 - NSLOT) * 4 * 16 +
+           2 * (size_t)BN * C::BLD * 2 + 4 * (size_t)C::SBP_BYTES;
+}
+// The deepest ring that fits the 160 KB of LDS.
+template <int BITS, int SDT, int BN, bool SBP>
+constexpr int ws_slots() {
+    return (RQ_WS_SLOTS >= 6 && ws_lds_bytes<BITS, SDT, BN, 6, SBP>() <= 160 * 1024) ? 6 : 4;
+}
+
+template <int BITS, int SDT, int BN, int NSLOT, bool SBP>
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_ws(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
     void* __restrict__ y, int y_dt, int tiles_m, int tiles_n) {
-    typedef WsCfg<BITS, SDT, BN, NSLOT> C;
+    typedef WsCfg<BITS, SDT, BN, NSLOT, SBP> C;
+    static_assert(!SBP || SDT != RQ_F32, "parked scales are 16-bit");
     constexpr int BM = C::BM;
     constexpr int WN = BN / 2;
     constexpr int TM = 8, TN = WN / 16;
-#define RQ_RING(name, bytes)                                                    \
-    __shared__ __attribute__((aligned(16))) uint8_t name##0[bytes];             \
-    __shared__ __attribute__((aligned(16))) uint8_t name##1[bytes];             \
-    __shared__ __attribute__((aligned(16))) uint8_t name##2[bytes];             \
-    __shared__ __attribute__((aligned(16))) uint8_t name##3[bytes];
+    // One __shared__ object per ring slot (up to 6; slots >= NSLOT are 16-byte
+    // stubs), so that the compiler can tell a DMA's target from the slots
+    // being read and never makes a read wait for a DMA in flight.
+#define RQ_RING(name, bytes)                                                              \
+    __shared__ __attribute__((aligned(16))) uint8_t name##0[bytes];                       \
+    __shared__ __attribute__((aligned(16))) uint8_t name##1[bytes];                       \
+    __shared__ __attribute__((aligned(16))) uint8_t name##2[bytes];                       \
+    __shared__ __attribute__((aligned(16))) uint8_t name##3[bytes];                       \
+    __shared__ __attribute__((aligned(16))) uint8_t name##4[NSLOT > 4 ? (bytes) : 16];    \
+    __shared__ __attribute__((aligned(16))) uint8_t name##5[NSLOT > 5 ? (bytes) : 16];
     RQ_RING(xr_, C::X_BYTES)
     RQ_RING(cr_, C::C_BYTES)
     RQ_RING(sr_, C::S_BYTES)
     RQ_RING(br_, C::S_BYTES)
 #undef RQ_RING
-    static_assert(NSLOT == 4, "four ring slots are declared");
+    static_assert(NSLOT == 4 || NSLOT == 6, "four or six ring slots are declared");
     __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * C::BLD];
     __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * C::BLD];
-#define RQ_PICK(name) \
-    [&](int u) -> uint8_t* { return u == 0 ? name##0 : u == 1 ? name##1 : u == 2 ? name##2 : name##3; }
+    // DMA targets and the copies read by the dequantisation: distinct objects,
+    // so the compiler never makes a read wait for the DMA in flight
+    __shared__ __attribute__((aligned(16))) uint8_t sbn_s[C::SBP_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t sbn_b[C::SBP_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t sbc_s[C::SBP_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t sbc_b[C::SBP_BYTES];
+#define RQ_PICK(name)                                                                   \
+    [&](int u) -> uint8_t* {                                                            \
+        return u == 0 ? name##0 : u == 1 ? name##1 : u == 2 ? name##2 : u == 3 ? name##3 \
+             : u == 4 ? name##4 : name##5;                                              \
+    }
     auto xr = RQ_PICK(xr_);
     auto cr = RQ_PICK(cr_);
     auto sr = RQ_PICK(sr_);
@@ -868,18 +913,57 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_ws(
                 __builtin_amdgcn_global_load_lds((const void*)(cb + coff[i]),
                                                  (lds_void_t*)(cr(slot) + (i * C::NP + pw * 64) * 4),
                                                  4, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void*)(sbase + gb + soff),
-                                             (lds_void_t*)(sr(slot) + pw * 64 * 4), C::SB, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void*)(bbase + gb + soff),
-                                             (lds_void_t*)(br(slot) + pw * 64 * 4), C::SB, 0, 0);
+            if constexpr (!SBP) {
+                __builtin_amdgcn_global_load_lds((const void*)(sbase + gb + soff),
+                                                 (lds_void_t*)(sr(slot) + pw * 64 * 4), C::SB, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(bbase + gb + soff),
+                                                 (lds_void_t*)(br(slot) + pw * 64 * 4), C::SB, 0, 0);
+            }
         };
-        auto dequant = [&](int slot, int bslot) {
+        // SBP: this thread's row's scales and biases of groups [8p, 8p+8)
+        // are DMA'd (16 B per row each) at the start of period p-1 and copied
+        // from there by the same thread at the start of period p.  Threads
+        // past BN issue none.
+        const int G32 = (int)G;
+        auto dma_sb = [&](int period) {
+            if constexpr (SBP) {
+                if (pt < BN) {
+                    int g0 = period * 8;
+                    g0 = g0 < G32 - 8 ? g0 : G32 - 8;
+                    const uint8_t* sp = (const uint8_t*)scales + (srow * G + g0) * 2;
+                    const uint8_t* bp = (const uint8_t*)biases + (srow * G + g0) * 2;
+                    __builtin_amdgcn_global_load_lds((const void*)sp,
+                                                     (lds_void_t*)(sbn_s + pw * 64 * 16), 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds((const void*)bp,
+                                                     (lds_void_t*)(sbn_b + pw * 64 * 16), 16, 0, 0);
+                }
+            }
+        };
+        auto dequant = [&](int slot, int bslot, int stage) {
+            int local = 0;
+            if constexpr (SBP) {
+                const int g = (stage * 32) >> gs_shift;
+                local = g & 7;
+                if (((stage * 32) & ((8 << gs_shift) - 1)) == 0) {  // first stage of a period
+                    if (pt < BN) {
+                        const u32x4_t vs = *(const u32x4_t*)(sbn_s + pt * 16);
+                        const u32x4_t vb = *(const u32x4_t*)(sbn_b + pt * 16);
+                        *(u32x4_t*)(sbc_s + pt * 16) = vs;
+                        *(u32x4_t*)(sbc_b + pt * 16) = vb;
+                    }
+                    dma_sb((g >> 3) + 1);  // after the copy has read the previous period
+                }
+            }
             if (pt < BN) {
                 uint32_t words[BITS];
 #pragma unroll
                 for (int w = 0; w < BITS; ++w) words[w] = *(const uint32_t*)(cr(slot) + (pt * BITS + w) * 4);
                 float s, b;
-                if constexpr (SDT == RQ_F32) {
+                if constexpr (SBP) {
+                    const int o = pt * 16 + 2 * local;
+                    s = dt_traits<SDT>::to_f32(*(const uint16_t*)(sbc_s + o));
+                    b = dt_traits<SDT>::to_f32(*(const uint16_t*)(sbc_b + o));
+                } else if constexpr (SDT == RQ_F32) {
                     s = *(const float*)(sr(slot) + pt * 4);
                     b = *(const float*)(br(slot) + pt * 4);
                 } else {
@@ -894,13 +978,14 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_ws(
             }
         };
 
+        dma_sb(0);  // period 0; the wait below covers it
 #pragma unroll
         for (int i = 0; i < C::AHEAD; ++i) dma(i, i);
         s_wait_vmcnt_lgkm0<(C::AHEAD - 1) * C::PER_STAGE>();
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();  // barrier 0: stage 0 has landed
         asm volatile("" ::: "memory");
-        dequant(0, 0);
+        dequant(0, 0, 0);
         for (int s = 0; s < nst; s += NSLOT) {
 #pragma unroll
             for (int u = 0; u < NSLOT; ++u) {
@@ -910,7 +995,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_ws(
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
                 dma(st + C::AHEAD, (u + C::AHEAD) % NSLOT);
-                if (st < nst) dequant((u + 1) % NSLOT, (u + 1) & 1);
+                if (st < nst) dequant((u + 1) % NSLOT, (u + 1) & 1, st + 1);
             }
         }
         s_wait_vmcnt_lgkm0<0>();
@@ -977,6 +1062,397 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_ws(
         }
 }
 
+
+// ------------------------------------------------------------- qmm_t_wsr
+//
+// Warp-specialised GEMM with register-staged producers (bf16 activations,
+// M >= 256).  8 waves per block: waves 0-3 run only MFMAs (2x2, wave tile
+// 128 x BN/2, fp32 accumulators); waves 4-7 ("producers") keep D stages of
+// 32 contraction elements in flight in their registers -- the block's 256
+// activation rows (4 x 16 B per thread), their weight row's codes and that
+// row's (scale, bias) -- and per stage write the activations to a 2-slot
+// LDS ring and dequantize the codes straight from registers into a 2-slot
+// bf16 ring.  Ordinary loads (not direct-to-LDS DMA) take the fast
+// register return path and let the compiler track their waits.  One
+// barrier per stage: producers write stage s, barrier s, consumers compute
+// stage s while producers prepare s+1.
+template <int BITS, int SDT, int BN, int D>
+__global__ __launch_bounds__(kWsBlock, 1) void qmm_t_wsr(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
+    const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
+    void* __restrict__ y, int y_dt, int tiles_m, int tiles_n) {
+    constexpr int BM = 256;
+    constexpr int WN = BN / 2;
+    constexpr int TM = 8, TN = WN / 16;
+    constexpr int BLD = 40;  // bf16 ring row stride (elements)
+    static_assert(D % 2 == 0, "the LDS rings are indexed by the unrolled stage parity");
+    static_assert(BN <= 256, "one producer thread dequantizes one weight row");
+    __shared__ __attribute__((aligned(16))) uint8_t xs0[BM * 64];
+    __shared__ __attribute__((aligned(16))) uint8_t xs1[BM * 64];
+    __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * BLD];
+    __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * BLD];
+
+    const int ntiles = tiles_m * tiles_n;
+    const int per_xcd = (ntiles + 7) / 8;
+    const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+    if (t >= ntiles) return;
+    const int64_t m0 = (int64_t)(t / tiles_n) * BM, n0 = (int64_t)(t % tiles_n) * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t runs = K >> 5, wpr = runs * BITS, G = K >> gs_shift;
+    const int nst = (int)runs;
+
+    if (wave >= 4) {
+        // ---------------------------------------------------------- producers
+        const int pt = tid - 256, pw = wave - 4;
+        // activations: chunk i of this thread = row (pw*4+i)*16 + lane/4, 16-byte
+        // chunk (lane&3) ^ ((row>>2)&3) of the stage's 64 bytes; it lands at LDS
+        // byte (pw*4+i)*1024 + 16*lane (the consumers' swizzled fragment layout)
+        typedef const __attribute__((address_space(1))) u32x4_t* gx_t;
+        uint32_t xoff[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = (pw * 4 + i) * 16 + (lane >> 2);
+            const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+            int64_t grow = m0 + row;
+            grow = grow < M ? grow : M - 1;
+            xoff[i] = (uint32_t)((grow - m0) * K * 2 + chunk * 16);
+        }
+        const uint8_t* xbase = (const uint8_t*)(x + m0 * K);
+        const bool has_row = pt < BN;
+        int64_t wrow = n0 + (has_row ? pt : 0);
+        wrow = wrow < R ? wrow : R - 1;
+        const uint32_t* wrow_p = wq + wrow * wpr;
+        const int64_t sb_row = wrow * G;
+
+        u32x4_t xv[D][4];
+        uint32_t cv[D][BITS];
+        uint32_t sv[D], bv[D];
+        auto issue = [&](int st, int r) {
+            const int sc = st < nst ? st : nst - 1;
+            const uint8_t* xb = xbase + (int64_t)sc * 64;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[r][i] = *(gx_t)(xb + xoff[i]);
+            if (has_row) {
+                load_run<BITS>(wrow_p + (int64_t)sc * BITS, cv[r]);
+                const int64_t gi = sb_row + (((int64_t)sc * 32) >> gs_shift);
+                if constexpr (SDT == RQ_F32) {
+                    sv[r] = ((const uint32_t*)scales)[gi];
+                    bv[r] = ((const uint32_t*)biases)[gi];
+                } else {
+                    sv[r] = ((const uint16_t*)scales)[gi];
+                    bv[r] = ((const uint16_t*)biases)[gi];
+                }
+            }
+        };
+#pragma unroll
+        for (int r = 0; r < D; ++r) issue(r, r);
+
+        for (int s0 = 0; s0 < nst; s0 += D) {
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                const int st = s0 + u;
+                uint8_t* xs = (u & 1) ? xs1 : xs0;
+                uint16_t* bq = (u & 1) ? bq1 : bq0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) *(u32x4_t*)(xs + (pw * 4 + i) * 1024 + 16 * lane) = xv[u][i];
+                if (has_row) {
+                    float sf, bf;
+                    if constexpr (SDT == RQ_F32) {
+                        sf = __uint_as_float(sv[u]);
+                        bf = __uint_as_float(bv[u]);
+                    } else {
+                        sf = dt_traits<SDT>::to_f32((uint16_t)sv[u]);
+                        bf = dt_traits<SDT>::to_f32((uint16_t)bv[u]);
+                    }
+                    uint32_t d[16];
+                    dequant_run_fast<BITS>(cv[u], sf, bf, d);
+                    u32x4_t* dst = (u32x4_t*)(bq + pt * BLD);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        dst[q] = u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
+                }
+                issue(st + D, u);
+                // this stage's LDS writes are complete before the barrier
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+            }
+        }
+        return;
+    }
+
+    // -------------------------------------------------------------- consumers
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lg = lane >> 4, lr = lane & 15;
+    f32x4_t acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    uint32_t aoff[TM];
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+        const int row = wm * 128 + a * 16 + lr;
+        aoff[a] = (uint32_t)(row * 64 + ((lg ^ ((row >> 2) & 3)) * 16));
+    }
+    const uint32_t boff = (uint32_t)((wn * WN + lr) * BLD + lg * 8);
+
+    for (int s0 = 0; s0 < nst; s0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int st = s0 + u;
+            // own LDS reads of the previous stage are done, then wait for stage st
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (st < nst) {
+                const uint8_t* xs = (u & 1) ? xs1 : xs0;
+                const uint16_t* bq = (u & 1) ? bq1 : bq0;
+                bf16x8_t af[TM], bf[TN];
+#pragma unroll
+                for (int a = 0; a < TM; ++a)
+                    af[a] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[a]));
+#pragma unroll
+                for (int b = 0; b < TN; ++b)
+                    bf[b] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(bq + boff + b * 16 * BLD));
+#pragma unroll
+                for (int a = 0; a < TM; ++a)
+#pragma unroll
+                    for (int b = 0; b < TN; ++b)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bf[b], acc[a][b],
+                                                                            0, 0, 0);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int64_t n = n0 + wn * WN + b * 16 + lr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t m = m0 + wm * 128 + a * 16 + 4 * lg + i;
+                if (m < M && n < R) store_dt(y, y_dt, m * R + n, acc[a][b][i]);
+            }
+        }
+}
+
+
+// ------------------------------------------------------------- qmm_t_k64
+//
+// The warp-specialised GEMM with 64-element contraction stages (bf16
+// activations, M >= 256, 16-bit scales, K a multiple of 8 groups).  The
+// per-CU memory rate of these kernels is set by how many L2 requests a CU
+// keeps in flight, so every request here carries a whole 128-byte line: a
+// producer wave-load covers 8 activation rows x 128 B, a weight row's codes
+// for a stage are 64 contiguous codes, and each row's (scale, bias) values
+// arrive 8 groups per 16-byte load, once per 8 groups.  Waves 0-3 run MFMAs
+// (2x2, wave tile 128 x BN/2, two k-steps of 32 per stage); waves 4-7 keep
+// D stages of loads in flight in registers, write the activations to a
+// 2-slot LDS ring (16-byte chunks XOR-swizzled by row) and dequantize their
+// row's codes straight from registers into a 2-slot bf16 ring.  One barrier
+// per stage.
+template <int BITS, int SDT, int BN, int GSH>
+__global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
+    const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, void* __restrict__ y,
+    int y_dt, int tiles_m, int tiles_n) {
+    constexpr int BM = 256;
+    constexpr int WN = BN / 2;
+    constexpr int TM = 8, TN = WN / 16;
+    constexpr int BLD = 72;                  // bf16 ring row stride (64 + 8 elements)
+    constexpr int D = 2;                     // stages of loads in flight per producer thread
+    constexpr int P = (8 << GSH) / 64;       // stages per 8-group (scale, bias) chunk: 4, 8, 16
+    static_assert(SDT != RQ_F32, "16-bit scales");
+    static_assert(BN <= 256, "one producer thread dequantizes one weight row");
+    __shared__ __attribute__((aligned(16))) uint8_t xs0[BM * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t xs1[BM * 128];
+    __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * BLD];
+    __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * BLD];
+
+    const int ntiles = tiles_m * tiles_n;
+    const int per_xcd = (ntiles + 7) / 8;
+    const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+    if (t >= ntiles) return;
+    const int64_t m0 = (int64_t)(t / tiles_n) * BM, n0 = (int64_t)(t % tiles_n) * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t wpr = (K >> 5) * BITS, G = K >> GSH;
+    const int nst = (int)(K >> 6);
+    const int nper = (nst + P - 1) / P;
+
+    if (wave >= 4) {
+        // ---------------------------------------------------------- producers
+        const int pt = tid - 256, pw = wave - 4;
+        typedef const __attribute__((address_space(1))) u32x4_t* gv_t;
+        // activations: load i of this thread = row (pw*8+i)*8 + lane/8, chunk
+        // lane%8 of the stage's 128 bytes; stored at chunk ^ (row & 7)
+        uint32_t xoff[8], xdst[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int row = (pw * 8 + i) * 8 + (lane >> 3);
+            const int chunk = lane & 7;
+            int64_t grow = m0 + row;
+            grow = grow < M ? grow : M - 1;
+            xoff[i] = (uint32_t)((grow - m0) * K * 2 + chunk * 16);
+            xdst[i] = (uint32_t)(row * 128 + ((chunk ^ (row & 7)) * 16));
+        }
+        const uint8_t* xbase = (const uint8_t*)(x + m0 * K);
+        const bool has_row = pt < BN;
+        int64_t wrow = n0 + (has_row ? pt : 0);
+        wrow = wrow < R ? wrow : R - 1;
+        const uint32_t* wrow_p = wq + wrow * wpr;
+        const uint16_t* srow_p = (const uint16_t*)scales + wrow * G;
+        const uint16_t* brow_p = (const uint16_t*)biases + wrow * G;
+
+        u32x4_t xv[D][8];
+        uint32_t cv[D][2 * BITS];
+        auto issue = [&](int st, int r) {
+            const int sc = st < nst ? st : nst - 1;
+            const uint8_t* xb = xbase + (int64_t)sc * 128;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[r][i] = *(gv_t)(xb + xoff[i]);
+            if (has_row) {
+                const uint32_t* cp = wrow_p + (int64_t)sc * 2 * BITS;
+                if constexpr ((BITS & 1) == 0) {
+#pragma unroll
+                    for (int q = 0; q < BITS / 2; ++q) {
+                        const u32x4_t v = *((gv_t)cp + q);
+                        cv[r][4 * q] = v[0]; cv[r][4 * q + 1] = v[1];
+                        cv[r][4 * q + 2] = v[2]; cv[r][4 * q + 3] = v[3];
+                    }
+                } else {
+                    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+                    for (int q = 0; q < BITS; ++q) {
+                        const u32x2_t v = *((const __attribute__((address_space(1))) u32x2_t*)cp + q);
+                        cv[r][2 * q] = v[0]; cv[r][2 * q + 1] = v[1];
+                    }
+                }
+            }
+        };
+        // (scale, bias) of 8 groups: cur for this period, nxt for the next one
+        auto load_sb = [&](int per, u32x4_t& sv, u32x4_t& bv) {
+            int g0 = per * 8;
+            g0 = g0 < (int)G - 8 ? g0 : (int)G - 8;
+            if (has_row) {
+                sv = *(gv_t)(srow_p + g0);
+                bv = *(gv_t)(brow_p + g0);
+            }
+        };
+        u32x4_t s_cur = {0u, 0u, 0u, 0u}, b_cur = s_cur, s_nxt = s_cur, b_nxt = s_cur;
+        load_sb(0, s_cur, b_cur);
+        load_sb(1, s_nxt, b_nxt);
+#pragma unroll
+        for (int r = 0; r < D; ++r) issue(r, r);
+
+        for (int per = 0; per < nper; ++per) {
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                const int st = per * P + u;
+                uint8_t* xs = (u & 1) ? xs1 : xs0;
+                uint16_t* bq = (u & 1) ? bq1 : bq0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u % D][i];
+                if (has_row) {
+                    uint32_t d[32];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        // group of run h of this stage within the 8-group chunk
+                        constexpr int GPS = 64 >> GSH ? 64 >> GSH : 1;  // groups per stage (>= 1)
+                        const int gl = GSH == 5 ? 2 * u + h : (GSH == 6 ? u : u / 2);
+                        const uint32_t sw = s_cur[(gl & 7) >> 1], bw = b_cur[(gl & 7) >> 1];
+                        const uint16_t sr = (gl & 1) ? (uint16_t)(sw >> 16) : (uint16_t)(sw & 0xffffu);
+                        const uint16_t br = (gl & 1) ? (uint16_t)(bw >> 16) : (uint16_t)(bw & 0xffffu);
+                        (void)GPS;
+                        dequant_run_fast<BITS>(&cv[u % D][h * BITS], dt_traits<SDT>::to_f32(sr),
+                                               dt_traits<SDT>::to_f32(br), d + 16 * h);
+                    }
+                    u32x4_t* dst = (u32x4_t*)(bq + pt * BLD);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        dst[q] = u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
+                }
+                issue(st + D, u % D);
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this stage's LDS writes are done
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+            }
+            s_cur = s_nxt;
+            b_cur = b_nxt;
+            load_sb(per + 2, s_nxt, b_nxt);
+        }
+        return;
+    }
+
+    // -------------------------------------------------------------- consumers
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lg = lane >> 4, lr = lane & 15;
+    f32x4_t acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    uint32_t aoff[2][TM];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+            const int row = wm * 128 + a * 16 + lr;
+            aoff[h][a] = (uint32_t)(row * 128 + (((h * 4 + lg) ^ (row & 7)) * 16));
+        }
+    const uint32_t boff = (uint32_t)((wn * WN + lr) * BLD + lg * 8);
+
+    for (int per = 0; per < nper; ++per) {
+#pragma unroll
+        for (int u = 0; u < P; ++u) {
+            const int st = per * P + u;
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // own LDS reads of the previous stage are done
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (st < nst) {
+                const uint8_t* xs = (u & 1) ? xs1 : xs0;
+                const uint16_t* bq = (u & 1) ? bq1 : bq0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    bf16x8_t af[TM], bf[TN];
+#pragma unroll
+                    for (int a = 0; a < TM; ++a)
+                        af[a] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
+#pragma unroll
+                    for (int b = 0; b < TN; ++b)
+                        bf[b] = __builtin_bit_cast(
+                            bf16x8_t, *(const u32x4_t*)(bq + boff + b * 16 * BLD + h * 32));
+#pragma unroll
+                    for (int a = 0; a < TM; ++a)
+#pragma unroll
+                        for (int b = 0; b < TN; ++b)
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bf[b],
+                                                                                acc[a][b], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int64_t n = n0 + wn * WN + b * 16 + lr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t m = m0 + wm * 128 + a * 16 + 4 * lg + i;
+                if (m < M && n < R) store_dt(y, y_dt, m * R + n, acc[a][b][i]);
+            }
+        }
+}
+
 }  // namespace
 
 namespace rq {
@@ -989,17 +1465,66 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
                                       int64_t m, int64_t rows, int64_t cols, int gs, void* y,
                                       int y_dt, hipStream_t stream) {
     const int gs_shift = __builtin_ctz(gs);
+    // 64-wide stages: 16-bit 16-byte aligned scales, whole 8-group chunks
+    if (m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 && cols % 64 == 0 &&
+        (cols / gs) % 8 == 0 && (((uintptr_t)scales | (uintptr_t)biases) & 15) == 0) {
+        const int bn = rows % 160 == 0 ? 160 : 128;
+        const int tm = (int)((m + 255) / 256);
+        const int tn = (int)((rows + bn - 1) / bn);
+        const int blocks = ((tm * tn + 7) / 8) * 8;
+#define RQ_K64(SD, BNV, GSHV)                                                                     \
+    hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, BNV, GSHV>), dim3(blocks), dim3(kWsBlock), 0,     \
+                       stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols, y, y_dt, tm, tn)
+#define RQ_K64_GS(SD, BNV)                                                                        \
+    switch (gs_shift) {                                                                           \
+        case 5: RQ_K64(SD, BNV, 5); break;                                                        \
+        case 6: RQ_K64(SD, BNV, 6); break;                                                        \
+        default: RQ_K64(SD, BNV, 7); break;                                                       \
+    }
+        if (sb_dt == RQ_BF16) {
+            if (bn == 160) { RQ_K64_GS(RQ_BF16, 160) } else { RQ_K64_GS(RQ_BF16, 128) }
+        } else {
+            if (bn == 160) { RQ_K64_GS(RQ_F16, 160) } else { RQ_K64_GS(RQ_F16, 128) }
+        }
+#undef RQ_K64_GS
+#undef RQ_K64
+        return hipGetLastError();
+    }
+    if (m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_REG) {
+        const int bn = rows % 160 == 0 ? 160 : 128;
+        const int tm = (int)((m + 255) / 256);
+        const int tn = (int)((rows + bn - 1) / bn);
+        const int blocks = ((tm * tn + 7) / 8) * 8;
+#define RQ_WSR(BNV)                                                                              \
+    RQ_DISPATCH_DT(sb_dt, SD,                                                                    \
+        hipLaunchKernelGGL((qmm_t_wsr<RQ_BITS, SD, BNV, RQ_GEMM_DEPTH>), dim3(blocks),           \
+                           dim3(kWsBlock), 0, stream, (const uint16_t*)x, wq, scales, biases, m,  \
+                           rows, cols, gs_shift, y, y_dt, tm, tn))
+        if (bn == 160) { RQ_WSR(160); } else { RQ_WSR(128); }
+#undef RQ_WSR
+        return hipGetLastError();
+    }
     if (m >= 256 && x_dt == RQ_BF16) {
         const int bn = rows % 160 == 0 ? 160 : 128;
         const int tm = (int)((m + 255) / 256);
         const int tn = (int)((rows + bn - 1) / bn);
         const int blocks = ((tm * tn + 7) / 8) * 8;
-#define RQ_DMA(BNV)                                                                              \
+        // parked scales: 16-bit, 16-byte aligned, whole periods of 8 groups
+        const bool sbp = sb_dt != RQ_F32 && (cols / gs) % 8 == 0 &&
+                         (((uintptr_t)scales | (uintptr_t)biases) & 15) == 0;
+#define RQ_DMA(BNV, SBPV)                                                                        \
     RQ_DISPATCH_DT(sb_dt, SD,                                                                    \
-        hipLaunchKernelGGL((qmm_t_ws<RQ_BITS, SD, BNV, 4>), dim3(blocks), dim3(kWsBlock), 0,     \
-                           stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,        \
-                           gs_shift, y, y_dt, tm, tn))
-        if (bn == 160) { RQ_DMA(160); } else { RQ_DMA(128); }
+        hipLaunchKernelGGL((qmm_t_ws<RQ_BITS, SD, BNV,                                          \
+                                     ws_slots<RQ_BITS, SD, BNV, SBPV && SD != RQ_F32>(),          \
+                                     SBPV && SD != RQ_F32>),                                      \
+                           dim3(blocks), dim3(kWsBlock), 0, stream, (const uint16_t*)x, wq,      \
+                           scales, biases, m,                                                    \
+                           rows, cols, gs_shift, y, y_dt, tm, tn))
+        if (sbp) {
+            if (bn == 160) { RQ_DMA(160, true); } else { RQ_DMA(128, true); }
+        } else {
+            if (bn == 160) { RQ_DMA(160, false); } else { RQ_DMA(128, false); }
+        }
 #undef RQ_DMA
         return hipGetLastError();
     }
