@@ -759,6 +759,15 @@ __global__ __launch_bounds__(kBlock, 1) void qmm_t_dma(
 //              DMA stage st+AHEAD; dequantize stage st+1 into bf16 slot.
 //   consumers: wait own LDS reads; barrier; MFMAs on stage st.
 constexpr int kWsBlock = 512;
+#ifndef RQ_K64_DEPTH
+#define RQ_K64_DEPTH 2  // qmm_t_k64: stages of loads in flight per producer thread
+#endif
+#ifndef RQ_K64_PPRIO
+#define RQ_K64_PPRIO 2  // qmm_t_k64: wave priority of the producer waves (0-3; 2 measured +4-6%)
+#endif
+#ifndef RQ_K64_CPRIO
+#define RQ_K64_CPRIO 0  // qmm_t_k64: wave priority of the MFMA waves (0-3)
+#endif
 #ifndef RQ_GEMM_K64
 #define RQ_GEMM_K64 1  // 1: 64-wide stages with whole-line loads (qmm_t_k64) where they apply
 #endif
@@ -1265,8 +1274,9 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     constexpr int WN = BN / 2;
     constexpr int TM = 8, TN = WN / 16;
     constexpr int BLD = 72;                  // bf16 ring row stride (64 + 8 elements)
-    constexpr int D = 2;                     // stages of loads in flight per producer thread
+    constexpr int D = RQ_K64_DEPTH;          // stages of loads in flight per producer thread
     constexpr int P = (8 << GSH) / 64;       // stages per 8-group (scale, bias) chunk: 4, 8, 16
+    static_assert(P % D == 0, "the register ring index is the unrolled stage index mod D");
     static_assert(SDT != RQ_F32, "16-bit scales");
     static_assert(BN <= 256, "one producer thread dequantizes one weight row");
     __shared__ __attribute__((aligned(16))) uint8_t xs0[BM * 128];
@@ -1287,6 +1297,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
 
     if (wave >= 4) {
         // ---------------------------------------------------------- producers
+        if (RQ_K64_PPRIO) __builtin_amdgcn_s_setprio(RQ_K64_PPRIO);
         const int pt = tid - 256, pw = wave - 4;
         typedef const __attribute__((address_space(1))) u32x4_t* gv_t;
         // activations: load i of this thread = row (pw*8+i)*8 + lane/8, chunk
@@ -1391,6 +1402,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     }
 
     // -------------------------------------------------------------- consumers
+    if (RQ_K64_CPRIO) __builtin_amdgcn_s_setprio(RQ_K64_CPRIO);
     const int wm = wave >> 1, wn = wave & 1;
     const int lg = lane >> 4, lr = lane & 15;
     f32x4_t acc[TM][TN];
