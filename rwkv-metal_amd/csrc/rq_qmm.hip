@@ -1465,6 +1465,243 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
         }
 }
 
+
+// ------------------------------------------------------------- qmm_n_k64
+//
+// Transposed product dX[M, K] = dY[M, R] . W^[R, K] (the QLoRA backward),
+// warp-specialised like qmm_t_k64: block tile 256 (dY rows) x 128 (output
+// columns k), 64 weight rows r per stage.  Waves 0-3 run MFMAs; waves 4-7
+// (producers) per stage
+//   - write the dY tile (256 rows x 128 B, whole-line loads) to a 2-slot ring,
+//   - dequantize the stage's 64 x 128 weight block from the packed code and
+//     (scale, bias) tiles they staged in LDS one stage earlier: thread
+//     (r-quad, k-octet) turns 4 rows x 8 columns into eight 8-byte writes of
+//     the bf16 tile Bt[k][r] (r contiguous, the MFMA B layout),
+//   - stage the next stage's code and (scale, bias) tiles (16-byte loads of
+//     the rows' packed words) and keep two stages of loads in flight.
+// Requires 16-bit scales, R % 64 == 0 and K % 128 == 0.
+template <int BITS, int SDT>
+__global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
+    const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
+    void* __restrict__ y, int y_dt, int tiles_m, int tiles_n) {
+    constexpr int BM = 256, BN = 128, WN = BN / 2;
+    constexpr int TM = 8, TN = WN / 16;
+    constexpr int BLD = 72;                 // bf16 tile row stride (64 + 8 elements)
+    constexpr int CW = BN * BITS / 32;      // packed words per weight row per stage
+    constexpr int CCH = CW / 4;             // 16-byte chunks per row (BITS of them)
+    constexpr int NCL = (64 * CCH + 255) / 256;  // code chunks per producer thread
+    static_assert(SDT != RQ_F32, "16-bit scales");
+    __shared__ __attribute__((aligned(16))) uint8_t xs0[BM * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t xs1[BM * 128];
+    __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * BLD];
+    __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * BLD];
+    __shared__ __attribute__((aligned(16))) uint32_t cs0[64 * CW];
+    __shared__ __attribute__((aligned(16))) uint32_t cs1[64 * CW];
+    __shared__ __attribute__((aligned(16))) uint16_t ss0[2 * 64 * 4];  // [scale|bias][row][<=4 groups]
+    __shared__ __attribute__((aligned(16))) uint16_t ss1[2 * 64 * 4];
+
+    const int ntiles = tiles_m * tiles_n;
+    const int per_xcd = (ntiles + 7) / 8;
+    const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+    if (t >= ntiles) return;
+    const int64_t m0 = (int64_t)(t / tiles_n) * BM, k0 = (int64_t)(t % tiles_n) * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t wpr = (K >> 5) * BITS, G = K >> gs_shift;
+    const int nst = (int)(R >> 6);
+    const int ng = BN >> gs_shift;          // groups per tile row: 4, 2, 1
+    const int64_t g_first = k0 >> gs_shift;
+
+    if (wave >= 4) {
+        // ---------------------------------------------------------- producers
+        if (RQ_K64_PPRIO) __builtin_amdgcn_s_setprio(RQ_K64_PPRIO);
+        const int pt = tid - 256, pw = wave - 4;
+        typedef const __attribute__((address_space(1))) u32x4_t* gv_t;
+        uint32_t xoff[8], xdst[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int row = (pw * 8 + i) * 8 + (lane >> 3);
+            const int chunk = lane & 7;
+            int64_t grow = m0 + row;
+            grow = grow < M ? grow : M - 1;
+            xoff[i] = (uint32_t)((grow - m0) * R * 2 + chunk * 16);
+            xdst[i] = (uint32_t)(row * 128 + ((chunk ^ (row & 7)) * 16));
+        }
+        const uint8_t* xbase = (const uint8_t*)(x + m0 * R);
+        // code chunks: chunk c = pt + 256 j -> weight row c / CCH, 16-byte chunk c % CCH
+        const uint32_t* wtile = wq + (k0 >> 5) * BITS;
+        // (scale, bias): thread pt < 128 loads row pt/2's ng values of array pt%2
+        const int srow = pt >> 1, sarr = pt & 1;
+        const uint16_t* sbsrc = (const uint16_t*)(sarr ? biases : scales) + g_first;
+
+        u32x4_t xv[2][8];
+        u32x4_t cv[2][NCL];
+        uint32_t sv[2][2];
+        auto load_x = [&](int st, int r) {
+            const int sc = st < nst ? st : nst - 1;
+            const uint8_t* xb = xbase + (int64_t)sc * 128;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[r][i] = *(gv_t)(xb + xoff[i]);
+        };
+        auto load_c = [&](int st, int r) {
+            const int sc = st < nst ? st : nst - 1;
+#pragma unroll
+            for (int j = 0; j < NCL; ++j) {
+                const int c = pt + 256 * j;
+                if (c < 64 * CCH) {
+                    const int64_t row = (int64_t)sc * 64 + c / CCH;
+                    cv[r][j] = *(gv_t)(wtile + row * wpr + (c % CCH) * 4);
+                }
+            }
+            if (pt < 128) {
+                const int64_t row = (int64_t)sc * 64 + srow;
+                const uint16_t* src = sbsrc + row * G;
+                if (ng == 4) {
+                    const uint2 v = *(const uint2*)src;
+                    sv[r][0] = v.x; sv[r][1] = v.y;
+                } else if (ng == 2) {
+                    sv[r][0] = *(const uint32_t*)src; sv[r][1] = 0u;
+                } else {
+                    sv[r][0] = *src; sv[r][1] = 0u;
+                }
+            }
+        };
+        auto put_c = [&](int r, uint32_t* cs, uint16_t* ss) {
+#pragma unroll
+            for (int j = 0; j < NCL; ++j) {
+                const int c = pt + 256 * j;
+                if (c < 64 * CCH) *(u32x4_t*)(cs + (c / CCH) * CW + (c % CCH) * 4) = cv[r][j];
+            }
+            if (pt < 128) {
+                uint32_t* d = (uint32_t*)(ss + sarr * 256 + srow * 4);
+                d[0] = sv[r][0];
+                d[1] = sv[r][1];
+            }
+        };
+        // dequantization unit: rows 4*rq .. 4*rq+3, columns 8*kc .. 8*kc+7
+        const int rq = pt & 15, kc = pt >> 4;
+        auto dequant = [&](const uint32_t* cs, const uint16_t* ss, uint16_t* bq) {
+            const int gl = (kc * 8) >> gs_shift;  // group of these columns within the tile
+            float v[4][8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = rq * 4 + i;
+                const int bit = kc * 8 * BITS;
+                const uint32_t* wr = cs + row * CW + (bit >> 5);
+                const uint64_t win = (uint64_t)wr[0] | ((bit & 31) + 8 * BITS > 32 ? (uint64_t)wr[1] << 32 : 0ull);
+                const int off = bit & 31;
+                const float sf = dt_traits<SDT>::to_f32(ss[row * 4 + gl]);
+                const float bf = dt_traits<SDT>::to_f32(ss[256 + row * 4 + gl]);
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    v[i][c] = fmaf(sf, (float)(uint32_t)((win >> (off + c * BITS)) & ((1u << BITS) - 1u)), bf);
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                *(u32x2_t*)(bq + (kc * 8 + c) * BLD + rq * 4) =
+                    u32x2_t{pack_bf16x2(v[0][c], v[1][c]), pack_bf16x2(v[2][c], v[3][c])};
+            }
+        };
+
+        load_x(0, 0);
+        load_x(1, 1);
+        load_c(0, 0);
+        load_c(1, 1);
+        put_c(0, cs0, ss0);
+        load_c(2, 0);
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();        // stage 0's code tile is staged
+        asm volatile("" ::: "memory");
+        for (int s0 = 0; s0 < nst; s0 += 2) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int st = s0 + u;
+                uint8_t* xs = u ? xs1 : xs0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u][i];
+                dequant(u ? cs1 : cs0, u ? ss1 : ss0, u ? bq1 : bq0);
+                put_c(u ^ 1, u ? cs0 : cs1, u ? ss0 : ss1);  // stage st+1's tiles
+                load_x(st + 2, u);
+                load_c(st + 3, u ^ 1);
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+            }
+        }
+        return;
+    }
+
+    // -------------------------------------------------------------- consumers
+    if (RQ_K64_CPRIO) __builtin_amdgcn_s_setprio(RQ_K64_CPRIO);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lg = lane >> 4, lr = lane & 15;
+    f32x4_t acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    uint32_t aoff[2][TM];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+            const int row = wm * 128 + a * 16 + lr;
+            aoff[h][a] = (uint32_t)(row * 128 + (((h * 4 + lg) ^ (row & 7)) * 16));
+        }
+    const uint32_t boff = (uint32_t)((wn * WN + lr) * BLD + lg * 8);
+
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // the producers' initial barrier
+    asm volatile("" ::: "memory");
+    for (int s0 = 0; s0 < nst; s0 += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int st = s0 + u;
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // own LDS reads of the previous stage are done
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (st < nst) {
+                const uint8_t* xs = u ? xs1 : xs0;
+                const uint16_t* bq = u ? bq1 : bq0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    bf16x8_t af[TM], bf[TN];
+#pragma unroll
+                    for (int a = 0; a < TM; ++a)
+                        af[a] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
+#pragma unroll
+                    for (int b = 0; b < TN; ++b)
+                        bf[b] = __builtin_bit_cast(
+                            bf16x8_t, *(const u32x4_t*)(bq + boff + b * 16 * BLD + h * 32));
+#pragma unroll
+                    for (int a = 0; a < TM; ++a)
+#pragma unroll
+                        for (int b = 0; b < TN; ++b)
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bf[b],
+                                                                                acc[a][b], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int64_t n = k0 + wn * WN + b * 16 + lr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t m = m0 + wm * 128 + a * 16 + 4 * lg + i;
+                if (m < M && n < K) store_dt(y, y_dt, m * K + n, acc[a][b][i]);
+            }
+        }
+}
+
 }  // namespace
 
 namespace rq {
@@ -1566,6 +1803,24 @@ hipError_t RQ_CAT(launch_qmm_n_b, RQ_BITS)(const void* x, int x_dt, const uint32
                                       const void* scales, const void* biases, int sb_dt,
                                       int64_t m, int64_t rows, int64_t cols, int gs, void* y,
                                       int y_dt, hipStream_t stream) {
+    // warp-specialised transposed GEMM: bf16 dY, 16-bit aligned scales,
+    // whole stages of 64 weight rows and 128 output columns
+    if (m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 && rows % 64 == 0 &&
+        cols % 128 == 0 && ((uintptr_t)x & 15) == 0 &&
+        (((uintptr_t)scales | (uintptr_t)biases) & 7) == 0) {
+        const int tm = (int)((m + 255) / 256);
+        const int tn = (int)(cols / 128);
+        const int blocks = ((tm * tn + 7) / 8) * 8;
+        if (sb_dt == RQ_BF16)
+            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_BF16>), dim3(blocks), dim3(kWsBlock), 0,
+                               stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
+                               __builtin_ctz(gs), y, y_dt, tm, tn);
+        else
+            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_F16>), dim3(blocks), dim3(kWsBlock), 0,
+                               stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
+                               __builtin_ctz(gs), y, y_dt, tm, tn);
+        return hipGetLastError();
+    }
     constexpr int BM = 128;
     const dim3 grid((unsigned)((cols + BN - 1) / BN), (unsigned)((m + BM - 1) / BM));
     const int gs_shift = __builtin_ctz(gs);

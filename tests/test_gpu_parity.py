@@ -204,6 +204,38 @@ def test_qmm_n_parity(O, rq, dev, bits, gs, M):
     rel_check(y, ref, what=f"qmm_n b{bits} g{gs} M{M}")
 
 
+@pytest.mark.parametrize("M", [256, 300])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_qmm_n_warp_specialised_parity(O, rq, dev, bits, gs, M):
+    """transpose=False at M >= 256 with R % 64 == 0 and K % 128 == 0: the
+    warp-specialised kernel (partial M tile at M=300)."""
+    R, K = 192, 384
+    w = weights(R, K, 19 * bits + gs)
+    wq, s, b = O.quantize(w, gs, bits)
+    dy = acts(M, R, M + 3)
+    say(f"qmm_n ws bits={bits} gs={gs} M={M}")
+    y = rq.quantized_matmul(dy.to(dev), wq.to(dev), s.to(dev), b.to(dev), False, gs, bits)
+    ref = O.quantized_matmul(dy, wq, s, b, False, gs, bits, out_dtype=torch.float32, weights="exact")
+    rel_check(y, ref, what=f"qmm_n ws b{bits} g{gs} M{M}")
+
+
+@pytest.mark.parametrize("M", [256, 300])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_qmm_t_k64_parity(O, rq, dev, bits, gs, M):
+    """transpose=True at M >= 256 with whole 8-group chunks: the 64-wide-stage
+    warp-specialised kernel (partial M and N tiles)."""
+    R, K = 200, 8 * gs * 2
+    w = weights(R, K, 23 * bits + gs)
+    wq, s, b = O.quantize(w, gs, bits)
+    x = acts(M, K, M + 5)
+    say(f"qmm_t k64 bits={bits} gs={gs} M={M}")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
+    ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
+    rel_check(y, ref, what=f"qmm_t k64 b{bits} g{gs} M{M}")
+
+
 @pytest.mark.parametrize("R", [130, 77, 64])
 def test_qmm_n_unaligned_rows(O, rq, dev, R):
     """Row counts whose activation rows are not 16-byte multiples (scalar loads)."""
