@@ -360,30 +360,41 @@ def main():
                 f()
         tpc = time_region(torch, per_call, max(3, args.steps // 4), 1)
         extra["decode_m1_one_launch_per_projection_gbs"] = round(total_wbytes / tpc / 1e9, 2)
-        # prefill GEMM, config 3 at M=4096
+        # prefill GEMM, config 3 (RWKV-7 2.9B shapes) at M = 4096 (aggregate) and
+        # 2048 / 512; the transposed product (QLoRA dX) at M = 4096
         pre = {}
         tot_flops, tot_t = 0.0, 0.0
         for R, K in ((2560, 2560), (10240, 2560), (2560, 10240)):
             g = torch.Generator(device=dev).manual_seed(3_000_000 + R)
             w = (torch.randn(R, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
             wq, s, b = rwkvq.quantize(w, gs, bits)
-            x = torch.randn(4096, K, device=dev).to(torch.bfloat16)
-            t = time_region(torch, lambda: rwkvq.quantized_matmul(x, wq, s, b, True, gs, bits),
-                            max(5, args.steps // 2), 2)
-            fl = 2.0 * 4096 * R * K
-            pre[f"{R}x{K}"] = round(fl / t / 1e12, 1)
-            tot_flops += fl
-            tot_t += t
-            # transposed (QLoRA backward)
+            for M in (4096, 2048, 512):
+                x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+                t = time_region(torch, lambda: rwkvq.quantized_matmul(x, wq, s, b, True, gs, bits),
+                                max(5, args.steps // 2), 2)
+                fl = 2.0 * M * R * K
+                pre[f"{R}x{K}_M{M}"] = round(fl / t / 1e12, 1)
+                if M == 4096:
+                    tot_flops += fl
+                    tot_t += t
             dy = torch.randn(4096, R, device=dev).to(torch.bfloat16)
             tn = time_region(torch, lambda: rwkvq.quantized_matmul(dy, wq, s, b, False, gs, bits),
                              max(5, args.steps // 2), 2)
-            pre[f"{R}x{K}_transposed"] = round(fl / tn / 1e12, 1)
+            pre[f"{R}x{K}_M4096_transposed"] = round(2.0 * 4096 * R * K / tn / 1e12, 1)
             del w
         agg = tot_flops / tot_t / 1e12
         extra["prefill_qmm_m4096"] = {"tflops": round(agg, 1),
                                       "frac_of_bf16_peak": round(agg / BF16_PEAK_TFLOPS, 4),
                                       "per_shape_tflops": pre}
+        # QLoRA backward, config 4 (D=2048, M = 8 x 512): dX = dY . W^ per projection
+        bwd = {}
+        for name, R, K in (("rkvo", D, D), ("ffn_key", FFN, D), ("ffn_value", D, FFN)):
+            wq, s, b = ws[PROJ.index(next(p for p in PROJ if p[0] == ("r" if name == "rkvo" else name)))]
+            dy = torch.randn(4096, R, device=dev).to(torch.bfloat16)
+            tn = time_region(torch, lambda: rwkvq.quantized_matmul(dy, wq, s, b, False, gs, bits),
+                             max(5, args.steps // 2), 2)
+            bwd[name] = round(2.0 * 4096 * R * K / tn / 1e12, 1)
+        extra["qlora_dx_m4096_tflops"] = bwd
         result["extra"] = extra
 
     if not args.no_cpu:
