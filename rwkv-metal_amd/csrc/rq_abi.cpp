@@ -262,7 +262,7 @@ int rq_grouped_plan_init(const rq_problem* problems, int n, rq_dtype x_dt, rq_dt
     std::vector<int> order;
     for (int i = 0; i < n; ++i) {
         if (problems[i].rows == 0) continue;
-        if (!rq::qmv_stream_covers(problems[i], sb_dt, m, group_size))
+        if (!rq::qmv_stream_covers(problems[i], sb_dt, m, group_size, bits))
             return fail(RQ_EUNSUPPORTED,
                         "rq_grouped_plan_init: problem %d is outside the planned GEMV (needs "
                         "m <= 4, 16-bit scales, cols %% 512 == 0, 16-byte aligned scales/biases, "
@@ -281,7 +281,7 @@ int rq_grouped_plan_init(const rq_problem* problems, int n, rq_dtype x_dt, rq_dt
     size_t lds = 0;
     for (int i = 0; i < nn; ++i) {
         descs[i] = problems[order[i]];
-        lds = std::max(lds, rq::qmv_stream_lds(m, descs[i].cols, group_size));
+        lds = std::max(lds, rq::qmv_stream_lds(m, descs[i].cols, group_size, bits));
     }
     const int64_t nblocks = plan_blocks(descs.data(), nn);
     const int64_t dbytes = plan_desc_bytes(nn);

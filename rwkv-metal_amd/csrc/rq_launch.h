@@ -35,10 +35,10 @@ struct QmvTable {
 constexpr int kQmvLdsBudget = 64 * 1024;  // LDS bytes a GEMV block may stage
 constexpr int kQmvRowsPerBlock = 64;      // rows of one streamed-GEMV block
 // LDS bytes of a streamed-GEMV block for one problem shape.
-size_t qmv_stream_lds(int64_t m, int64_t cols, int gs);
+size_t qmv_stream_lds(int64_t m, int64_t cols, int gs, int bits);
 // Whether the streamed GEMV covers a problem (16-bit scales, cols % 512 == 0,
 // 16-byte aligned scales/biases, staging within budget).
-bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs);
+bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs, int bits);
 hipError_t launch_qmv_table(const QmvTable& t, int blocks, int sb_dt, int gs, int bits,
                             size_t lds, hipStream_t stream);
 

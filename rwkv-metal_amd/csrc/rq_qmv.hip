@@ -697,6 +697,35 @@ typedef const RQ_GLOBAL uint32_t* gptr_u32;
 typedef const RQ_GLOBAL uint16_t* gptr_u16;
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
+// 3-bit codes of a lane's 64-code slice (six words, LSB first) as bf16 pairs
+// (c_p, c_{p+4}), p = 32h + 8j + i, i = 0..3 -- the pair order of the 4-bit
+// path, so x is staged the same way.  One funnel shift puts c_p at bits 4..6
+// of the low half and c_{p+4} (12 bits further) at bits 0..2 of the high
+// half; one v_and_or_b32 with mask 0x00070070 and exponent bits 0x43004100
+// then gives the exact bf16 values 8 + c_p (0x4100 | c << 4: unit 1/16 at
+// 8.0) and 128 + c_{p+4}.  Low-half positions are the elements k % 8 < 4.
+RQ_DEV PairConsts pair3_consts() {
+    PairConsts c{0x00070070u, 0x43004100u};
+    asm volatile("" : "+v"(c.mask), "+v"(c.magic));
+    return c;
+}
+RQ_DEV void codes3_to_bf16_pairs(const uint32_t* w, int h, int j, uint32_t* out,
+                                 const PairConsts& k) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int pos = 3 * (32 * h + 8 * j + i) - 4;  // bit of the slice at bit 0 of v
+        uint32_t v;
+        if (pos < 0) {
+            v = w[0] << (-pos);
+        } else {
+            const int wi = pos >> 5, s = pos & 31;
+            // the last word needs no funnel: c_{p+4} ends at bit s + 18 < 32 there
+            v = s == 0 ? w[wi] : (wi < 5 ? __builtin_amdgcn_alignbit(w[wi + 1], w[wi], s) : w[wi] >> s);
+        }
+        out[i] = (v & k.mask) | k.magic;
+    }
+}
+
 template <int BITS>
 RQ_DEV void load_two_runs(gptr_u32 p, uint32_t* out) {
     // 2*BITS contiguous words; 16-byte aligned for even BITS, 8-byte for odd
@@ -774,7 +803,10 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
     const int GX = (int)(K >> XSH);
     const uint32_t xsum_f = (uint32_t)((2 * kZeroElems + (((int64_t)M * K * 2 + 15) & ~15ll)) >> 2);
     float* xsum = (float*)lds + xsum_f;
-    uint8_t* win = (uint8_t*)(xsum + (((int64_t)M * GX + 3) & ~3ll)) + wave * W::WAVE_BYTES;
+    // 3-bit: a second array of sums over the low-half positions (k % 8 < 4)
+    constexpr int NSUM = BITS == 3 ? 2 : 1;
+    const uint32_t xlo_d = (uint32_t)(((int64_t)M * GX + 3) & ~3ll);  // offset of that array
+    uint8_t* win = (uint8_t*)(xsum + NSUM * xlo_d) + wave * W::WAVE_BYTES;
     if (threadIdx.x < kZeroElems / 8) *(u32x4_t*)&lds[threadIdx.x * 8] = u32x4_t{0u, 0u, 0u, 0u};
     {
         const void* __restrict__ x = P.x;
@@ -799,20 +831,29 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
             uint32_t pr[4];
             reorder_pairs(d, pr);
             *(u32x4_t*)&xs[e * 8] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
-            float sum = 0.f;
+            float sum = 0.f, lo = 0.f;
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                sum += __uint_as_float(d[q] << 16) + __uint_as_float(d[q] & 0xffff0000u);
+            for (int q = 0; q < 4; ++q) {
+                const float v = __uint_as_float(d[q] << 16) + __uint_as_float(d[q] & 0xffff0000u);
+                sum += v;
+                if (q < 2) lo += v;
+            }
 #pragma unroll
-            for (int w = 1; w < (1 << (XSH - 3)); w <<= 1) sum += __shfl_xor(sum, w, 64);
-            if ((e & ((1 << (XSH - 3)) - 1)) == 0) xsum[e >> (XSH - 3)] = sum;
+            for (int w = 1; w < (1 << (XSH - 3)); w <<= 1) {
+                sum += __shfl_xor(sum, w, 64);
+                if constexpr (BITS == 3) lo += __shfl_xor(lo, w, 64);
+            }
+            if ((e & ((1 << (XSH - 3)) - 1)) == 0) {
+                xsum[e >> (XSH - 3)] = sum;
+                if constexpr (BITS == 3) xsum[xlo_d + (e >> (XSH - 3))] = lo;
+            }
         }
     }
     __syncthreads();
     if (row0 >= R) return;  // no rows for this wave (after the barrier)
 
     // ---- per-lane constants
-    const PairConsts kc = pair_consts();
+    const PairConsts kc = BITS == 3 ? pair3_consts() : pair_consts();
     // A: lane (lr, lg) supplies row m' = lr on lane group lg's k-slice; that
     // row carries x[c*4 + lr%4] when its slot lr/4 is lg.
     uint32_t a_idx[NMC], a_step[NMC];
@@ -855,7 +896,7 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
             load_codes(st + NS - 1, cw[(t + NS - 1) % NS]);
             if (st < nst) {
                 // scales and biases of this lane's group(s) at this stage
-                float sc[GL], cb[GL];
+                float sc[GL], cb[GL], cl[GL];
 #pragma unroll
                 for (int q = 0; q < GL; ++q) {
                     const uint16_t sr = *(const uint16_t*)(win_r + (t * W::GPS + q) * 2);
@@ -863,6 +904,7 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
                     sc[q] = raw_to_f32<SDT>(sr);
                     const float bi = raw_to_f32<SDT>(br);
                     cb[q] = (BITS == 8) ? bi : fmaf(sc[q], -128.f, bi);
+                    cl[q] = 120.f * sc[q];  // 3-bit: low-half positions carry 8, not 128
                 }
                 f32x4_t d[NMC][2];
 #pragma unroll
@@ -871,7 +913,8 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         uint32_t pr[4];
-                        codes_to_bf16_pairs<BITS>(cw[t] + h * BITS, j, pr, kc);
+                        if constexpr (BITS == 3) codes3_to_bf16_pairs(cw[t], h, j, pr, kc);
+                        else codes_to_bf16_pairs<BITS>(cw[t] + h * BITS, j, pr, kc);
                         bop[j] = as_bf16x8(pr[0], pr[1], pr[2], pr[3]);
                     }
 #pragma unroll
@@ -892,6 +935,12 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
 #pragma unroll
                     for (int i = 0; i < MI; ++i) {
                         const float* xg = (const float*)lds + g_idx[c][i] + (uint32_t)st * g_step[c][i];
+                        if constexpr (BITS == 3) {
+                            const float* xl = xg + xlo_d;
+#pragma unroll
+                            for (int q = 0; q < GL; ++q)
+                                acc[c][i] = fmaf(cl[q], xl[q], acc[c][i]);
+                        }
                         if constexpr (GL == 2) {
                             acc[c][i] = fmaf(sc[0], d[c][0][i], fmaf(cb[0], xg[0], acc[c][i]));
                             acc[c][i] = fmaf(sc[1], d[c][1][i], fmaf(cb[1], xg[1], acc[c][i]));
@@ -1026,9 +1075,9 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
     for (int i = 0; i < n; ++i) rowblocks += (probs[i]->rows + 15) / 16;
     const int cfg = rowblocks >= RQ_QMV_BIG_MIN ? 2 : (rowblocks >= 2048 ? 1 : 0);
     bool streamed = cfg >= 1 && RQ_QMV_STREAM;
-    for (int i = 0; i < n && streamed; ++i) streamed = qmv_stream_covers(*probs[i], sb_dt, m, gs);
+    for (int i = 0; i < n && streamed; ++i) streamed = qmv_stream_covers(*probs[i], sb_dt, m, gs, RQ_BITS);
     if (streamed) {
-        const size_t lds = qmv_stream_lds(m, K, gs);
+        const size_t lds = qmv_stream_lds(m, K, gs, RQ_BITS);
         for (int base = 0; base < n; base += RQ_MAX_GROUPED) {
             const int cnt = (n - base) < RQ_MAX_GROUPED ? (n - base) : RQ_MAX_GROUPED;
             QmvArgs a;
@@ -1092,20 +1141,21 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
 }
 
 #if RQ_BITS == 4  // bit-width independent helpers: defined in one unit only
-size_t qmv_stream_lds(int64_t m, int64_t cols, int gs) {
+size_t qmv_stream_lds(int64_t m, int64_t cols, int gs, int bits) {
     const int wave_bytes = gs == 32 ? StreamWin<5>::WAVE_BYTES
                          : (gs == 64 ? StreamWin<6>::WAVE_BYTES : StreamWin<7>::WAVE_BYTES);
     const int xg = gs < 64 ? gs : 64;  // elements per activation sum
+    const size_t nsum = bits == 3 ? 2 : 1;  // 3-bit: sums over all and over low-half positions
     return 2 * kZeroElems + (((size_t)m * cols * 2 + 15) & ~(size_t)15) +
-           (((size_t)m * (cols / xg) * 4 + 15) & ~(size_t)15) + 4 * (size_t)wave_bytes;
+           nsum * (((size_t)m * (cols / xg) * 4 + 15) & ~(size_t)15) + 4 * (size_t)wave_bytes;
 }
-bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs) {
+bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs, int bits) {
     // m > 4 takes ceil(m/4) passes of 4 slots here; the LDS-staged kernel's
     // 8-row slots (gs 64) do less MFMA work there
     return m <= 4 && sb_dt != RQ_F32 && p.cols % 512 == 0 &&
            p.rows <= (int64_t)65536 * kQmvRowsPerBlock &&
            (((uintptr_t)p.scales | (uintptr_t)p.biases) & 15) == 0 &&
-           qmv_stream_lds(m, p.cols, gs) <= (size_t)kQmvLdsBudget;
+           qmv_stream_lds(m, p.cols, gs, bits) <= (size_t)kQmvLdsBudget;
 }
 #endif
 

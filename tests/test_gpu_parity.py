@@ -463,16 +463,18 @@ def test_planned_many_problems_one_launch(O, rq, dev):
 
 
 @pytest.mark.parametrize("M", [1, 4])
-def test_streamed_single_launch_path(O, rq, dev, M):
+@pytest.mark.parametrize("bits", [3, 4, 8])
+def test_streamed_single_launch_path(O, rq, dev, bits, M):
     """A single problem big enough (>= 2048 16-row blocks) for the streamed
-    kernel through rq_qmm itself."""
+    kernel through rq_qmm itself (3-bit: codes straddling words, the
+    mixed-offset pair extraction)."""
     R, K = 32768 + 40, 1024
-    w = weights(R, K, 8100)
-    wq, s, b = O.quantize(w, 64, 4)
+    w = weights(R, K, 8100 + bits)
+    wq, s, b = O.quantize(w, 64, bits)
     x = acts(M, K, 8100)
-    say(f"streamed single M={M}")
-    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
-    rel_check(y, O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32, weights="exact"))
+    say(f"streamed single bits={bits} M={M}")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, bits)
+    rel_check(y, O.quantized_matmul(x, wq, s, b, True, 64, bits, out_dtype=torch.float32, weights="exact"))
 
 
 # ---------------------------------------------- autograd / modules / LoRA
