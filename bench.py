@@ -11,8 +11,11 @@ a single launch over the 145 independent GEMVs.  `value` = effective weight-stre
 inputs resident in HBM.
 
 Alongside: the same sweep at M=8, one GEMV launch per projection, the prefill
-GEMM (RWKV-7 2.9B shapes, M=4096) in TFLOP/s, and the CPU
-oracle's GEMV timed on the host cores on a bounded sample.
+GEMM (RWKV-7 2.9B shapes, M=4096/2048/512) and its
+transposed product in TFLOP/s, the QLoRA dX product at config-4 shapes, the
+config-5 mixed-bit model (7.2B shapes, 3-bit layers + 8-bit head: decode
+sweep GB/s, prefill M=2048 TFLOP/s), and the CPU oracle's GEMV timed on the
+host cores on a bounded sample.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
 
@@ -50,8 +53,11 @@ def weight_bytes(R, K, bits=4, gs=64, sb=2):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # One step of the headline is ~0.13 ms: 100 warmup steps (~13 ms of
+    # back-to-back launches) get past the clock/power transient that follows
+    # the quantization phase and any idle gap; 200 timed steps are ~26 ms.
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bounded CPU-baseline sample length")
     ap.add_argument("--no-cpu", action="store_true")
@@ -208,6 +214,52 @@ def make_sweep(rq, torch, dev, M, bits=4, gs=64):
     return probs, qgbs
 
 
+def config5(torch, rq, dev, args):
+    """RWKV-7 7.2B shapes (D=4096, FFN 16384, vocab 65536),
+    3-bit g64 r/k/v/o and FFN, 8-bit g64 head, bf16 scales/biases.  Decode:
+    all 32 layers' 3-bit projections in one planned launch plus the 8-bit
+    head in a second, M=1, GB/s of packed weights + scales/biases.  Prefill:
+    each shape at M=2048, TFLOP/s."""
+    D5, F5, V5, L5 = 4096, 16384, 65536, 32
+    shapes = [(D5, D5)] * 4 + [(F5, D5), (D5, F5)]
+    ws, xs, nbytes = [], [], 0
+    for layer in range(L5):
+        for i, (R, K) in enumerate(shapes):
+            g = torch.Generator(device=dev).manual_seed(5_000_000 + 10 * layer + i)
+            w = (torch.randn(R, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            ws.append(rq.quantize(w, 64, 3))
+            xs.append(torch.randn(1, K, generator=g, device=dev).to(torch.bfloat16))
+            nbytes += weight_bytes(R, K, 3)
+            del w
+    g = torch.Generator(device=dev).manual_seed(5_999_999)
+    w = (torch.randn(V5, D5, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    head = rq.quantize(w, 64, 8)
+    del w
+    xh = torch.randn(1, D5, generator=g, device=dev).to(torch.bfloat16)
+    nbytes += weight_bytes(V5, D5, 8)
+    p3 = rq.GroupedQmv(xs, ws, 64, 3)
+    p8 = rq.GroupedQmv([xh], [head], 64, 8)
+
+    def step():
+        p3.run()
+        p8.run()
+    t = time_region(torch, step, max(5, args.steps // 2), 2)
+    out = {"decode_m1_gbs": round(nbytes / t / 1e9, 1),
+           "decode_weight_bytes": nbytes,
+           "decode_planned": p3.plan is not None and p8.plan is not None}
+    del p3, xs
+    pre = {}
+    for name, R, K, wq3 in (("rkvo", D5, D5, ws[0]), ("ffn_key", F5, D5, ws[4]),
+                            ("ffn_value", D5, F5, ws[5]), ("head_8bit", V5, D5, head)):
+        bits = 8 if name == "head_8bit" else 3
+        x = torch.randn(2048, K, device=dev).to(torch.bfloat16)
+        tt = time_region(torch, lambda: rq.quantized_matmul(x, *wq3, True, 64, bits),
+                         max(5, args.steps // 4), 2)
+        pre[name] = round(2.0 * 2048 * R * K / tt / 1e12, 1)
+    out["prefill_m2048_tflops"] = pre
+    return out
+
+
 def time_region(torch, fn, steps, warmup):
     for _ in range(warmup):
         fn()
@@ -219,25 +271,6 @@ def time_region(torch, fn, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / 1e3 / steps
-
-
-def call_duration(torch, fn, reps):
-    """Mean HIP-event duration of one fn() call, one event pair per call,
-    recorded on torch's current stream -- the stream the library launches
-    on.  Each measured call follows an unmeasured one, so the GPU is busy
-    while the host enqueues the first event, the call and the second event:
-    the pair then brackets the kernel, not the host's submission latency.
-    A synchronisation between rounds keeps the rounds apart."""
-    tot = 0.0
-    for _ in range(reps):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        fn()
-        a.record()
-        fn()
-        b.record()
-        b.synchronize()
-        tot += a.elapsed_time(b) / 1e3
-    return tot / reps
 
 
 def cpu_baseline(torch, seconds):
@@ -305,12 +338,14 @@ def main():
     value = total_wbytes / t_step / 1e9
 
     # The step is one planned grouped call (rq_grouped_plan_run): ONE launch
-    # of qmv_stream_table over all 145 problems (3168 blocks of 64 rows,
-    # K=8192 blocks first).  Average launch = event time of the call.
+    # of qmv_stream_table over all 145 problems (7936 blocks of 64 rows,
+    # K=8192 blocks first).  Average launch duration = the timed region's
+    # HIP-event time (events on torch's current stream, the stream the
+    # library launches on) over the launches in it; the launches run back to
+    # back, so the region is kernel time.
     assert plan.plan is not None, "the config-2 sweep must run on the planned GEMV"
     launches = 1
-    call_t = call_duration(torch, plan.run, max(5, args.steps))
-    avg_launch = call_t / launches
+    avg_launch = t_step / launches
     bytes_per_launch = total_wbytes / launches
     achieved = bytes_per_launch / avg_launch / 1e9
     result = {
@@ -395,6 +430,8 @@ def main():
                              max(5, args.steps // 2), 2)
             bwd[name] = round(2.0 * 4096 * R * K / tn / 1e12, 1)
         extra["qlora_dx_m4096_tflops"] = bwd
+        del ws, xs, xs8, outs8, plan8, singles
+        extra["config5_mixed_bit"] = config5(torch, rwkvq, dev, args)
         result["extra"] = extra
 
     if not args.no_cpu:

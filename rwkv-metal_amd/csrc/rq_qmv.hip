@@ -770,7 +770,10 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
         int g0 = it * W::GPI + part;
         g0 = g0 < G - W::GPI / 2 ? g0 : G - W::GPI / 2;  // past the last stage: any valid data
         win_t v;
-        const gptr_u16 src = sbrow + g0;
+        // The window after the last iteration is never read: load the staged
+        // activations instead (L2-resident, 16-byte aligned, >= 1 KB), so the
+        // load stays unconditional without fetching scale lines again.
+        const gptr_u16 src = it < niter ? sbrow + g0 : (gptr_u16)P.x;
         if constexpr (W::LB == 32) {
             const u32x4_t a = *(const RQ_GLOBAL u32x4_t*)src, b = *((const RQ_GLOBAL u32x4_t*)src + 1);
             v.w[0] = a[0]; v.w[1] = a[1]; v.w[2] = a[2]; v.w[3] = a[3];
