@@ -40,6 +40,7 @@ for _p in (ROOT, os.path.join(ROOT, "rwkv-metal_amd")):
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 flop/clk)
+GEMM_WARMUP = 10               # untimed GEMM launches before each timed GEMM region
 D, FFN, VOCAB, LAYERS = 2048, 8192, 65536, 24
 PROJ = [("r", D, D), ("k", D, D), ("v", D, D), ("o", D, D), ("ffn_key", FFN, D),
         ("ffn_value", D, FFN)]
@@ -248,16 +249,32 @@ def config5(torch, rq, dev, args):
            "decode_weight_bytes": nbytes,
            "decode_planned": p3.plan is not None and p8.plan is not None}
     del p3, xs
+    gemm_steady_state(torch, rq, dev)
     pre = {}
     for name, R, K, wq3 in (("rkvo", D5, D5, ws[0]), ("ffn_key", F5, D5, ws[4]),
                             ("ffn_value", D5, F5, ws[5]), ("head_8bit", V5, D5, head)):
         bits = 8 if name == "head_8bit" else 3
         x = torch.randn(2048, K, device=dev).to(torch.bfloat16)
-        tt = time_region(torch, lambda: rq.quantized_matmul(x, *wq3, True, 64, bits),
-                         max(5, args.steps // 4), 2)
+        tt = time_region(torch, rq.BoundQmm(x, *wq3, True, 64, bits).run,
+                         max(5, args.steps // 4), GEMM_WARMUP)
         pre[name] = round(2.0 * 2048 * R * K / tt / 1e12, 1)
     out["prefill_m2048_tflops"] = pre
     return out
+
+
+def gemm_steady_state(torch, rq, dev, seconds=0.15):
+    """Untimed MFMA-heavy GEMM work before the GEMM measurements: coming from
+    the memory-bound decode sweeps, the first ~100 ms of back-to-back GEMMs
+    run 5-20 % slower while the clocks settle, and a prefill or training
+    step is steady-state GEMM work."""
+    w = (torch.randn(10240, 2560, device=dev) * 0.02).to(torch.bfloat16)
+    run = rq.BoundQmm(torch.randn(4096, 2560, device=dev).to(torch.bfloat16),
+                      *rq.quantize(w, 64, 4), True, 64, 4).run
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            run()
+        torch.cuda.synchronize()
 
 
 def time_region(torch, fn, steps, warmup):
@@ -399,22 +416,23 @@ def main():
         # 2048 / 512; the transposed product (QLoRA dX) at M = 4096
         pre = {}
         tot_flops, tot_t = 0.0, 0.0
+        gemm_steady_state(torch, rwkvq, dev)
         for R, K in ((2560, 2560), (10240, 2560), (2560, 10240)):
             g = torch.Generator(device=dev).manual_seed(3_000_000 + R)
             w = (torch.randn(R, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
             wq, s, b = rwkvq.quantize(w, gs, bits)
             for M in (4096, 2048, 512):
                 x = torch.randn(M, K, device=dev).to(torch.bfloat16)
-                t = time_region(torch, lambda: rwkvq.quantized_matmul(x, wq, s, b, True, gs, bits),
-                                max(5, args.steps // 2), 2)
+                t = time_region(torch, rwkvq.BoundQmm(x, wq, s, b, True, gs, bits).run,
+                                max(5, args.steps // 2), GEMM_WARMUP)
                 fl = 2.0 * M * R * K
                 pre[f"{R}x{K}_M{M}"] = round(fl / t / 1e12, 1)
                 if M == 4096:
                     tot_flops += fl
                     tot_t += t
             dy = torch.randn(4096, R, device=dev).to(torch.bfloat16)
-            tn = time_region(torch, lambda: rwkvq.quantized_matmul(dy, wq, s, b, False, gs, bits),
-                             max(5, args.steps // 2), 2)
+            tn = time_region(torch, rwkvq.BoundQmm(dy, wq, s, b, False, gs, bits).run,
+                             max(5, args.steps // 2), GEMM_WARMUP)
             pre[f"{R}x{K}_M4096_transposed"] = round(2.0 * 4096 * R * K / tn / 1e12, 1)
             del w
         agg = tot_flops / tot_t / 1e12
@@ -426,8 +444,8 @@ def main():
         for name, R, K in (("rkvo", D, D), ("ffn_key", FFN, D), ("ffn_value", D, FFN)):
             wq, s, b = ws[PROJ.index(next(p for p in PROJ if p[0] == ("r" if name == "rkvo" else name)))]
             dy = torch.randn(4096, R, device=dev).to(torch.bfloat16)
-            tn = time_region(torch, lambda: rwkvq.quantized_matmul(dy, wq, s, b, False, gs, bits),
-                             max(5, args.steps // 2), 2)
+            tn = time_region(torch, rwkvq.BoundQmm(dy, wq, s, b, False, gs, bits).run,
+                             max(5, args.steps // 2), GEMM_WARMUP)
             bwd[name] = round(2.0 * 4096 * R * K / tn / 1e12, 1)
         extra["qlora_dx_m4096_tflops"] = bwd
         del ws, xs, xs8, outs8, plan8, singles

@@ -1251,6 +1251,83 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_wsr(
 }
 
 
+// Two outputs of dtype dt (bf16 or f16) packed in one dword, RNE.
+RQ_DEV uint32_t pack2_dt(int dt, float lo, float hi) {
+    return dt == RQ_BF16 ? pack_bf16x2(lo, hi) : (f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16));
+}
+
+// Store one wave's 128 x WN output tile of a k64 GEMM.  The MFMAs ran with
+// the weight fragment as the A operand, so lane (lg = lane / 16, lr =
+// lane % 16) of 16x16 tile (a, b) holds the outputs of row a*16 + lr at
+// columns b*16 + 4*lg .. +3: four consecutive columns of one row.
+//  * fp32 outputs leave as one 16-byte store per tile and lane.
+//  * 16-bit outputs go through a wave-private LDS strip of 32 rows (stg,
+//    32 * (2*WN + 16) bytes) and leave as whole 16-byte chunks of the row
+//    segment (2*WN bytes per row), instead of 2-byte scattered stores.
+// Rows >= nrows and columns >= ld are not written.
+template <int TM, int TN>
+RQ_DEV void store_wave_tile(const f32x4_t (&acc)[TM][TN], uint8_t* stg, void* __restrict__ y,
+                            int y_dt, int64_t nrows, int64_t ld, int64_t r0, int64_t c0,
+                            int lane) {
+    constexpr int WN = TN * 16;
+    const int lg = lane >> 4, lr = lane & 15;
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    if (y_dt == RQ_F32) {
+        const bool vec = (((uintptr_t)y & 15) == 0) && (ld & 3) == 0;
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < TN; ++b) {
+                const int64_t m = r0 + a * 16 + lr, n = c0 + b * 16 + 4 * lg;
+                if (m >= nrows) continue;
+                float* dst = (float*)y + m * ld + n;
+                if (vec && n + 4 <= ld) {
+                    *(f32x4_t*)dst = acc[a][b];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (n + r < ld) dst[r] = acc[a][b][r];
+                }
+            }
+        return;
+    }
+    constexpr int RB = WN * 2;    // bytes per output row of the wave tile
+    constexpr int SR = RB + 16;   // staging row stride (16-byte aligned)
+    constexpr int CPR = RB / 16;  // 16-byte chunks per row
+    constexpr int NCH = 32 * CPR; // chunks per 32-row strip
+    const bool vec = (((uintptr_t)y & 15) == 0) && (ld & 7) == 0;
+    uint16_t* yo = (uint16_t*)y;
+#pragma unroll
+    for (int a2 = 0; a2 < TM; a2 += 2) {
+#pragma unroll
+        for (int aa = 0; aa < 2; ++aa)
+#pragma unroll
+            for (int b = 0; b < TN; ++b) {
+                const f32x4_t v = acc[a2 + aa][b];
+                *(u32x2_t*)(stg + (aa * 16 + lr) * SR + (b * 16 + 4 * lg) * 2) =
+                    u32x2_t{pack2_dt(y_dt, v[0], v[1]), pack2_dt(y_dt, v[2], v[3])};
+            }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the strip is in LDS
+#pragma unroll
+        for (int j = 0; j < (NCH + 63) / 64; ++j) {
+            const int c = lane + 64 * j;
+            if (NCH % 64 != 0 && c >= NCH) break;
+            const int row = c / CPR, col = c % CPR;
+            const u32x4_t v = *(const u32x4_t*)(stg + row * SR + col * 16);
+            const int64_t m = r0 + a2 * 16 + row, n = c0 + col * 8;
+            if (m >= nrows) continue;
+            if (vec && n + 8 <= ld) {
+                *(u32x4_t*)(yo + m * ld + n) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (n + e < ld) yo[m * ld + n + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // strip read back before it is overwritten
+    }
+}
+
 // ------------------------------------------------------------- qmm_t_k64
 //
 // The warp-specialised GEMM with 64-element contraction stages (bf16
@@ -1445,24 +1522,17 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                     for (int a = 0; a < TM; ++a)
 #pragma unroll
                         for (int b = 0; b < TN; ++b)
-                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bf[b],
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[b], af[a],
                                                                                 acc[a][b], 0, 0, 0);
                 }
             }
         }
     }
 
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b) {
-            const int64_t n = n0 + wn * WN + b * 16 + lr;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t m = m0 + wm * 128 + a * 16 + 4 * lg + i;
-                if (m < M && n < R) store_dt(y, y_dt, m * R + n, acc[a][b][i]);
-            }
-        }
+    // after the last barrier the ring slot of stage nst - 2 (nst & 1) is read
+    // by nobody and written by nobody: 8 KB of it per wave stage the output
+    store_wave_tile<TM, TN>(acc, ((nst & 1) ? xs1 : xs0) + wave * 8192, y, y_dt, M, R,
+                            m0 + wm * 128, n0 + wn * WN, lane);
 }
 
 
@@ -1682,24 +1752,16 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                     for (int a = 0; a < TM; ++a)
 #pragma unroll
                         for (int b = 0; b < TN; ++b)
-                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bf[b],
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[b], af[a],
                                                                                 acc[a][b], 0, 0, 0);
                 }
             }
         }
     }
 
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b) {
-            const int64_t n = k0 + wn * WN + b * 16 + lr;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t m = m0 + wm * 128 + a * 16 + 4 * lg + i;
-                if (m < M && n < K) store_dt(y, y_dt, m * K + n, acc[a][b][i]);
-            }
-        }
+    // after the last barrier the ring slot of stage nst - 2 (nst & 1) is free
+    store_wave_tile<TM, TN>(acc, ((nst & 1) ? xs1 : xs0) + wave * 8192, y, y_dt, M, K,
+                            m0 + wm * 128, k0 + wn * WN, lane);
 }
 
 }  // namespace

@@ -236,6 +236,57 @@ def quantized_matmul(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor,
     return _qmm_op(x, w_q, scales, biases, bool(transpose), group_size, bits)
 
 
+class BoundQmm:
+    """One validated quantized_matmul (either transpose) with a fixed output
+    buffer: run() is a single rq_qmm call on the current stream, with no
+    per-call validation, allocation or custom-op dispatch.  For serving or
+    training loops that repeat the same product on the same buffers (and for
+    timing the kernel rather than the Python dispatch).  Same semantics and
+    output dtype as quantized_matmul; x may be overwritten in place between
+    runs."""
+
+    def __init__(self, x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor,
+                 transpose: bool = True, group_size: int = 64, bits: int = 4,
+                 out: Tensor | None = None):
+        _check_args(group_size, bits)
+        w_q = _words(w_q)
+        _float(x, "x")
+        _float(scales, "scales")
+        _on_gpu(x, w_q, scales, biases)
+        if w_q.dim() != 2:
+            raise ValueError("quantized_matmul expects a 2-D packed weight")
+        K = _check_packed(w_q, scales, biases, group_size, bits)
+        R = w_q.shape[0]
+        n_in, n_out = (K, R) if transpose else (R, K)
+        if x.shape[-1] != n_in:
+            raise ValueError(f"x has inner dimension {x.shape[-1]} but the quantized weight "
+                             f"expects {n_in} (transpose={transpose})")
+        if not x.is_contiguous():
+            raise ValueError("BoundQmm needs a contiguous x (it is read in place on every run)")
+        w_q, scales = _ready(w_q), _ready(scales)
+        biases = _ready(biases.to(scales.dtype))
+        ydt = _promote(x.dtype, scales.dtype)
+        y = out if out is not None else torch.empty(*x.shape[:-1], n_out, dtype=ydt,
+                                                    device=x.device)
+        if y.dtype != ydt or not y.is_contiguous() or tuple(y.shape) != (*x.shape[:-1], n_out):
+            raise ValueError(f"BoundQmm: output must be a contiguous {ydt} tensor of shape "
+                             f"{(*x.shape[:-1], n_out)}")
+        self._keep = (x, w_q, scales, biases)
+        self.out, self.device = y, x.device
+        m = x.numel() // x.shape[-1] if x.shape[-1] else 0
+        self._args = (x.data_ptr(), DTYPE_CODE[x.dtype], w_q.data_ptr(), scales.data_ptr(),
+                      biases.data_ptr(), DTYPE_CODE[scales.dtype], m, R, K, group_size, bits,
+                      1 if transpose else 0, y.data_ptr(), DTYPE_CODE[ydt])
+        self._empty = y.numel() == 0
+
+    def run(self) -> Tensor:
+        if not self._empty:
+            with torch.cuda.device(self.device):
+                rc = lib().rq_qmm(*self._args, torch.cuda.current_stream(self.device).cuda_stream)
+            check(rc, "quantized_matmul")
+        return self.out
+
+
 class GroupedQmv:
     """A validated set of independent decode products y_i = x_i @ W_i^T
     (m <= 16): one ctypes call and, where the planned kernel covers the

@@ -236,6 +236,29 @@ def test_qmm_t_k64_parity(O, rq, dev, bits, gs, M):
     rel_check(y, ref, what=f"qmm_t k64 b{bits} g{gs} M{M}")
 
 
+@pytest.mark.parametrize("transpose,R", [(True, 200), (True, 203), (True, 320), (False, 192)])
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float16])
+def test_qmm_k64_output_tiles(O, rq, dev, transpose, R, sdt):
+    """The 64-wide-stage GEMMs' staged output stores: bf16 outputs (bf16
+    scales) and fp32 outputs (bf16 x with f16 scales promote to fp32), whole
+    and partial tiles in both dims, and an output row length that is not a
+    multiple of 8 (R=203: element-wise tail stores)."""
+    gs, bits, M = 64, 4, 300
+    K = 8 * gs * 2
+    w = weights(R, K, 29 + R, dtype=sdt)
+    wq, s, b = O.quantize(w, gs, bits)
+    x = acts(M, K if transpose else R, R + 7)
+    say(f"qmm k64 tiles transpose={transpose} R={R} sdt={sdt}")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), transpose, gs, bits)
+    assert y.dtype == (torch.bfloat16 if sdt == torch.bfloat16 else torch.float32)
+    ref = O.quantized_matmul(x, wq, s, b, transpose, gs, bits, out_dtype=torch.float32,
+                             weights="exact")
+    rel_check(y, ref, what=f"qmm k64 tiles t{transpose} R{R} {sdt}")
+    # every output element is written: compare against the oracle element-wise
+    err = (y.double().cpu() - ref.double()).abs()
+    assert (err <= 1e-2 * ref.double().abs().max() + 1e-3).all()
+
+
 @pytest.mark.parametrize("R", [130, 77, 64])
 def test_qmm_n_unaligned_rows(O, rq, dev, R):
     """Row counts whose activation rows are not 16-byte multiples (scalar loads)."""
@@ -583,3 +606,23 @@ def test_uint32_words_accepted(O, rq, dev):
     y1 = rq.quantized_matmul(x.to(dev), wq.to(dev).view(torch.uint32), s.to(dev), b.to(dev))
     y2 = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev))
     assert torch.equal(y1, y2)
+
+
+@pytest.mark.parametrize("transpose", [True, False])
+def test_bound_qmm_matches_op(O, rq, dev, transpose):
+    """BoundQmm.run() is the same rq_qmm call as quantized_matmul, on a fixed
+    output buffer; rewriting x in place between runs changes the result."""
+    gs, bits, R, K, M = 64, 4, 192, 1024, 260
+    w = weights(R, K, 41)
+    wq, s, b = (t.to(dev) for t in O.quantize(w, gs, bits))
+    x = acts(M, K if transpose else R, 43).to(dev)
+    bound = rq.BoundQmm(x, wq, s, b, transpose, gs, bits)
+    y1 = bound.run().clone()
+    assert torch.equal(y1, rq.quantized_matmul(x, wq, s, b, transpose, gs, bits))
+    x.copy_(acts(M, x.shape[1], 47).to(dev))
+    y2 = bound.run()
+    assert y2.data_ptr() == bound.out.data_ptr()
+    assert torch.equal(y2, rq.quantized_matmul(x, wq, s, b, transpose, gs, bits))
+    assert not torch.equal(y1, y2)
+    with pytest.raises(ValueError):
+        rq.BoundQmm(x, wq, s, b, transpose, gs, bits, out=torch.empty(1, device=dev))
