@@ -338,30 +338,39 @@ __global__ __launch_bounds__(kBlock) void qmm_n_kernel(
 // tiles (shared activation rows and weight rows stay in that XCD's L2).
 
 // One run of 32 codes -> 16 dwords of bf16 pairs, ŵ = bf16(scale*code + bias),
-// using byte converts (v_cvt_f32_ubyte*) for 4- and 8-bit codes.
+// using byte converts (v_cvt_f32_ubyte0..3) for 4- and 8-bit codes.  The
+// nibble masks are hidden from the optimiser (empty asm): otherwise it folds
+// mask and byte select into one bit-field extract per code, a second VALU
+// op per code in front of a v_cvt_f32_ubyte0.  Per 8 codes at 4 bits: 3
+// mask ops, 8 converts, 8 fmas, 4 packs.
 template <int BITS>
 RQ_DEV void dequant_run_fast(const uint32_t* words, float s, float b, uint32_t* out) {
     if constexpr (BITS == 4) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            const uint32_t lo = words[w] & 0x0F0F0F0Fu;         // codes 0,2,4,6 of the word
-            const uint32_t hi = (words[w] >> 4) & 0x0F0F0F0Fu;  // codes 1,3,5,7
+            uint32_t lo = words[w] & 0x0F0F0F0Fu;         // codes 0,2,4,6 of the word
+            uint32_t hi = (words[w] >> 4) & 0x0F0F0F0Fu;  // codes 1,3,5,7
+            asm("" : "+v"(lo));
+            asm("" : "+v"(hi));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float c0 = (float)((lo >> (8 * i)) & 0xffu);
-                const float c1 = (float)((hi >> (8 * i)) & 0xffu);
+                const float c0 = (float)(uint8_t)(lo >> (8 * i));
+                const float c1 = (float)(uint8_t)(hi >> (8 * i));
                 out[4 * w + i] = pack_bf16x2(fmaf(s, c0, b), fmaf(s, c1, b));
             }
         }
     } else if constexpr (BITS == 8) {
 #pragma unroll
-        for (int w = 0; w < 8; ++w)
+        for (int w = 0; w < 8; ++w) {
+            uint32_t v = words[w];
+            asm("" : "+v"(v));
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const float c0 = (float)((words[w] >> (16 * i)) & 0xffu);
-                const float c1 = (float)((words[w] >> (16 * i + 8)) & 0xffu);
+                const float c0 = (float)(uint8_t)(v >> (16 * i));
+                const float c1 = (float)(uint8_t)(v >> (16 * i + 8));
                 out[2 * w + i] = pack_bf16x2(fmaf(s, c0, b), fmaf(s, c1, b));
             }
+        }
     } else {
         dequant_run_bf16<BITS>(words, s, b, out);
     }
@@ -1339,9 +1348,19 @@ RQ_DEV void store_wave_tile(const f32x4_t (&acc)[TM][TN], uint8_t* stg, void* __
 // arrive 8 groups per 16-byte load, once per 8 groups.  Waves 0-3 run MFMAs
 // (2x2, wave tile 128 x BN/2, two k-steps of 32 per stage); waves 4-7 keep
 // D stages of loads in flight in registers, write the activations to a
-// 2-slot LDS ring (16-byte chunks XOR-swizzled by row) and dequantize their
-// row's codes straight from registers into a 2-slot bf16 ring.  One barrier
-// per stage.
+// 2-slot LDS ring (16-byte chunks XOR-swizzled by row) and dequantize the
+// stage's codes straight from registers into a 2-slot bf16 ring.  One
+// barrier per stage.
+//  * A wave64 VALU op costs ~6-8 cycles and runs beside the MFMA wave on
+//    the same SIMD, so the dequantization is split evenly over all 256
+//    producer lanes: each takes NJ jobs of JW packed words (one 8-code word
+//    at 4 bits with BN = 160, one 32-code run otherwise), reading the job's
+//    fp32 (scale, bias) from an LDS table that one thread per row refreshes
+//    once per 8 groups.
+//  * The MFMA waves hold 160 accumulator registers, so their fragments are
+//    software-pipelined by hand (B fragments of the next k-step and A
+//    fragments two MFMA groups ahead), with scheduling barriers keeping the
+//    order: the compiler's own order waited on every fragment read.
 template <int BITS, int SDT, int BN, int GSH>
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
@@ -1355,11 +1374,12 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     constexpr int P = (8 << GSH) / 64;       // stages per 8-group (scale, bias) chunk: 4, 8, 16
     static_assert(P % D == 0, "the register ring index is the unrolled stage index mod D");
     static_assert(SDT != RQ_F32, "16-bit scales");
-    static_assert(BN <= 256, "one producer thread dequantizes one weight row");
+    static_assert(BN <= 256, "one producer thread stages one row's (scale, bias)");
     __shared__ __attribute__((aligned(16))) uint8_t xs0[BM * 128];
     __shared__ __attribute__((aligned(16))) uint8_t xs1[BM * 128];
     __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * BLD];
     __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * BLD];
+    __shared__ __attribute__((aligned(16))) float sbf[2][BN * 16];  // fp32 (scale, bias), [row][8 groups]
 
     const int ntiles = tiles_m * tiles_n;
     const int per_xcd = (ntiles + 7) / 8;
@@ -1372,13 +1392,19 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     const int nst = (int)(K >> 6);
     const int nper = (nst + P - 1) / P;
 
+    constexpr int SW = 2 * BITS;                              // packed words per row per stage
+    constexpr int JW = (BITS == 4 && BN == 160) ? 1 : BITS;   // words per dequant job
+    constexpr int JPR = SW / JW;                              // jobs per row per stage
+    constexpr int NJ = BN * JPR / 256;                        // jobs per producer thread
+    constexpr int JC = 32 * JW / BITS;                        // codes per job
+    static_assert(NJ * 256 == BN * JPR, "every producer thread gets the same dequant work");
+
     if (wave >= 4) {
         // ---------------------------------------------------------- producers
         if (RQ_K64_PPRIO) __builtin_amdgcn_s_setprio(RQ_K64_PPRIO);
         const int pt = tid - 256, pw = wave - 4;
         typedef const __attribute__((address_space(1))) u32x4_t* gv_t;
-        // activations: load i of this thread = row (pw*8+i)*8 + lane/8, chunk
-        // lane%8 of the stage's 128 bytes; stored at chunk ^ (row & 7)
+        typedef const __attribute__((address_space(1))) uint32_t* gw_t;
         uint32_t xoff[8], xdst[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -1390,53 +1416,79 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
             xdst[i] = (uint32_t)(row * 128 + ((chunk ^ (row & 7)) * 16));
         }
         const uint8_t* xbase = (const uint8_t*)(x + m0 * K);
+        // dequant jobs: job j = pt + 256 i is part j % JPR (JW words) of tile row j / JPR
+        const uint32_t* wtile = wq + n0 * wpr;
+        uint32_t coff[NJ], qoff[NJ], soff[NJ];
+#pragma unroll
+        for (int i = 0; i < NJ; ++i) {
+            const int j = pt + 256 * i, row = j / JPR, part = j % JPR;
+            const int rr = n0 + row < R ? row : (int)(R - 1 - n0);
+            coff[i] = (uint32_t)(rr * wpr + part * JW);
+            qoff[i] = (uint32_t)(row * BLD + part * JC);
+            soff[i] = (uint32_t)(row * 16 + (GSH == 5 ? 2 * ((part * JC) >> 5) : 0));
+        }
+        // (scale, bias) staging: thread pt < BN converts row pt's 8 groups of a period
         const bool has_row = pt < BN;
         int64_t wrow = n0 + (has_row ? pt : 0);
         wrow = wrow < R ? wrow : R - 1;
-        const uint32_t* wrow_p = wq + wrow * wpr;
         const uint16_t* srow_p = (const uint16_t*)scales + wrow * G;
         const uint16_t* brow_p = (const uint16_t*)biases + wrow * G;
 
         u32x4_t xv[D][8];
-        uint32_t cv[D][2 * BITS];
+        uint32_t cv[D][NJ][JW];
         auto issue = [&](int st, int r) {
             const int sc = st < nst ? st : nst - 1;
             const uint8_t* xb = xbase + (int64_t)sc * 128;
 #pragma unroll
             for (int i = 0; i < 8; ++i) xv[r][i] = *(gv_t)(xb + xoff[i]);
-            if (has_row) {
-                const uint32_t* cp = wrow_p + (int64_t)sc * 2 * BITS;
-                if constexpr ((BITS & 1) == 0) {
+            const uint32_t* ws = wtile + (int64_t)sc * SW;
 #pragma unroll
-                    for (int q = 0; q < BITS / 2; ++q) {
-                        const u32x4_t v = *((gv_t)cp + q);
-                        cv[r][4 * q] = v[0]; cv[r][4 * q + 1] = v[1];
-                        cv[r][4 * q + 2] = v[2]; cv[r][4 * q + 3] = v[3];
+            for (int i = 0; i < NJ; ++i) {
+                if constexpr (JW % 4 == 0) {
+#pragma unroll
+                    for (int q = 0; q < JW / 4; ++q) {
+                        const u32x4_t v = *((gv_t)(ws + coff[i]) + q);
+                        cv[r][i][4 * q] = v[0]; cv[r][i][4 * q + 1] = v[1];
+                        cv[r][i][4 * q + 2] = v[2]; cv[r][i][4 * q + 3] = v[3];
                     }
                 } else {
-                    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 #pragma unroll
-                    for (int q = 0; q < BITS; ++q) {
-                        const u32x2_t v = *((const __attribute__((address_space(1))) u32x2_t*)cp + q);
-                        cv[r][2 * q] = v[0]; cv[r][2 * q + 1] = v[1];
-                    }
+                    for (int q = 0; q < JW; ++q) cv[r][i][q] = *((gw_t)(ws + coff[i]) + q);
                 }
             }
         };
-        // (scale, bias) of 8 groups: cur for this period, nxt for the next one
-        auto load_sb = [&](int per, u32x4_t& sv, u32x4_t& bv) {
+        u32x4_t s_nxt = {0u, 0u, 0u, 0u}, b_nxt = s_nxt;
+        auto load_sb = [&](int per) {
             int g0 = per * 8;
             g0 = g0 < (int)G - 8 ? g0 : (int)G - 8;
             if (has_row) {
-                sv = *(gv_t)(srow_p + g0);
-                bv = *(gv_t)(brow_p + g0);
+                s_nxt = *(gv_t)(srow_p + g0);
+                b_nxt = *(gv_t)(brow_p + g0);
             }
         };
-        u32x4_t s_cur = {0u, 0u, 0u, 0u}, b_cur = s_cur, s_nxt = s_cur, b_nxt = s_cur;
-        load_sb(0, s_cur, b_cur);
-        load_sb(1, s_nxt, b_nxt);
+        auto put_sb = [&](int buf) {
+            if (has_row) {
+                float* d = sbf[buf] + pt * 16;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t sw = s_nxt[q], bw = b_nxt[q];
+                    *(f32x4_t*)(d + 4 * q) = f32x4_t{
+                        dt_traits<SDT>::to_f32((uint16_t)(sw & 0xffffu)),
+                        dt_traits<SDT>::to_f32((uint16_t)(bw & 0xffffu)),
+                        dt_traits<SDT>::to_f32((uint16_t)(sw >> 16)),
+                        dt_traits<SDT>::to_f32((uint16_t)(bw >> 16))};
+                }
+            }
+        };
+        load_sb(0);
+        put_sb(0);
+        load_sb(1);
 #pragma unroll
         for (int r = 0; r < D; ++r) issue(r, r);
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // period 0's (scale, bias) are staged
+        asm volatile("" ::: "memory");
 
         for (int per = 0; per < nper; ++per) {
 #pragma unroll
@@ -1444,25 +1496,33 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                 const int st = per * P + u;
                 uint8_t* xs = (u & 1) ? xs1 : xs0;
                 uint16_t* bq = (u & 1) ? bq1 : bq0;
+                if (u == 0) {
+                    put_sb((per + 1) & 1);  // the next period's values (read from stage (per+1)*P on)
+                    load_sb(per + 2);
+                }
 #pragma unroll
                 for (int i = 0; i < 8; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u % D][i];
-                if (has_row) {
-                    uint32_t d[32];
+                const float* sb = sbf[per & 1] + 2 * ((u * 64) >> GSH);
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        // group of run h of this stage within the 8-group chunk
-                        constexpr int GPS = 64 >> GSH ? 64 >> GSH : 1;  // groups per stage (>= 1)
-                        const int gl = GSH == 5 ? 2 * u + h : (GSH == 6 ? u : u / 2);
-                        const uint32_t sw = s_cur[(gl & 7) >> 1], bw = b_cur[(gl & 7) >> 1];
-                        const uint16_t sr = (gl & 1) ? (uint16_t)(sw >> 16) : (uint16_t)(sw & 0xffffu);
-                        const uint16_t br = (gl & 1) ? (uint16_t)(bw >> 16) : (uint16_t)(bw & 0xffffu);
-                        (void)GPS;
-                        dequant_run_fast<BITS>(&cv[u % D][h * BITS], dt_traits<SDT>::to_f32(sr),
-                                               dt_traits<SDT>::to_f32(br), d + 16 * h);
+                for (int i = 0; i < NJ; ++i) {
+                    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+                    const f32x2_t sv = *(const f32x2_t*)(sb + soff[i]);
+                    uint32_t d[JC / 2];
+                    if constexpr (JW == 1) {
+                        uint32_t lo = cv[u % D][i][0] & 0x0F0F0F0Fu;
+                        uint32_t hi = (cv[u % D][i][0] >> 4) & 0x0F0F0F0Fu;
+                        asm("" : "+v"(lo));
+                        asm("" : "+v"(hi));
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            d[k] = pack_bf16x2(fmaf(sv[0], (float)(uint8_t)(lo >> (8 * k)), sv[1]),
+                                               fmaf(sv[0], (float)(uint8_t)(hi >> (8 * k)), sv[1]));
+                    } else {
+                        dequant_run_fast<BITS>(cv[u % D][i], sv[0], sv[1], d);
                     }
-                    u32x4_t* dst = (u32x4_t*)(bq + pt * BLD);
+                    u32x4_t* dst = (u32x4_t*)(bq + qoff[i]);
 #pragma unroll
-                    for (int q = 0; q < 8; ++q)
+                    for (int q = 0; q < JC / 8; ++q)
                         dst[q] = u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
                 }
                 issue(st + D, u % D);
@@ -1471,9 +1531,6 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
             }
-            s_cur = s_nxt;
-            b_cur = b_nxt;
-            load_sb(per + 2, s_nxt, b_nxt);
         }
         return;
     }
@@ -1496,6 +1553,9 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
             aoff[h][a] = (uint32_t)(row * 128 + (((h * 4 + lg) ^ (row & 7)) * 16));
         }
     const uint32_t boff = (uint32_t)((wn * WN + lr) * BLD + lg * 8);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // the producers' prologue barrier
+    asm volatile("" ::: "memory");
 
     for (int per = 0; per < nper; ++per) {
 #pragma unroll
@@ -1508,22 +1568,37 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
             if (st < nst) {
                 const uint8_t* xs = (u & 1) ? xs1 : xs0;
                 const uint16_t* bq = (u & 1) ? bq1 : bq0;
+                // software pipeline over (h, a): B fragments of k-step h+1 are read
+                // while k-step h runs; A fragments rotate through 3 registers, read
+                // 2 MFMA groups (10 MFMAs) ahead of their use.
+                bf16x8_t bf[2][TN], af[3];
+                auto rdA = [&](int h, int a) {
+                    return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
+                };
+                auto rdB = [&](int h, int b) {
+                    return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(bq + boff + b * 16 * BLD + h * 32));
+                };
+#pragma unroll
+                for (int b = 0; b < TN; ++b) bf[0][b] = rdB(0, b);
+                af[0] = rdA(0, 0);
+                af[1] = rdA(0, 1);
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    bf16x8_t af[TM], bf[TN];
 #pragma unroll
-                    for (int a = 0; a < TM; ++a)
-                        af[a] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
+                    for (int a = 0; a < TM; ++a) {
+                        const int q = h * TM + a + 2;   // the (h, a) index read now
+                        if (q < 2 * TM) af[q % 3] = rdA(q / TM, q % TM);
+                        if (h == 0 && a == 2) {
 #pragma unroll
-                    for (int b = 0; b < TN; ++b)
-                        bf[b] = __builtin_bit_cast(
-                            bf16x8_t, *(const u32x4_t*)(bq + boff + b * 16 * BLD + h * 32));
-#pragma unroll
-                    for (int a = 0; a < TM; ++a)
+                            for (int b = 0; b < TN; ++b) bf[1][b] = rdB(1, b);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                         for (int b = 0; b < TN; ++b)
-                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[b], af[a],
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[h][b], af[(h * TM + a) % 3],
                                                                                 acc[a][b], 0, 0, 0);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
             }
         }
@@ -1779,7 +1854,9 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
     // 64-wide stages: 16-bit 16-byte aligned scales, whole 8-group chunks
     if (m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 && cols % 64 == 0 &&
         (cols / gs) % 8 == 0 && (((uintptr_t)scales | (uintptr_t)biases) & 15) == 0) {
-        const int bn = rows % 160 == 0 ? 160 : 128;
+        // 160-row tiles (whole rounds over 256 CUs for the 2560-wide RWKV-7 shapes) split
+        // evenly into 8-code dequant jobs only at 4 bits
+        const int bn = (RQ_BITS == 4 && rows % 160 == 0) ? 160 : 128;
         const int tm = (int)((m + 255) / 256);
         const int tn = (int)((rows + bn - 1) / bn);
         const int blocks = ((tm * tn + 7) / 8) * 8;
@@ -1792,11 +1869,15 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
         case 6: RQ_K64(SD, BNV, 6); break;                                                        \
         default: RQ_K64(SD, BNV, 7); break;                                                       \
     }
+#if RQ_BITS == 4
         if (sb_dt == RQ_BF16) {
             if (bn == 160) { RQ_K64_GS(RQ_BF16, 160) } else { RQ_K64_GS(RQ_BF16, 128) }
         } else {
             if (bn == 160) { RQ_K64_GS(RQ_F16, 160) } else { RQ_K64_GS(RQ_F16, 128) }
         }
+#else
+        if (sb_dt == RQ_BF16) { RQ_K64_GS(RQ_BF16, 128) } else { RQ_K64_GS(RQ_F16, 128) }
+#endif
 #undef RQ_K64_GS
 #undef RQ_K64
         return hipGetLastError();
