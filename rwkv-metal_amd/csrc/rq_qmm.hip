@@ -1738,9 +1738,34 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                 const int off = bit & 31;
                 const float sf = dt_traits<SDT>::to_f32(ss[row * 4 + gl]);
                 const float bf = dt_traits<SDT>::to_f32(ss[256 + row * 4 + gl]);
+                float cf[8];
+                if constexpr (BITS == 4) {
+                    // one word = the 8 codes; byte converts on the nibble halves
+                    // (masks hidden from the optimiser, see dequant_run_fast)
+                    uint32_t lo = wr[0] & 0x0F0F0F0Fu, hi = (wr[0] >> 4) & 0x0F0F0F0Fu;
+                    asm("" : "+v"(lo));
+                    asm("" : "+v"(hi));
 #pragma unroll
-                for (int c = 0; c < 8; ++c)
-                    v[i][c] = fmaf(sf, (float)(uint32_t)((win >> (off + c * BITS)) & ((1u << BITS) - 1u)), bf);
+                    for (int q = 0; q < 4; ++q) {
+                        cf[2 * q] = (float)(uint8_t)(lo >> (8 * q));
+                        cf[2 * q + 1] = (float)(uint8_t)(hi >> (8 * q));
+                    }
+                } else if constexpr (BITS == 8) {
+                    uint32_t w0 = wr[0], w1 = wr[1];
+                    asm("" : "+v"(w0));
+                    asm("" : "+v"(w1));
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        cf[q] = (float)(uint8_t)(w0 >> (8 * q));
+                        cf[4 + q] = (float)(uint8_t)(w1 >> (8 * q));
+                    }
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; ++c)
+                        cf[c] = (float)(uint32_t)((win >> (off + c * BITS)) & ((1u << BITS) - 1u));
+                }
+#pragma unroll
+                for (int c = 0; c < 8; ++c) v[i][c] = fmaf(sf, cf[c], bf);
             }
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
@@ -1813,22 +1838,36 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
             if (st < nst) {
                 const uint8_t* xs = u ? xs1 : xs0;
                 const uint16_t* bq = u ? bq1 : bq0;
+                // fragments software-pipelined as in qmm_t_k64
+                bf16x8_t bf[2][TN], af[3];
+                auto rdA = [&](int h, int a) {
+                    return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
+                };
+                auto rdB = [&](int h, int b) {
+                    return __builtin_bit_cast(bf16x8_t,
+                                              *(const u32x4_t*)(bq + boff + b * 16 * BLD + h * 32));
+                };
+#pragma unroll
+                for (int b = 0; b < TN; ++b) bf[0][b] = rdB(0, b);
+                af[0] = rdA(0, 0);
+                af[1] = rdA(0, 1);
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    bf16x8_t af[TM], bf[TN];
 #pragma unroll
-                    for (int a = 0; a < TM; ++a)
-                        af[a] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
+                    for (int a = 0; a < TM; ++a) {
+                        const int q = h * TM + a + 2;
+                        if (q < 2 * TM) af[q % 3] = rdA(q / TM, q % TM);
+                        if (h == 0 && a == 2) {
 #pragma unroll
-                    for (int b = 0; b < TN; ++b)
-                        bf[b] = __builtin_bit_cast(
-                            bf16x8_t, *(const u32x4_t*)(bq + boff + b * 16 * BLD + h * 32));
-#pragma unroll
-                    for (int a = 0; a < TM; ++a)
+                            for (int b = 0; b < TN; ++b) bf[1][b] = rdB(1, b);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                         for (int b = 0; b < TN; ++b)
-                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[b], af[a],
-                                                                                acc[a][b], 0, 0, 0);
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                bf[h][b], af[(h * TM + a) % 3], acc[a][b], 0, 0, 0);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
             }
         }

@@ -83,6 +83,9 @@ constexpr int kBlock = 64 * kWaves;
 #ifndef RQ_QMV_BIG_RB
 #define RQ_QMV_BIG_RB 1  // 16-row blocks per wave for big launches
 #endif
+#ifndef RQ_QMV_STREAM_MMAX
+#define RQ_QMV_STREAM_MMAX 4  // largest m the streamed-scale GEMV takes
+#endif
 #ifndef RQ_QMV_STREAM
 #define RQ_QMV_STREAM 1  // 0: never use the streamed-scale GEMV
 #endif
@@ -1155,7 +1158,7 @@ size_t qmv_stream_lds(int64_t m, int64_t cols, int gs, int bits) {
 bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs, int bits) {
     // m > 4 takes ceil(m/4) passes of 4 slots here; the LDS-staged kernel's
     // 8-row slots (gs 64) do less MFMA work there
-    return m <= 4 && sb_dt != RQ_F32 && p.cols % 512 == 0 &&
+    return m <= RQ_QMV_STREAM_MMAX && sb_dt != RQ_F32 && p.cols % 512 == 0 &&
            p.rows <= (int64_t)65536 * kQmvRowsPerBlock &&
            (((uintptr_t)p.scales | (uintptr_t)p.biases) & 15) == 0 &&
            qmv_stream_lds(m, p.cols, gs, bits) <= (size_t)kQmvLdsBudget;
