@@ -18,6 +18,8 @@
  *                     (codes -> MLX bitstream; executable form tests/dev_pack_native_mlx.py:38-57)
  *   rq_unpack      <- the inverse of that packing rule (rwkvq_native.py:18-33), i.e. the
  *                     code extraction inside mx.dequantize
+ *   rq_embedding   <- nn.QuantizedEmbedding lookup (gather + mx.dequantize), target "emb"
+ *                     of rwkv_metal/lora/finetune.py:42, used at rwkv_metal/model/rwkv7_x070.py:302
  *   rq_qmm_grouped <- several independent mx.quantized_matmul(transpose=True) nodes of one
  *                     lazy MLX graph evaluated together (e.g. tmix r/k/v projections,
  *                     rwkv_metal/model/rwkv7_x070.py:142-144); one launch for all of them
@@ -88,6 +90,17 @@ int rq_dequantize(const uint32_t* w_q, const void* scales, const void* biases, r
 int rq_qmm(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
            const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
            int group_size, int bits, int transpose, void* y, rq_dtype y_dt, void* stream);
+
+/* nn.QuantizedEmbedding lookup (upstream MLX; the "emb" target of
+ * rwkv_metal/lora/finetune.py:42, looked up at rwkv_metal/model/rwkv7_x070.py:302):
+ * out[i, :] = rq_dequantize of table row idx[i], for i < n, in one launch (the
+ * gather is fused into the dequantization; no gathered copy of the packed
+ * rows).  idx: int64[n] on the device; out: [n, cols] in out_dt.  The table is
+ * [rows, cols].  An index outside [0, rows) yields a row of NaN and reads
+ * nothing outside the table. */
+int rq_embedding(const int64_t* idx, int64_t n, const uint32_t* w_q, const void* scales,
+                 const void* biases, rq_dtype sb_dt, int64_t rows, int64_t cols, int group_size,
+                 int bits, void* out, rq_dtype out_dt, void* stream);
 
 /* Pack codes uint8[rows, cols] (values < 2^bits) into the MLX bitstream
  * w_q uint32[rows, cols*bits/32].  cols must be a multiple of 32. */

@@ -161,6 +161,20 @@ int rq_dequantize(const uint32_t* w_q, const void* scales, const void* biases, r
                          "rq_dequantize");
 }
 
+int rq_embedding(const int64_t* idx, int64_t n, const uint32_t* w_q, const void* scales,
+                 const void* biases, rq_dtype sb_dt, int64_t rows, int64_t cols, int group_size,
+                 int bits, void* out, rq_dtype out_dt, void* stream) {
+    if (int rc = check_common(rows, cols, group_size, bits)) return rc;
+    if (n < 0) return fail(RQ_EINVAL, "rq_embedding: negative n");
+    if (!valid_dt(sb_dt) || !valid_dt(out_dt)) return fail(RQ_EINVAL, "unsupported dtype");
+    if (n * cols == 0) return ok();
+    if (!idx || !w_q || !scales || !biases || !out) return fail(RQ_EINVAL, "rq_embedding: NULL pointer");
+    if (!aligned16(w_q) || !aligned16(out)) return fail(RQ_EALIGN, "rq_embedding: w_q and out must be 16-byte aligned");
+    return launch_status(rq::launch_embedding(idx, n, w_q, scales, biases, sb_dt, rows, cols,
+                                              group_size, bits, out, out_dt, (hipStream_t)stream),
+                         "rq_embedding");
+}
+
 int rq_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* w_q,
             void* stream) {
     if (int rc = check_common(rows, cols, 32, bits)) return rc;

@@ -16,6 +16,12 @@ hipError_t launch_dequantize(const uint32_t* wq, const void* scales, const void*
                              int sb_dt, int64_t rows, int64_t cols, int gs, int bits, void* out,
                              int out_dt, hipStream_t stream);
 
+// Row gather + dequantize (embedding lookup): out[i] = dequantize(row idx[i]).
+hipError_t launch_embedding(const int64_t* idx, int64_t n, const uint32_t* wq,
+                            const void* scales, const void* biases, int sb_dt, int64_t rows,
+                            int64_t cols, int gs, int bits, void* out, int out_dt,
+                            hipStream_t stream);
+
 hipError_t launch_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* wq,
                        hipStream_t stream);
 

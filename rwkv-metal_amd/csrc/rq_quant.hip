@@ -87,28 +87,37 @@ __global__ __launch_bounds__(kBlock) void quantize_kernel(
 // evaluates multiply and add as two ops in that dtype).  __fmul_rn/__fadd_rn
 // keep the two roundings separate when T is f32.
 template <int BITS, int ODT>
+// One thread per 32-code run.  With idx != NULL this is the embedding
+// lookup: output row r is table row idx[r] (rows = number of indices,
+// src_rows = table rows); an index outside the table gives a row of NaN and
+// reads nothing.
 __global__ __launch_bounds__(kBlock) void dequantize_kernel(
     const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int sb_dt, int64_t rows, int64_t cols, int gs_shift,
-    void* __restrict__ out) {
+    void* __restrict__ out, const int64_t* __restrict__ idx, int64_t src_rows) {
     const int64_t runs_per_row = cols >> 5;
     const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (t >= rows * runs_per_row) return;
     const int64_t row = t / runs_per_row;
     const int64_t run = t - row * runs_per_row;
-    const int64_t gi = row * (cols >> gs_shift) + (run >> (gs_shift - 5));
-    const float s = load_dt(scales, sb_dt, gi);
-    const float b = load_dt(biases, sb_dt, gi);
-
-    uint32_t words[BITS];
-    load_run<BITS>(wq + row * (runs_per_row * BITS) + run * BITS, words);
-
+    const int64_t src = idx ? idx[row] : row;
     float vals[32];
+    if (src < 0 || src >= src_rows) {
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        const float c = (float)run_code<BITS>(words, j);
-        const float p = round_to_dt(sb_dt, __fmul_rn(c, s));
-        vals[j] = round_to_dt(sb_dt, __fadd_rn(p, b));
+        for (int j = 0; j < 32; ++j) vals[j] = __builtin_nanf("");
+    } else {
+        const int64_t gi = src * (cols >> gs_shift) + (run >> (gs_shift - 5));
+        const float s = load_dt(scales, sb_dt, gi);
+        const float b = load_dt(biases, sb_dt, gi);
+
+        uint32_t words[BITS];
+        load_run<BITS>(wq + src * (runs_per_row * BITS) + run * BITS, words);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const float c = (float)run_code<BITS>(words, j);
+            const float p = round_to_dt(sb_dt, __fmul_rn(c, s));
+            vals[j] = round_to_dt(sb_dt, __fadd_rn(p, b));
+        }
     }
     const int64_t o = row * cols + run * 32;
     if constexpr (ODT == RQ_F32) {
@@ -206,7 +215,22 @@ hipError_t launch_dequantize(const uint32_t* wq, const void* scales, const void*
     const int gs_shift = __builtin_ctz(gs);
     RQ_DISPATCH_BITS(bits, B, RQ_DISPATCH_DT(out_dt, D,
         hipLaunchKernelGGL((dequantize_kernel<B, D>), dim3(grid_for(threads)), dim3(kBlock), 0,
-                           stream, wq, scales, biases, sb_dt, rows, cols, gs_shift, out)));
+                           stream, wq, scales, biases, sb_dt, rows, cols, gs_shift, out,
+                           (const int64_t*)nullptr, rows)));
+    return hipGetLastError();
+}
+
+hipError_t launch_embedding(const int64_t* idx, int64_t n, const uint32_t* wq,
+                            const void* scales, const void* biases, int sb_dt, int64_t rows,
+                            int64_t cols, int gs, int bits, void* out, int out_dt,
+                            hipStream_t stream) {
+    const int64_t threads = n * (cols / 32);
+    if (threads == 0) return hipSuccess;
+    const int gs_shift = __builtin_ctz(gs);
+    RQ_DISPATCH_BITS(bits, B, RQ_DISPATCH_DT(out_dt, D,
+        hipLaunchKernelGGL((dequantize_kernel<B, D>), dim3(grid_for(threads)), dim3(kBlock), 0,
+                           stream, wq, scales, biases, sb_dt, n, cols, gs_shift, out, idx,
+                           rows)));
     return hipGetLastError();
 }
 

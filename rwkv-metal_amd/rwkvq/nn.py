@@ -82,7 +82,8 @@ class QuantizedLinear(nn.Module):
 
 
 class QuantizedEmbedding(nn.Module):
-    """Row gather of packed words, scales and biases, then dequantize."""
+    """nn.QuantizedEmbedding: a [num_embeddings, dims] table in packed form;
+    the lookup is one fused gather-dequantize launch (rq_embedding)."""
 
     def __init__(self, num_embeddings: int, dims: int, group_size: int = 64, bits: int = 4,
                  device=None, dtype: torch.dtype = torch.bfloat16):
@@ -113,10 +114,8 @@ class QuantizedEmbedding(nn.Module):
         return q
 
     def forward(self, idx: Tensor) -> Tensor:
-        flat = idx.reshape(-1)
-        rows = ops.dequantize(self.weight[flat], self.scales[flat], self.biases[flat],
-                              self.group_size, self.bits)
-        return rows.reshape(*idx.shape, self.dims)
+        return ops.quantized_embedding(idx, self.weight, self.scales, self.biases,
+                                       self.group_size, self.bits)
 
     def as_linear(self, x: Tensor) -> Tensor:
         """Tied output head: x @ dequant(weight)^T."""

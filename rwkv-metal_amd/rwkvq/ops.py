@@ -5,6 +5,7 @@
     quantized_matmul(x, w_q, scales, biases, transpose,   <- mx.quantized_matmul
                      group_size, bits)
     pack_codes(codes, bits) / unpack_codes(w_q, bits)     <- the MLX bitstream rule
+    quantized_embedding(idx, w_q, scales, biases, ...)    <- nn.QuantizedEmbedding lookup
 
 Reference call sites: rwkv_metal/lora/finetune.py:88-89 (nn.quantize),
 rwkv_metal/lora/lora.py:45-46 (QuantizedLinear.from_linear),
@@ -166,6 +167,47 @@ def dequantize(w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int = 64
     _float(scales, "scales")
     _check_packed(w_q, scales, biases, group_size, bits)
     return _dequantize_op(w_q, scales, biases, group_size, bits)
+
+
+# ------------------------------------------------------------ embedding
+
+@torch.library.custom_op("rwkvq::quantized_embedding", mutates_args=())
+def _embedding_op(idx: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int,
+                  bits: int) -> Tensor:
+    _on_gpu(idx, w_q, scales, biases)
+    flat = _ready(idx.reshape(-1).to(torch.int64))
+    w_q, scales, biases = _ready(w_q), _ready(scales), _ready(biases.to(scales.dtype))
+    R, K = w_q.shape[0], w_q.shape[1] * 32 // bits
+    out = torch.empty(*idx.shape, K, dtype=scales.dtype, device=w_q.device)
+    if out.numel() == 0:
+        return out
+    with torch.cuda.device(w_q.device):
+        rc = lib().rq_embedding(_ptr(flat), flat.numel(), _ptr(w_q), _ptr(scales), _ptr(biases),
+                                DTYPE_CODE[scales.dtype], R, K, group_size, bits, _ptr(out),
+                                DTYPE_CODE[out.dtype], _stream(w_q))
+    check(rc, "quantized_embedding")
+    return out
+
+
+@_embedding_op.register_fake
+def _(idx, w_q, scales, biases, group_size, bits):
+    return scales.new_empty(*idx.shape, w_q.shape[1] * 32 // bits)
+
+
+def quantized_embedding(idx: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor,
+                        group_size: int = 64, bits: int = 4) -> Tensor:
+    """nn.QuantizedEmbedding's lookup: dequantize(table rows idx) in one fused
+    gather-dequantize launch; out[..., :] has idx's shape plus the row width,
+    in the scales dtype.  Indices outside the table give rows of NaN."""
+    _check_args(group_size, bits)
+    w_q = _words(w_q)
+    _float(scales, "scales")
+    if w_q.dim() != 2:
+        raise ValueError("quantized_embedding expects a 2-D packed table")
+    _check_packed(w_q, scales, biases, group_size, bits)
+    if idx.dtype not in (torch.int64, torch.int32, torch.int16, torch.uint8):
+        raise ValueError(f"indices must be an integer tensor (got {idx.dtype})")
+    return _embedding_op(idx, w_q, scales, biases, group_size, bits)
 
 
 # ------------------------------------------------------- quantized_matmul

@@ -27,7 +27,7 @@ def test_header_declares_the_expected_surface():
     assert declared_functions() == sorted([
         "rq_abi_version", "rq_last_error", "rq_quantize", "rq_dequantize", "rq_qmm",
         "rq_pack", "rq_unpack", "rq_qmm_grouped", "rq_grouped_plan_table_bytes",
-        "rq_grouped_plan_init", "rq_grouped_plan_run"])
+        "rq_grouped_plan_init", "rq_grouped_plan_run", "rq_embedding"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -54,6 +54,12 @@ def test_invalid_arguments_return_einval(L):
     assert L.rq_qmm(p, 7, p, p, p, 0, 1, 64, 64, 64, 4, 1, p, 0, None) == -1
     assert L.rq_qmm(0, 0, p, p, p, 0, 1, 64, 64, 64, 4, 1, p, 0, None) == -1
     assert "NULL" in _err(L)
+    assert L.rq_embedding(p, -1, p, p, p, 0, 8, 64, 64, 4, p, 0, None) == -1
+    assert "negative" in _err(L)
+    assert L.rq_embedding(0, 3, p, p, p, 0, 8, 64, 64, 4, p, 0, None) == -1
+    assert "NULL" in _err(L)
+    assert L.rq_embedding(p, 3, p, p, p, 0, 8, 64, 64, 7, p, 0, None) == -1
+    assert L.rq_embedding(p, 0, p, p, p, 0, 8, 64, 64, 4, p, 0, None) == 0
 
 
 def test_misaligned_pointers_return_ealign(L):

@@ -157,3 +157,88 @@ def test_save_load_lora_roundtrip(rq, tmp_path):
     rq.load_lora(m2, path)
     for k, v in rq.lora_state(m).items():
         assert torch.equal(v, dict(m2.named_parameters())[k])
+
+
+def _fill_quantized(model, gen):
+    """Random packed contents for every quantized module (host only)."""
+    for _, m in model.named_modules():
+        if isinstance(m, (__import__("rwkvq").QuantizedLinear, __import__("rwkvq").QuantizedEmbedding)):
+            m.weight.copy_(torch.randint(-2**31, 2**31 - 1, m.weight.shape, generator=gen,
+                                         dtype=torch.int64).to(torch.int32))
+            m.scales.copy_(torch.randn(m.scales.shape, generator=gen).to(m.scales.dtype))
+            m.biases.copy_(torch.randn(m.biases.shape, generator=gen).to(m.biases.dtype))
+
+
+def _empty_quantize(rq, model, targets, bits_for):
+    """Structure-only quantization (no kernels): swap the targets for empty
+    quantized modules of the given bits, group size 64."""
+    for path, m in list(model.named_modules()):
+        if not any(path.endswith(t) for t in targets):
+            continue
+        parent_path, _, name = path.rpartition(".")
+        parent = model.get_submodule(parent_path) if parent_path else model
+        b = bits_for(path)
+        if isinstance(m, nn.Linear):
+            q = rq.QuantizedLinear(m.in_features, m.out_features, bias=m.bias is not None,
+                                   group_size=64, bits=b)
+        else:
+            q = rq.QuantizedEmbedding(m.num_embeddings, m.embedding_dim, group_size=64, bits=b)
+        setattr(parent, name, q)
+
+
+def test_quantized_checkpoint_roundtrip(rq, tmp_path):
+    """save_quantized writes MLX's key names with uint32 packed words and the
+    quantization entry (per-module override for the 8-bit head);
+    load_quantized rebuilds the quantized modules from shapes alone."""
+    from safetensors import safe_open
+    from rwkvq import io as rio
+
+    src = Tiny(device="cpu")
+    _empty_quantize(rq, src, ("cmix.key", "cmix.value", "head", "emb"),
+                    lambda p: 8 if p == "head" else 3)
+    g = torch.Generator().manual_seed(5)
+    with torch.no_grad():
+        _fill_quantized(src, g)
+        for p in src.parameters():
+            p.copy_(torch.randn(p.shape, generator=g).to(p.dtype))
+    path = str(tmp_path / "q.safetensors")
+    rio.save_quantized(src, path)
+    with safe_open(path, "pt") as f:
+        keys = set(f.keys())
+        assert f.get_tensor("blocks.0.cmix.key.weight").dtype == torch.uint32
+        assert f.get_tensor("head.scales").dtype == torch.bfloat16
+    assert {"head.weight", "head.scales", "head.biases", "emb.weight", "emb.scales",
+            "blocks.2.cmix.value.biases", "blocks.1.tmix.r_proj.weight"} <= keys
+    cfg = rio.quantization_config(path)
+    assert cfg["bits"] == 3 and cfg["group_size"] == 64 and cfg["head"] == {"group_size": 64, "bits": 8}
+
+    dst = Tiny(device="cpu")
+    rio.load_quantized(dst, path)
+    assert isinstance(dst.head, rq.QuantizedLinear) and dst.head.bits == 8
+    assert isinstance(dst.emb, rq.QuantizedEmbedding) and dst.emb.bits == 3
+    assert isinstance(dst.blocks[1].cmix.value, rq.QuantizedLinear)
+    assert dst.blocks[1].cmix.value.bits == 3 and dst.blocks[1].cmix.value.group_size == 64
+    assert isinstance(dst.blocks[1].tmix.r_proj, nn.Linear)
+    for (k, a), (k2, b) in zip(sorted(src.state_dict().items()), sorted(dst.state_dict().items())):
+        assert k == k2 and a.dtype == b.dtype and torch.equal(a, b), k
+
+
+def test_quantized_checkpoint_mismatch_raises(rq, tmp_path):
+    from rwkvq import io as rio
+    src = Tiny(device="cpu")
+    _empty_quantize(rq, src, ("head",), lambda p: 4)
+    path = str(tmp_path / "q.safetensors")
+    rio.save_quantized(src, path)
+    other = Tiny(d=128, n=2, device="cpu")   # one block fewer: unexpected keys
+    with pytest.raises(KeyError):
+        rio.load_quantized(other, path)
+    rio.load_quantized(Tiny(d=128, n=2, device="cpu"), path, strict=False)
+
+
+def test_embedding_op_refuses_cpu_and_bad_indices(rq):
+    wq = torch.zeros(8, 8, dtype=torch.int32)
+    s = torch.zeros(8, 1)
+    with pytest.raises(RuntimeError, match="GPU"):
+        rq.quantized_embedding(torch.zeros(3, dtype=torch.int64), wq, s, s, 64, 4)
+    with pytest.raises(ValueError):
+        rq.quantized_embedding(torch.zeros(3), wq, s, s, 64, 4)

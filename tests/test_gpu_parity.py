@@ -563,6 +563,34 @@ def test_quantized_embedding_and_linear_module(O, rq, dev):
     rel_check(ql(x), ref, what="QuantizedLinear")
 
 
+@pytest.mark.parametrize("bits,gs,sdt", [(4, 64, torch.bfloat16), (3, 32, torch.float16),
+                                         (8, 128, torch.float32), (6, 64, torch.bfloat16)])
+def test_embedding_gather_dequant(O, rq, dev, bits, gs, sdt):
+    """rq_embedding (fused gather + dequantize) is bit-exact to the oracle's
+    dequantize of the gathered rows, for int32/int64 indices of any shape,
+    repeated indices, and gives NaN rows (not a fault) for indices outside
+    the table."""
+    R, K = 333, 4 * gs
+    w = weights(R, K, 61 + bits, dtype=sdt)
+    wq, s, b = O.quantize(w, gs, bits)
+    table = O.dequantize(wq, s, b, gs, bits)
+    g = torch.Generator().manual_seed(bits)
+    idx = torch.randint(0, R, (3, 7, 5), generator=g)
+    idx[0, 0, 0], idx[2, 6, 4] = 0, R - 1
+    say(f"embedding bits={bits} gs={gs} sdt={sdt}")
+    for it in (torch.int64, torch.int32):
+        out = rq.quantized_embedding(idx.to(dev, it), wq.to(dev), s.to(dev), b.to(dev), gs, bits)
+        assert out.shape == (3, 7, 5, K) and out.dtype == sdt
+        assert bits_equal(out, table[idx])
+    bad = torch.tensor([5, -1, R, 7], device=dev)
+    out = rq.quantized_embedding(bad, wq.to(dev), s.to(dev), b.to(dev), gs, bits).cpu()
+    assert bits_equal(out[0], table[5]) and bits_equal(out[3], table[7])
+    assert torch.isnan(out[1].float()).all() and torch.isnan(out[2].float()).all()
+    empty = rq.quantized_embedding(torch.zeros(0, dtype=torch.int64, device=dev), wq.to(dev),
+                                   s.to(dev), b.to(dev), gs, bits)
+    assert empty.shape == (0, K)
+
+
 # --------------------------------------------------- determinism / edges
 
 def test_repeated_launches_bitwise_identical(rq, dev):
@@ -626,3 +654,37 @@ def test_bound_qmm_matches_op(O, rq, dev, transpose):
     assert not torch.equal(y1, y2)
     with pytest.raises(ValueError):
         rq.BoundQmm(x, wq, s, b, transpose, gs, bits, out=torch.empty(1, device=dev))
+
+
+def test_quantized_checkpoint_roundtrip_gpu(O, rq, dev, tmp_path):
+    """A model quantized on the GPU (quantize_base_model, 3-bit body and 8-bit
+    head via a per-module predicate), saved with save_quantized and loaded into
+    a fresh float model with load_quantized, gives bit-identical outputs."""
+    from torch import nn
+    from rwkvq import io as rio
+
+    class M(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.emb = nn.Embedding(512, 256)
+            self.key = nn.Linear(256, 1024, bias=False)
+            self.value = nn.Linear(1024, 256, bias=True)
+            self.head = nn.Linear(256, 512, bias=False)
+
+    torch.manual_seed(3)
+    src = M().to(dev, torch.bfloat16)
+    rq.quantize_model(src, 64, 3, class_predicate=lambda p, m: (
+        {"bits": 8} if p == "head" else isinstance(m, (nn.Linear, nn.Embedding))))
+    path = str(tmp_path / "m.safetensors")
+    rio.save_quantized(src, path)
+    dst = M().to(dev, torch.bfloat16)
+    rio.load_quantized(dst, path)
+    idx = torch.tensor([[1, 7, 511]], device=dev)
+    say("checkpoint roundtrip")
+
+    def run(m):
+        h = m.emb(idx)
+        return m.head(m.value(m.key(h)))
+
+    assert dst.head.bits == 8 and dst.key.bits == 3
+    assert torch.equal(run(src), run(dst))
