@@ -20,6 +20,10 @@
  *                     code extraction inside mx.dequantize
  *   rq_embedding   <- nn.QuantizedEmbedding lookup (gather + mx.dequantize), target "emb"
  *                     of rwkv_metal/lora/finetune.py:42, used at rwkv_metal/model/rwkv7_x070.py:302
+ *   rq_sb6_dequantize / rq_sb6_to_affine
+ *                  <- the .rwkvq (rwkv-quant sb6) base: RwkvqLinear's fused dequant
+ *                     (rwkv_metal/lora/rwkvq_kernel.py) and RwkvqNativeLinear's repack into
+ *                     the MLX layout (rwkv_metal/lora/rwkvq_native.py:49-113)
  *   rq_qmm_grouped <- several independent mx.quantized_matmul(transpose=True) nodes of one
  *                     lazy MLX graph evaluated together (e.g. tmix r/k/v projections,
  *                     rwkv_metal/model/rwkv7_x070.py:142-144); one launch for all of them
@@ -34,7 +38,7 @@
  * Conventions: every pointer is a device pointer owned by the caller; nothing
  * is allocated; work is enqueued on `stream` (a hipStream_t, NULL = the
  * default stream) with no implicit synchronisation.  Row-major, contiguous.
- * All device pointers must be 16-byte aligned.
+ * Device pointers must be 16-byte aligned unless an entry point says otherwise.
  *
  * Return codes: RQ_OK (0); RQ_EINVAL (-1): bits not in {2,3,4,5,6,8},
  * group_size not in {32,64,128}, cols % group_size != 0, a negative size, a
@@ -101,6 +105,36 @@ int rq_qmm(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales
 int rq_embedding(const int64_t* idx, int64_t n, const uint32_t* w_q, const void* scales,
                  const void* biases, rq_dtype sb_dt, int64_t rows, int64_t cols, int group_size,
                  int bits, void* out, rq_dtype out_dt, void* stream);
+
+/* rwkv-quant "sb6" tensors in the K3-interleaved layout RwkvqLinear holds
+ * (rwkv_metal/lora/rwkvq_linear.py:96-110; layout stated at
+ * rwkv_metal/lora/rwkvq_kernel.py:18-25).  The tensor is [rows, cols] in
+ * blocks of gw_gs = 32 codes, nb = cols/32 blocks per row:
+ *   qblk uint8[rows, nb*(16+4*xbits)]: per block 16 bytes (byte j = code j |
+ *        code j+16 << 4), then for xbits >= 1 a uint32 bit plane (bit c = bit
+ *        4 of code c), for xbits == 2 another (bit 5);
+ *   qsqm uint8[rows, nb*2]: (qs uint8, qm int8) per block;
+ *   ddm  float16[rows, (nb/gw_sb)*2]: (d, dm) per super-block of gw_sb blocks.
+ * scale = f16(qs*d), min = f16(qm*dm), w = code*scale + min (fp32).
+ * qblk and ddm 4-byte aligned, qsqm 2-byte aligned.
+ *
+ * rq_sb6_dequantize <- RwkvqLinear._dequant_w / the fused sb6 dequant kernel
+ *   (rwkv_metal/lora/rwkvq_linear.py:131-135, rwkvq_kernel.py:86-124): dense
+ *   out[rows, cols] in out_dt (fp32 as computed, or rounded to bf16/f16). */
+int rq_sb6_dequantize(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, int64_t rows,
+                      int64_t cols, int gw_gs, int gw_sb, int xbits, void* out, rq_dtype out_dt,
+                      void* stream);
+
+/* rq_sb6_to_affine <- the one-time repack of RwkvqNativeLinear
+ *   (rwkv_metal/lora/rwkvq_native.py:49-78, 103-113) into the MLX affine
+ *   layout used by rq_qmm: w_q uint32[rows, nb*bits] with bits = 4 + xbits
+ *   (codes bit for bit), scales = max(scale, 1e-8) and biases = min as fp32
+ *   [rows, nb], group size 32.  w_q may be NULL (and then qblk too): only
+ *   scales/biases are written (RwkvqHybridLinear._expand_scale_bias,
+ *   rwkvq_hybrid.py:72-86).  Outputs 4-byte aligned. */
+int rq_sb6_to_affine(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, int64_t rows,
+                     int64_t cols, int gw_gs, int gw_sb, int xbits, uint32_t* w_q, float* scales,
+                     float* biases, void* stream);
 
 /* Pack codes uint8[rows, cols] (values < 2^bits) into the MLX bitstream
  * w_q uint32[rows, cols*bits/32].  cols must be a multiple of 32. */

@@ -46,6 +46,9 @@ def lib() -> ctypes.CDLL:
         L.rqo_round_bf16.argtypes = [ctypes.c_float]
         L.rqo_round_bf16.restype = ctypes.c_float
         L.rqo_max_threads.restype = i32
+        L.rqo_sb6_codes.argtypes = [vp, i64, i64, i32, vp]
+        L.rqo_sb6_scale_min.argtypes = [vp, vp, i64, i64, i32, i32, vp, vp]
+        L.rqo_sb6_dequantize.argtypes = [vp, vp, vp, i64, i64, i32, i32, vp]
         _lib = L
     return _lib
 
@@ -147,3 +150,35 @@ def qmv_bf16(x, wq, scales, biases, group_size=64, bits=4, nthreads=0):
 
 def max_threads() -> int:
     return int(lib().rqo_max_threads())
+
+
+# ----------------------------------------------------------- sb6 / K3
+
+def sb6_codes(qblk: torch.Tensor, rows: int, cols: int, xbits: int) -> torch.Tensor:
+    """Codes uint8[rows, cols] of a K3-interleaved sb6 tensor."""
+    qblk = qblk.contiguous()
+    codes = torch.empty(rows, cols, dtype=torch.uint8)
+    lib().rqo_sb6_codes(_p(qblk), rows, cols, xbits, _p(codes))
+    return codes
+
+
+def sb6_scale_min(qsqm, ddm, rows, cols, gw_sb, clamp=False):
+    """(scale, min) fp32 [rows, cols/32]: f16(qs*d), f16(qm*dm); clamp applies
+    max(scale, 1e-8) as the native repack does."""
+    qsqm, ddm = qsqm.contiguous(), ddm.contiguous()
+    sc = torch.empty(rows, cols // 32, dtype=torch.float32)
+    mn = torch.empty_like(sc)
+    lib().rqo_sb6_scale_min(_p(qsqm), _p(ddm.view(torch.int16)), rows, cols, gw_sb,
+                            1 if clamp else 0, _p(sc), _p(mn))
+    return sc, mn
+
+
+def sb6_dequantize(qblk, qsqm, ddm, rows, cols, gw_sb, xbits) -> torch.Tensor:
+    """Dense fp32 [rows, cols]: code * scale + min (the fused kernel's form)."""
+    qblk, qsqm, ddm = qblk.contiguous(), qsqm.contiguous(), ddm.contiguous()
+    out = torch.empty(rows, cols, dtype=torch.float32)
+    rc = lib().rqo_sb6_dequantize(_p(qblk), _p(qsqm), _p(ddm.view(torch.int16)), rows, cols,
+                                  gw_sb, xbits, _p(out))
+    if rc != 0:
+        raise ValueError(f"oracle sb6 dequantize rejected arguments (rc={rc})")
+    return out

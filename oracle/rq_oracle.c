@@ -32,6 +32,10 @@
  *                      with no rounding (the form of MLX's qmv, which applies
  *                      scale and bias to per-group sums of x*code and x);
  *                      products are accumulated in double.
+ *   - rqo_sb6_*      : the rwkv-quant sb6 (K3) decode, dense dequantize and
+ *                      the scale/min expansion of the native repack
+ *                      (rwkv_metal/lora/rwkvq_kernel.py, rwkvq_linear.py,
+ *                      rwkvq_native.py; see the section below).
  *
  * Build: oracle/Makefile (gcc, -ffp-contract=off so no FMA contraction changes
  * the quantize arithmetic).
@@ -454,6 +458,77 @@ int rqo_qmv_bf16(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
     }
     free(xf);
     free(xs);
+    return 0;
+}
+
+/* ------------------------------------------------------------ sb6 / K3
+ *
+ * rwkv-quant "sb6" tensors in the K3-interleaved layout that RwkvqLinear
+ * holds (layout stated at rwkv_metal/lora/rwkvq_kernel.py:18-25, arithmetic
+ * at rwkv_metal/lora/rwkvq_linear.py:140-175 and rwkvq_kernel.py:86-100).
+ * Blocks are 32 codes of one row (gw_gs = 32, rwkvq_kernel.py:36):
+ *   qblk[row, blk] : 16 bytes, byte j = code j (low nibble) | code j+16
+ *                    (high nibble); xbits >= 1 adds a uint32 whose bit c is
+ *                    bit 4 of code c; xbits == 2 one more for bit 5;
+ *   qsqm[row, blk] : (qs uint8, qm int8);
+ *   ddm[row, sblk] : (d, dm) float16, sblk = blk / gw_sb;
+ *   scale = f16(qs * d), min = f16(qm * dm) (fp32 products rounded to f16),
+ *   w = code * scale + min in fp32 (code * scale is exact: at most 6 + 11
+ *   significant bits, so this is one rounding however it is evaluated).
+ * The native repack (rwkvq_native.py:49-78) stores max(scale, 1e-8) as the
+ * affine scale and min as the bias, fp32, group size 32; the dense
+ * dequantize of the fused kernel (rwkvq_kernel.py:86-100) has no clamp. */
+void rqo_sb6_codes(const uint8_t* qblk, int64_t rows, int64_t cols, int xbits, uint8_t* codes) {
+    const int64_t nb = cols / 32, bb = 16 + 4 * xbits;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t b = 0; b < nb; ++b) {
+            const uint8_t* q = qblk + (r * nb + b) * bb;
+            uint8_t* c = codes + r * cols + b * 32;
+            for (int j = 0; j < 16; ++j) {
+                c[j] = q[j] & 0xF;
+                c[j + 16] = q[j] >> 4;
+            }
+            for (int x = 0; x < xbits; ++x) {
+                const uint32_t plane = (uint32_t)q[16 + 4 * x] | ((uint32_t)q[17 + 4 * x] << 8) |
+                                       ((uint32_t)q[18 + 4 * x] << 16) | ((uint32_t)q[19 + 4 * x] << 24);
+                for (int k = 0; k < 32; ++k) c[k] |= (uint8_t)(((plane >> k) & 1u) << (4 + x));
+            }
+        }
+}
+
+void rqo_sb6_scale_min(const uint8_t* qsqm, const uint16_t* ddm, int64_t rows, int64_t cols,
+                       int gw_sb, int clamp, float* scale, float* mn) {
+    const int64_t nb = cols / 32, nsb = nb / gw_sb;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t b = 0; b < nb; ++b) {
+            const float qs = (float)qsqm[(r * nb + b) * 2];
+            const float qm = (float)(int8_t)qsqm[(r * nb + b) * 2 + 1];
+            const float d = f16_to_f32(ddm[(r * nsb + b / gw_sb) * 2]);
+            const float dm = f16_to_f32(ddm[(r * nsb + b / gw_sb) * 2 + 1]);
+            float sc = round_to(RQ_F16, qs * d);
+            if (clamp && !(sc >= 1e-8f)) sc = 1e-8f;
+            scale[r * nb + b] = sc;
+            mn[r * nb + b] = round_to(RQ_F16, qm * dm);
+        }
+}
+
+int rqo_sb6_dequantize(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
+                       int64_t rows, int64_t cols, int gw_sb, int xbits, float* out) {
+    if (cols % 32 || xbits < 0 || xbits > 2 || gw_sb <= 0 || (cols / 32) % gw_sb) return -1;
+    const int64_t nb = cols / 32;
+    uint8_t* codes = (uint8_t*)malloc((size_t)(rows * cols));
+    float* sc = (float*)malloc((size_t)(rows * nb) * sizeof(float));
+    float* mn = (float*)malloc((size_t)(rows * nb) * sizeof(float));
+    rqo_sb6_codes(qblk, rows, cols, xbits, codes);
+    rqo_sb6_scale_min(qsqm, ddm, rows, cols, gw_sb, 0, sc, mn);
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t k = 0; k < cols; ++k) {
+            const float p = (float)codes[r * cols + k] * sc[r * nb + k / 32];
+            out[r * cols + k] = p + mn[r * nb + k / 32];
+        }
+    free(codes);
+    free(sc);
+    free(mn);
     return 0;
 }
 

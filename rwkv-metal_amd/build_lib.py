@@ -37,7 +37,8 @@ FLAGS = [
 
 
 def _units():
-    units = [("rq_quant.hip", [], "rq_quant.o"), ("rq_abi.cpp", ["-x", "hip"], "rq_abi.o")]
+    units = [("rq_quant.hip", [], "rq_quant.o"), ("rq_sb6.hip", [], "rq_sb6.o"),
+             ("rq_abi.cpp", ["-x", "hip"], "rq_abi.o")]
     for b in BITS:
         # MFMA results straight into VGPRs: the GEMV consumes every MFMA
         # result with VALU fmas, so accumulator registers only add copies

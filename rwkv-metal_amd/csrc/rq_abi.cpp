@@ -175,6 +175,54 @@ int rq_embedding(const int64_t* idx, int64_t n, const uint32_t* w_q, const void*
                          "rq_embedding");
 }
 
+// qblk is read only when codes are decoded (need_codes).
+static int check_sb6(const char* what, const uint8_t* qblk, const uint8_t* qsqm,
+                     const uint16_t* ddm, int64_t rows, int64_t cols, int gw_gs, int gw_sb,
+                     int xbits, bool need_codes) {
+    if (rows < 0 || cols < 0) return fail(RQ_EINVAL, "%s: negative size", what);
+    if (gw_gs != 32) return fail(RQ_EINVAL, "%s: sb6 blocks are 32 codes (gw_gs=%d)", what, gw_gs);
+    if (cols % 32) return fail(RQ_EINVAL, "%s: cols %lld is not a multiple of 32", what, (long long)cols);
+    if (xbits < 0 || xbits > 2) return fail(RQ_EINVAL, "%s: xbits must be 0, 1 or 2 (got %d)", what, xbits);
+    if (gw_sb <= 0 || (cols / 32) % gw_sb)
+        return fail(RQ_EINVAL, "%s: gw_sb=%d does not divide the %lld blocks per row", what, gw_sb,
+                    (long long)(cols / 32));
+    if (rows * cols && ((need_codes && !qblk) || !qsqm || !ddm))
+        return fail(RQ_EINVAL, "%s: NULL pointer", what);
+    if (((uintptr_t)qblk & 3) || ((uintptr_t)qsqm & 1) || ((uintptr_t)ddm & 3))
+        return fail(RQ_EALIGN, "%s: qblk and ddm must be 4-byte aligned, qsqm 2-byte aligned", what);
+    return RQ_OK;
+}
+
+int rq_sb6_dequantize(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, int64_t rows,
+                      int64_t cols, int gw_gs, int gw_sb, int xbits, void* out, rq_dtype out_dt,
+                      void* stream) {
+    if (int rc = check_sb6("rq_sb6_dequantize", qblk, qsqm, ddm, rows, cols, gw_gs, gw_sb, xbits,
+                           true))
+        return rc;
+    if (!valid_dt(out_dt)) return fail(RQ_EINVAL, "unsupported dtype");
+    if (rows * cols == 0) return ok();
+    if (!out) return fail(RQ_EINVAL, "rq_sb6_dequantize: NULL output");
+    if (!aligned16(out)) return fail(RQ_EALIGN, "rq_sb6_dequantize: out must be 16-byte aligned");
+    return launch_status(rq::launch_sb6_dequantize(qblk, qsqm, ddm, rows, cols, gw_sb, xbits, out,
+                                                   out_dt, (hipStream_t)stream),
+                         "rq_sb6_dequantize");
+}
+
+int rq_sb6_to_affine(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, int64_t rows,
+                     int64_t cols, int gw_gs, int gw_sb, int xbits, uint32_t* w_q, float* scales,
+                     float* biases, void* stream) {
+    if (int rc = check_sb6("rq_sb6_to_affine", qblk, qsqm, ddm, rows, cols, gw_gs, gw_sb, xbits,
+                           w_q != nullptr))
+        return rc;
+    if (rows * cols == 0) return ok();
+    if (!scales || !biases) return fail(RQ_EINVAL, "rq_sb6_to_affine: NULL scales/biases");
+    if (((uintptr_t)w_q | (uintptr_t)scales | (uintptr_t)biases) & 3)
+        return fail(RQ_EALIGN, "rq_sb6_to_affine: outputs must be 4-byte aligned");
+    return launch_status(rq::launch_sb6_to_affine(qblk, qsqm, ddm, rows, cols, gw_sb, xbits, w_q,
+                                                  scales, biases, (hipStream_t)stream),
+                         "rq_sb6_to_affine");
+}
+
 int rq_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* w_q,
             void* stream) {
     if (int rc = check_common(rows, cols, 32, bits)) return rc;

@@ -22,6 +22,15 @@ hipError_t launch_embedding(const int64_t* idx, int64_t n, const uint32_t* wq,
                             int64_t cols, int gs, int bits, void* out, int out_dt,
                             hipStream_t stream);
 
+// rwkv-quant sb6 (K3-interleaved) tensors: dense dequantize, and the repack
+// into the MLX affine layout (bits = 4 + xbits, fp32 scales/biases, gs 32).
+hipError_t launch_sb6_dequantize(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
+                                 int64_t rows, int64_t cols, int gw_sb, int xbits, void* out,
+                                 int out_dt, hipStream_t stream);
+hipError_t launch_sb6_to_affine(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
+                                int64_t rows, int64_t cols, int gw_sb, int xbits, uint32_t* wq,
+                                float* scales, float* biases, hipStream_t stream);
+
 hipError_t launch_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* wq,
                        hipStream_t stream);
 

@@ -53,6 +53,8 @@ SIGNATURES = {
                _i32),
     "rq_embedding": ([_vp, _i64, _vp, _vp, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _i32, _vp],
                      _i32),
+    "rq_sb6_dequantize": ([_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _i32, _vp], _i32),
+    "rq_sb6_to_affine": ([_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "rq_pack": ([_vp, _i64, _i64, _i32, _vp, _vp], _i32),
     "rq_unpack": ([_vp, _i64, _i64, _i32, _vp, _vp], _i32),
     "rq_qmm_grouped": ([ctypes.POINTER(RqProblem), _i32, _i32, _i32, _i32, _i64, _i32, _i32, _vp],

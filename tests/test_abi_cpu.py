@@ -27,7 +27,8 @@ def test_header_declares_the_expected_surface():
     assert declared_functions() == sorted([
         "rq_abi_version", "rq_last_error", "rq_quantize", "rq_dequantize", "rq_qmm",
         "rq_pack", "rq_unpack", "rq_qmm_grouped", "rq_grouped_plan_table_bytes",
-        "rq_grouped_plan_init", "rq_grouped_plan_run", "rq_embedding"])
+        "rq_grouped_plan_init", "rq_grouped_plan_run", "rq_embedding", "rq_sb6_dequantize",
+        "rq_sb6_to_affine"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -60,6 +61,14 @@ def test_invalid_arguments_return_einval(L):
     assert "NULL" in _err(L)
     assert L.rq_embedding(p, 3, p, p, p, 0, 8, 64, 64, 7, p, 0, None) == -1
     assert L.rq_embedding(p, 0, p, p, p, 0, 8, 64, 64, 4, p, 0, None) == 0
+    assert L.rq_sb6_dequantize(p, p, p, 4, 64, 64, 1, 2, p, 2, None) == -1
+    assert "32 codes" in _err(L)
+    assert L.rq_sb6_dequantize(p, p, p, 4, 64, 32, 1, 3, p, 2, None) == -1
+    assert "xbits" in _err(L)
+    assert L.rq_sb6_dequantize(p, p, p, 4, 96, 32, 2, 0, p, 2, None) == -1
+    assert "gw_sb" in _err(L)
+    assert L.rq_sb6_to_affine(p, p, p, 4, 64, 32, 1, 0, p, 0, p, None) == -1
+    assert L.rq_sb6_to_affine(p + 1, p, p, 4, 64, 32, 1, 0, p, p, p, None) == -2
 
 
 def test_misaligned_pointers_return_ealign(L):

@@ -688,3 +688,137 @@ def test_quantized_checkpoint_roundtrip_gpu(O, rq, dev, tmp_path):
 
     assert dst.head.bits == 8 and dst.key.bits == 3
     assert torch.equal(run(src), run(dst))
+
+
+# ------------------------------------------------------------ sb6 / K3
+
+@pytest.mark.parametrize("xbits", [0, 1, 2])
+def test_sb6_dequantize_and_repack_bit_exact(O, rq, dev, xbits):
+    """rq_sb6_dequantize (fp32 and bf16) and rq_sb6_to_affine (packed codes,
+    clamped fp32 scales, biases; scales-only mode) against the oracle, bit for
+    bit, including subnormal float16 super-block scales."""
+    import sb6_k3 as k3
+    from rwkvq import sb6
+    R, K, gw_sb = 37, 1024, 8
+    codes, qs, qm, d, dm = k3.random_sb6(R, K, xbits, gw_sb, seed=100 + xbits, tiny=True)
+    qblk, qsqm, ddm = k3.encode(codes, qs, qm, d, dm, xbits)
+    say(f"sb6 xbits={xbits}")
+    lin = rq.RwkvqLinear(qblk.to(dev), qsqm.to(dev), ddm.to(dev), (R, K), 32, gw_sb, xbits)
+    want = O.sb6_dequantize(qblk, qsqm, ddm, R, K, gw_sb, xbits)
+    assert bits_equal(lin._dequant_w_fp32(), want)
+    assert bits_equal(lin._dequant_w(), want.to(torch.bfloat16))
+    wq, sc, bi = sb6._to_affine(lin)
+    assert torch.equal(wq.cpu(), O.pack(O.sb6_codes(qblk, R, K, xbits), 4 + xbits))
+    osc, omn = O.sb6_scale_min(qsqm, ddm, R, K, gw_sb, clamp=True)
+    assert bits_equal(sc, osc) and bits_equal(bi, omn)
+    hyb = rq.RwkvqHybridLinear(lin)
+    hs, hb = hyb._expand_scale_bias()
+    assert bits_equal(hs, osc) and bits_equal(hb, omn) and torch.equal(hyb.wq, wq)
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_sb6_linear_modules(O, rq, dev, xdt):
+    """The three sb6 bases agree with the oracle's products: RwkvqNativeLinear
+    and RwkvqHybridLinear (quantized_matmul on the repacked layout, fp32 x,
+    group 32; identical bits to each other) and RwkvqLinear (dense dequant +
+    matmul), within rel-err 1e-2, at decode (M=1, 8) and prefill (M=300)."""
+    import sb6_k3 as k3
+    R, K, gw_sb, xbits = 256, 2048, 8, 2
+    codes, qs, qm, d, dm = k3.random_sb6(R, K, xbits, gw_sb, seed=7)
+    qs[qs == 0] = 1
+    qblk, qsqm, ddm = k3.encode(codes, qs, qm, d, dm, xbits)
+    lin = rq.RwkvqLinear(qblk.to(dev), qsqm.to(dev), ddm.to(dev), (R, K), 32, gw_sb, xbits)
+    nat, hyb = rq.RwkvqNativeLinear(lin), rq.RwkvqHybridLinear(lin)
+    wq = O.pack(O.sb6_codes(qblk, R, K, xbits), 4 + xbits)
+    osc, omn = O.sb6_scale_min(qsqm, ddm, R, K, gw_sb, clamp=True)
+    dense = O.sb6_dequantize(qblk, qsqm, ddm, R, K, gw_sb, xbits).double()
+    for M in (1, 8, 300):
+        x = acts(M, K, M, xdt)
+        say(f"sb6 modules x={xdt} M={M}")
+        yn = nat(x.to(dev))
+        assert yn.dtype == xdt and torch.equal(yn, hyb(x.to(dev)))
+        ref = O.quantized_matmul(x.float(), wq, osc, omn, True, 32, 6, out_dtype=torch.float32,
+                                 weights="exact")
+        rel_check(yn, ref, what=f"native M{M}")
+        yl = lin(x.to(dev))
+        rel_check(yl, x.double() @ dense.t(), what=f"RwkvqLinear M{M}")
+
+
+def test_add_lora_rwkvq_from_sidecar(O, rq, dev, tmp_path):
+    """add_lora_rwkvq swaps tmix projections (LoRA-wrapped), cmix key/value and
+    the head for the sb6 base read from a sidecar (<path>.safetensors +
+    <path>.json, official key names); only the adapters train; the forward of
+    a wrapped projection equals the base plus the LoRA term."""
+    import json
+    from safetensors.torch import save_file
+    from torch import nn
+    import sb6_k3 as k3
+
+    D, V, L = 256, 512, 2
+
+    class TMix(nn.Module):
+        def __init__(self):
+            super().__init__()
+            for n in ("r_proj", "k_proj", "v_proj", "o_proj"):
+                setattr(self, n, nn.Linear(D, D, bias=False))
+
+    class CMix(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.key, self.value = nn.Linear(D, 4 * D, bias=False), nn.Linear(4 * D, D, bias=False)
+
+    class Blk(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.tmix, self.cmix = TMix(), CMix()
+
+    class Model(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.blocks = nn.ModuleList([Blk() for _ in range(L)])
+            self.head = nn.Linear(D, V, bias=False)
+
+    shapes = {"head.weight": (V, D)}
+    for i in range(L):
+        for n in ("receptance", "key", "value", "output"):
+            shapes[f"blocks.{i}.att.{n}.weight"] = (D, D)
+        shapes[f"blocks.{i}.ffn.key.weight"] = (4 * D, D)
+        shapes[f"blocks.{i}.ffn.value.weight"] = (D, 4 * D)
+    arrays, meta = {}, {"tensors": {}}
+    for j, (key, (R, K)) in enumerate(shapes.items()):
+        xb = j % 3
+        codes, qs, qm, d, dm = k3.random_sb6(R, K, xb, 4, seed=j)
+        qblk, qsqm, ddm = k3.encode(codes, qs, qm, d, dm, xb)
+        arrays[f"{key}::qblk"], arrays[f"{key}::qsqm"], arrays[f"{key}::ddm"] = qblk, qsqm, ddm
+        meta["tensors"][key] = {"kind": "sb6", "shape": [R, K], "gw_gs": 32, "gw_sb": 4,
+                                "xbits": xb}
+    side = str(tmp_path / "model.rwkvq_mlx")
+    save_file(arrays, side + ".safetensors")
+    with open(side + ".json", "w") as f:
+        json.dump(meta, f)
+
+    model = Model().to(dev, torch.bfloat16)
+    model, info = rq.add_lora_rwkvq(model, side, rank=8, alpha=16.0, layers=[-1])
+    say("add_lora_rwkvq")
+    assert info["num_lora_adapters"] == 4 and info["wrapped_per_block"] == [
+        "tmix.k_proj", "tmix.o_proj", "tmix.r_proj", "tmix.v_proj"]
+    blk = model.blocks[1]
+    assert isinstance(blk.tmix.r_proj, rq.LoRALinear)
+    assert isinstance(blk.tmix.r_proj.linear, rq.RwkvqNativeLinear)
+    assert isinstance(blk.cmix.value, rq.RwkvqNativeLinear) and blk.cmix.value.bits == 4 + (
+        list(shapes).index("blocks.1.ffn.value.weight") % 3)
+    assert isinstance(model.head, rq.RwkvqNativeLinear)
+    assert isinstance(model.blocks[0].tmix.r_proj, nn.Linear)   # layer 0 not selected
+    trainable = {n for n, p in model.named_parameters() if p.requires_grad}
+    assert trainable == {f"blocks.1.tmix.{n}.lora_{ab}" for n in ("r_proj", "k_proj", "v_proj",
+                                                                   "o_proj") for ab in "ab"}
+    with torch.no_grad():
+        blk.tmix.k_proj.lora_b.normal_()
+    x = acts(4, D, 3).to(dev)
+    lay = blk.tmix.k_proj
+    y = lay(x)
+    ref = lay.linear(x).float() + lay.scale * ((x.float() @ lay.lora_a.float().t())
+                                               @ lay.lora_b.float().t())
+    rel_check(y, ref, what="lora over sb6")
+    with pytest.raises(NotImplementedError):
+        rq.load_sidecar(str(tmp_path / "model.rwkvq"))

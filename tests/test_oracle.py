@@ -246,3 +246,66 @@ def test_quantize_rejects_bad_arguments(O):
         O.quantize(w, 64, 7)
     with pytest.raises(ValueError):
         O.quantize(torch.zeros(2, 96), 64, 4)
+
+
+# ------------------------------------------------------------ sb6 / K3
+
+@pytest.mark.parametrize("xbits", [0, 1, 2])
+def test_sb6_oracle_matches_the_layout_text(O, xbits):
+    """The oracle's sb6 decode against an independent encoder written from
+    the layout text (tests/sb6_k3.py): codes round-trip exactly, scale/min are
+    numpy's f16(qs*d) / f16(qm*dm), and the dense weight is code*scale + min
+    in fp32, bit for bit (including subnormal float16 super-block scales)."""
+    import sb6_k3 as k3
+    R, K, gw_sb = 7, 512, 4
+    codes, qs, qm, d, dm = k3.random_sb6(R, K, xbits, gw_sb, seed=xbits, tiny=True)
+    qblk, qsqm, ddm = k3.encode(codes, qs, qm, d, dm, xbits)
+    assert torch.equal(O.sb6_codes(qblk, R, K, xbits), torch.from_numpy(codes).to(torch.uint8))
+    sc, mn = O.sb6_scale_min(qsqm, ddm, R, K, gw_sb)
+    esc, emn = k3.scale_min(qs, qm, d, dm, gw_sb)
+    assert np.array_equal(sc.numpy().view(np.int32), esc.view(np.int32))
+    assert np.array_equal(mn.numpy().view(np.int32), emn.view(np.int32))
+    w = O.sb6_dequantize(qblk, qsqm, ddm, R, K, gw_sb, xbits)
+    assert np.array_equal(w.numpy().view(np.int32), k3.dense(codes, qs, qm, d, dm, gw_sb).view(np.int32))
+
+
+def test_sb6_oracle_hand_worked_block(O):
+    """One block decoded by hand: byte 0 = 0xA3 gives code 0 = 3 and code 16
+    = 10; bit 0 of the first plane adds 16 to code 0, bit 16 of the second adds
+    32 to code 16; qs = 5, d = 0.5 -> scale 2.5; qm = -3 (byte 0xFD), dm = 0.25
+    -> min -0.75; w0 = 19*2.5 - 0.75 = 46.75, w16 = 42*2.5 - 0.75 = 104.25."""
+    blk = np.zeros(24, dtype=np.uint8)
+    blk[0] = 0xA3
+    blk[16:20] = np.array([1, 0, 0, 0], dtype=np.uint8)        # plane 1: bit 0
+    blk[20:24] = np.array([0, 0, 1, 0], dtype=np.uint8)        # plane 2: bit 16
+    qblk = torch.from_numpy(blk.reshape(1, 24))
+    codes = O.sb6_codes(qblk, 1, 32, 2)
+    assert codes[0, 0].item() == 3 + 16 and codes[0, 16].item() == 10 + 32
+    assert codes[0, 1:16].sum().item() == 0 and codes[0, 17:].sum().item() == 0
+    qsqm = torch.tensor([[5, 0xFD]], dtype=torch.uint8)
+    ddm = torch.tensor([[0.5, 0.25]], dtype=torch.float16)
+    w = O.sb6_dequantize(qblk, qsqm, ddm, 1, 32, 1, 2)
+    assert w[0, 0].item() == 46.75 and w[0, 16].item() == 104.25 and w[0, 1].item() == -0.75
+    sc, _ = O.sb6_scale_min(qsqm, torch.tensor([[-0.5, 0.25]], dtype=torch.float16), 1, 32, 1,
+                            clamp=True)
+    assert sc[0, 0].item() == pytest.approx(1e-8)   # max(scale, 1e-8) of the native repack
+
+
+def test_sb6_repack_equals_affine_dequantize(O):
+    """The native repack (codes into the MLX bitstream at 4+xbits bits, fp32
+    scale/bias, group 32) dequantizes, through the affine oracle, to exactly
+    the sb6 dense weight: MLX's fp32 s*q then +b is the same single rounding."""
+    import sb6_k3 as k3
+    R, K, gw_sb, xbits = 5, 256, 2, 2
+    codes, qs, qm, d, dm = k3.random_sb6(R, K, xbits, gw_sb, seed=11)
+    zero = qs == 0          # scale 0: the repack stores max(0, 1e-8) instead
+    assert zero.any() and not zero.all()
+    qblk, qsqm, ddm = k3.encode(codes, qs, qm, d, dm, xbits)
+    wq = O.pack(O.sb6_codes(qblk, R, K, xbits), 4 + xbits)
+    sc, mn = O.sb6_scale_min(qsqm, ddm, R, K, gw_sb, clamp=True)
+    got = O.dequantize(wq, sc, mn, 32, 4 + xbits)
+    want = O.sb6_dequantize(qblk, qsqm, ddm, R, K, gw_sb, xbits)
+    same = ~torch.from_numpy(np.repeat(zero, 32, axis=1))
+    assert torch.equal(got[same].view(torch.int32), want[same].view(torch.int32))
+    clamped = torch.from_numpy(codes).float() * np.float32(1e-8) + want  # want = min there
+    assert torch.equal(got[~same], clamped[~same])
