@@ -262,6 +262,54 @@ def config5(torch, rq, dev, args):
     return out
 
 
+def qlora_step(torch, rq, dev, ws, args):
+    """one QLoRA training step of one RWKV-7 1.5B layer
+    (D=2048) on a frozen 4-bit g64 base -- for each of r, k, v, o, ffn_key,
+    ffn_value: y = qmm(x, Wq) + (alpha/r) (x A^T) B^T, r = alpha = 16,
+    A ~ N(0, 1/D), B ~ N(0, 0.01) (std), x [8, 512, K] bf16, then dX, dA, dB
+    for a given dY.  `fused`: LoRALinear's path (low-rank term in the GEMMs'
+    output stage, rq_qmm_lora); `composed`: the same layer as separate ops
+    (quantized_matmul + two torch GEMMs + scale + add, autograd).  Reported:
+    ms per layer step and the step's TFLOP/s (base forward + dX GEMMs, 4*M*R*K,
+    plus the adapter GEMMs)."""
+    from torch import nn
+    r, alpha, M = 16, 16.0, 8 * 512
+    layers, flops = [], 0.0
+    for name, R, K in PROJ:
+        wq, s, b = ws[PROJ.index((name, R, K))]
+        base = rq.QuantizedLinear(K, R, bias=False, group_size=64, bits=4, device=dev)
+        base.weight, base.scales, base.biases = wq, s, b
+        lay = rq.LoRALinear(rank=r, alpha=alpha, base_module=base)
+        g = torch.Generator(device=dev).manual_seed(4_000_000 + R * 7 + K)
+        with torch.no_grad():
+            lay.lora_a.copy_((torch.randn(r, K, generator=g, device=dev) / K ** 0.5).to(torch.bfloat16))
+            lay.lora_b.copy_((torch.randn(R, r, generator=g, device=dev) * 0.01).to(torch.bfloat16))
+        x = torch.randn(8, 512, K, device=dev).to(torch.bfloat16).requires_grad_(True)
+        dy = torch.randn(8, 512, R, device=dev).to(torch.bfloat16)
+        layers.append((lay, x, dy))
+        flops += 4.0 * M * R * K + 6.0 * M * r * (R + K)
+
+    def fused():
+        for lay, x, dy in layers:
+            torch.autograd.grad(lay(x), (x, lay.lora_a, lay.lora_b), dy)
+
+    def composed():
+        for lay, x, dy in layers:
+            base = rq.quantized_matmul(x, lay.linear.weight, lay.linear.scales,
+                                       lay.linear.biases, True, 64, 4)
+            y = base + lay.scale * ((x @ lay.lora_a.t()) @ lay.lora_b.t())
+            torch.autograd.grad(y, (x, lay.lora_a, lay.lora_b), dy)
+
+    out = {}
+    for key, fn in (("fused", fused), ("composed", composed)):
+        t = time_region(torch, fn, max(5, args.steps // 10), 3)
+        out[key] = {"ms_per_layer_step": round(t * 1e3, 3),
+                    "tflops": round(flops / t / 1e12, 1)}
+    out["speedup_fused"] = round(out["composed"]["ms_per_layer_step"]
+                                 / out["fused"]["ms_per_layer_step"], 3)
+    return out
+
+
 def gemm_steady_state(torch, rq, dev, seconds=0.15):
     """Untimed MFMA-heavy GEMM work before the GEMM measurements: coming from
     the memory-bound decode sweeps, the first ~100 ms of back-to-back GEMMs
@@ -448,6 +496,7 @@ def main():
                              max(5, args.steps // 2), GEMM_WARMUP)
             bwd[name] = round(2.0 * 4096 * R * K / tn / 1e12, 1)
         extra["qlora_dx_m4096_tflops"] = bwd
+        extra["qlora_step_config4"] = qlora_step(torch, rwkvq, dev, ws, args)
         del ws, xs, xs8, outs8, plan8, singles
         extra["config5_mixed_bit"] = config5(torch, rwkvq, dev, args)
         result["extra"] = extra

@@ -20,6 +20,9 @@
  *                     code extraction inside mx.dequantize
  *   rq_embedding   <- nn.QuantizedEmbedding lookup (gather + mx.dequantize), target "emb"
  *                     of rwkv_metal/lora/finetune.py:42, used at rwkv_metal/model/rwkv7_x070.py:302
+ *   rq_qmm_lora    <- LoRALinear.__call__ over a quantized base (rwkv_metal/lora/lora.py:58-63)
+ *                     and its dX (finetune.py:141): the low-rank term fused into rq_qmm's
+ *                     output stage
  *   rq_sb6_dequantize / rq_sb6_to_affine
  *                  <- the .rwkvq (rwkv-quant sb6) base: RwkvqLinear's fused dequant
  *                     (rwkv_metal/lora/rwkvq_kernel.py) and RwkvqNativeLinear's repack into
@@ -135,6 +138,24 @@ int rq_sb6_dequantize(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* 
 int rq_sb6_to_affine(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, int64_t rows,
                      int64_t cols, int gw_gs, int gw_sb, int xbits, uint32_t* w_q, float* scales,
                      float* biases, void* stream);
+
+/* The QLoRA layer over a quantized base (LoRALinear.__call__,
+ * rwkv_metal/lora/lora.py:58-63: base(x) + scale * (x A^T) B^T) with the
+ * low-rank term fused into the GEMM's output stage:
+ *   y = rq_qmm(x, ...) + scale * z . L^T
+ * z: bf16 [m, rank]; lora (L): bf16 [n_out, rank], n_out = rows (transpose=1)
+ * or cols (transpose=0).  Forward: z = x . lora_a^T, L = lora_b.  Backward dX
+ * (the transpose=0 product of the QLoRA backward, finetune.py:141):
+ * z = dY . lora_b, L = lora_a^T.  rank in {16, 32, 48, 64}; the term is
+ * accumulated in fp32 with the GEMM and rounded once into y_dt.  Runs on the
+ * 64-wide-stage GEMMs only (bf16 x, m >= 256, 16-bit scales 16-byte aligned;
+ * transpose=1: cols a multiple of 8 groups; transpose=0: rows % 64 == 0,
+ * cols % 128 == 0); other problems return RQ_EUNSUPPORTED and the caller
+ * runs rq_qmm plus the term separately. */
+int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
+                const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
+                int group_size, int bits, int transpose, const void* z, const void* lora,
+                int64_t rank, float scale, void* y, rq_dtype y_dt, void* stream);
 
 /* Pack codes uint8[rows, cols] (values < 2^bits) into the MLX bitstream
  * w_q uint32[rows, cols*bits/32].  cols must be a multiple of 32. */

@@ -21,9 +21,11 @@ namespace rq {
     hipError_t launch_qmv_b##B(const rq_problem*, int, int, int, int, int64_t, int,             \
                                hipStream_t);                                                    \
     hipError_t launch_qmm_t_b##B(const void*, int, const uint32_t*, const void*, const void*,    \
-                                 int, int64_t, int64_t, int64_t, int, void*, int, hipStream_t); \
+                                 int, int64_t, int64_t, int64_t, int, void*, int, hipStream_t,  \
+                                 const LoraArgs*);                                              \
     hipError_t launch_qmm_n_b##B(const void*, int, const uint32_t*, const void*, const void*,    \
-                                 int, int64_t, int64_t, int64_t, int, void*, int, hipStream_t);
+                                 int, int64_t, int64_t, int64_t, int, void*, int, hipStream_t,  \
+                                 const LoraArgs*);
 #define RQ_DECLARE_TABLE(B)                                                                    \
     hipError_t launch_qmv_table_b##B(const QmvTable&, int, int, int, size_t, hipStream_t);
 RQ_DECLARE_TABLE(2)
@@ -68,19 +70,19 @@ hipError_t launch_qmv(const rq_problem* problems, int n, int x_dt, int sb_dt, in
 
 #define RQ_QMM_SWITCH(FN)                                                                      \
     switch (bits) {                                                                            \
-        case 2: return FN##2(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
-        case 3: return FN##3(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
-        case 4: return FN##4(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
-        case 5: return FN##5(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
-        case 6: return FN##6(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
-        case 8: return FN##8(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream); \
+        case 2: return FN##2(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream, lora); \
+        case 3: return FN##3(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream, lora); \
+        case 4: return FN##4(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream, lora); \
+        case 5: return FN##5(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream, lora); \
+        case 6: return FN##6(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream, lora); \
+        case 8: return FN##8(x, x_dt, wq, scales, biases, sb_dt, m, rows, cols, gs, y, y_dt, stream, lora); \
         default: return hipErrorInvalidValue;                                                  \
     }
 
 static hipError_t launch_qmm(int transpose, const void* x, int x_dt, const uint32_t* wq,
                              const void* scales, const void* biases, int sb_dt, int64_t m,
                              int64_t rows, int64_t cols, int gs, int bits, void* y, int y_dt,
-                             hipStream_t stream) {
+                             hipStream_t stream, const LoraArgs* lora = nullptr) {
     if (transpose) {
         RQ_QMM_SWITCH(launch_qmm_t_b)
     } else {
@@ -263,6 +265,35 @@ int rq_qmm(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales
                            group_size, bits, y, y_dt, (hipStream_t)stream);
     }
     return launch_status(e, "rq_qmm");
+}
+
+int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
+                const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
+                int group_size, int bits, int transpose, const void* z, const void* lora,
+                int64_t rank, float scale, void* y, rq_dtype y_dt, void* stream) {
+    if (int rc = check_common(rows, cols, group_size, bits)) return rc;
+    if (!valid_dt(x_dt) || !valid_dt(sb_dt) || !valid_dt(y_dt)) return fail(RQ_EINVAL, "unsupported dtype");
+    if (m < 0) return fail(RQ_EINVAL, "negative m");
+    if (rank < 16 || rank > 64 || rank % 16)
+        return fail(RQ_EINVAL, "rq_qmm_lora: rank must be 16, 32, 48 or 64 (got %lld)", (long long)rank);
+    const int64_t n_out = transpose ? rows : cols;
+    if (m == 0 || n_out == 0) return ok();
+    const int64_t n_in = transpose ? cols : rows;
+    if (n_in == 0) return fail(RQ_EINVAL, "rq_qmm_lora: empty contraction is not supported");
+    if (!x || !w_q || !scales || !biases || !y || !z || !lora)
+        return fail(RQ_EINVAL, "rq_qmm_lora: NULL pointer");
+    if (!aligned16(x) || !aligned16(w_q) || !aligned16(z) || !aligned16(lora))
+        return fail(RQ_EALIGN, "rq_qmm_lora: x, w_q, z and lora must be 16-byte aligned");
+    const rq::LoraArgs lo{z, lora, (int)rank, scale};
+    const hipError_t e = rq::launch_qmm(transpose, x, x_dt, w_q, scales, biases, sb_dt, m, rows,
+                                        cols, group_size, bits, y, y_dt, (hipStream_t)stream, &lo);
+    if (e == hipErrorNotSupported)
+        return fail(RQ_EUNSUPPORTED,
+                    "rq_qmm_lora: the fused low-rank term needs the 64-wide-stage GEMMs (bf16 x, "
+                    "m >= 256, 16-bit 16-byte aligned scales; transpose=1: cols a multiple of 8 "
+                    "groups; transpose=0: rows %% 64 == 0, cols %% 128 == 0); use rq_qmm and add "
+                    "the term separately");
+    return launch_status(e, "rq_qmm_lora");
 }
 
 static int check_grouped(const char* what, const rq_problem* problems, int n, rq_dtype x_dt,

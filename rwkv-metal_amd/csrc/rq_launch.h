@@ -57,14 +57,27 @@ bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs, int bi
 hipError_t launch_qmv_table(const QmvTable& t, int blocks, int sb_dt, int gs, int bits,
                             size_t lds, hipStream_t stream);
 
+// Low-rank term fused into the output stage of the 64-wide-stage GEMMs:
+// y += scale * z . L^T with z [m, rank] and L [n_out, rank], both bf16,
+// rank a multiple of 16 and at most 64.  A launcher given one returns
+// hipErrorNotSupported when its problem does not run on those kernels.
+struct LoraArgs {
+    const void* z;
+    const void* l;
+    int rank;
+    float scale;
+};
+
 // MFMA GEMM, transpose=True: y[m, rows] = x[m, cols] . W^T.
 hipError_t launch_qmm_t(const void* x, int x_dt, const uint32_t* wq, const void* scales,
                         const void* biases, int sb_dt, int64_t m, int64_t rows, int64_t cols,
-                        int gs, int bits, void* y, int y_dt, hipStream_t stream);
+                        int gs, int bits, void* y, int y_dt, hipStream_t stream,
+                        const LoraArgs* lora = nullptr);
 
 // MFMA GEMM, transpose=False: y[m, cols] = x[m, rows] . W.
 hipError_t launch_qmm_n(const void* x, int x_dt, const uint32_t* wq, const void* scales,
                         const void* biases, int sb_dt, int64_t m, int64_t rows, int64_t cols,
-                        int gs, int bits, void* y, int y_dt, hipStream_t stream);
+                        int gs, int bits, void* y, int y_dt, hipStream_t stream,
+                        const LoraArgs* lora = nullptr);
 
 }  // namespace rq

@@ -1337,6 +1337,48 @@ RQ_DEV void store_wave_tile(const f32x4_t (&acc)[TM][TN], uint8_t* stg, void* __
     }
 }
 
+// The QLoRA low-rank term in the output stage: acc += scale * z . L^T for a
+// wave's 128 x WN tile (rows r0.., columns c0..; acc in the weight-as-A
+// layout of store_wave_tile).  z [nrows, rank] and L [ncols, rank] are bf16
+// and small (rank <= 64), read straight from global memory: lane (lg, lr)
+// takes elements 8*lg .. +7 of a 32-wide rank slice of row lr of each 16-row
+// tile; slices past the rank and rows past the bounds read as zero.
+template <int TM, int TN>
+RQ_DEV void lora_epilogue(f32x4_t (&acc)[TM][TN], const rq::LoraArgs& lo, int64_t nrows,
+                          int64_t ncols, int64_t r0, int64_t c0, int lane) {
+    const int lg = lane >> 4, lr = lane & 15;
+    const uint16_t* z = (const uint16_t*)lo.z;
+    const uint16_t* l = (const uint16_t*)lo.l;
+    for (int j0 = 0; j0 < lo.rank; j0 += 32) {
+        const int j = j0 + 8 * lg;
+        const bool has = j < lo.rank;
+        bf16x8_t zf[TM], lf[TN];
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+            const int64_t m = r0 + a * 16 + lr;
+            u32x4_t v = {0u, 0u, 0u, 0u};
+            if (has && m < nrows) v = *(const u32x4_t*)(z + m * lo.rank + j);
+            zf[a] = __builtin_bit_cast(bf16x8_t, v);
+        }
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int64_t n = c0 + b * 16 + lr;
+            u32x4_t v = {0u, 0u, 0u, 0u};
+            if (has && n < ncols) v = *(const u32x4_t*)(l + n * lo.rank + j);
+            lf[b] = __builtin_bit_cast(bf16x8_t, v);
+        }
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < TN; ++b) {
+                const f32x4_t t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    lf[b], zf[a], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(lo.scale, t[r], acc[a][b][r]);
+            }
+    }
+}
+
 // ------------------------------------------------------------- qmm_t_k64
 //
 // The warp-specialised GEMM with 64-element contraction stages (bf16
@@ -1365,7 +1407,7 @@ template <int BITS, int SDT, int BN, int GSH>
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, void* __restrict__ y,
-    int y_dt, int tiles_m, int tiles_n) {
+    int y_dt, int tiles_m, int tiles_n, rq::LoraArgs lora) {
     constexpr int BM = 256;
     constexpr int WN = BN / 2;
     constexpr int TM = 8, TN = WN / 16;
@@ -1606,6 +1648,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
 
     // after the last barrier the ring slot of stage nst - 2 (nst & 1) is read
     // by nobody and written by nobody: 8 KB of it per wave stage the output
+    if (lora.z) lora_epilogue<TM, TN>(acc, lora, M, R, m0 + wm * 128, n0 + wn * WN, lane);
     store_wave_tile<TM, TN>(acc, ((nst & 1) ? xs1 : xs0) + wave * 8192, y, y_dt, M, R,
                             m0 + wm * 128, n0 + wn * WN, lane);
 }
@@ -1629,7 +1672,7 @@ template <int BITS, int SDT>
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
-    void* __restrict__ y, int y_dt, int tiles_m, int tiles_n) {
+    void* __restrict__ y, int y_dt, int tiles_m, int tiles_n, rq::LoraArgs lora) {
     constexpr int BM = 256, BN = 128, WN = BN / 2;
     constexpr int TM = 8, TN = WN / 16;
     constexpr int BLD = 72;                 // bf16 tile row stride (64 + 8 elements)
@@ -1874,6 +1917,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
     }
 
     // after the last barrier the ring slot of stage nst - 2 (nst & 1) is free
+    if (lora.z) lora_epilogue<TM, TN>(acc, lora, M, K, m0 + wm * 128, k0 + wn * WN, lane);
     store_wave_tile<TM, TN>(acc, ((nst & 1) ? xs1 : xs0) + wave * 8192, y, y_dt, M, K,
                             m0 + wm * 128, k0 + wn * WN, lane);
 }
@@ -1888,8 +1932,9 @@ namespace rq {
 hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32_t* wq,
                                       const void* scales, const void* biases, int sb_dt,
                                       int64_t m, int64_t rows, int64_t cols, int gs, void* y,
-                                      int y_dt, hipStream_t stream) {
+                                      int y_dt, hipStream_t stream, const LoraArgs* lora) {
     const int gs_shift = __builtin_ctz(gs);
+    const LoraArgs lo = lora ? *lora : LoraArgs{nullptr, nullptr, 0, 0.f};
     // 64-wide stages: 16-bit 16-byte aligned scales, whole 8-group chunks
     if (m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 && cols % 64 == 0 &&
         (cols / gs) % 8 == 0 && (((uintptr_t)scales | (uintptr_t)biases) & 15) == 0) {
@@ -1901,7 +1946,8 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
         const int blocks = ((tm * tn + 7) / 8) * 8;
 #define RQ_K64(SD, BNV, GSHV)                                                                     \
     hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, BNV, GSHV>), dim3(blocks), dim3(kWsBlock), 0,     \
-                       stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols, y, y_dt, tm, tn)
+                       stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols, y, y_dt, tm, tn,  \
+                       lo)
 #define RQ_K64_GS(SD, BNV)                                                                        \
     switch (gs_shift) {                                                                           \
         case 5: RQ_K64(SD, BNV, 5); break;                                                        \
@@ -1921,6 +1967,7 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
 #undef RQ_K64
         return hipGetLastError();
     }
+    if (lora) return hipErrorNotSupported;  // the low-rank term rides on the k64 kernels only
     if (m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_REG) {
         const int bn = rows % 160 == 0 ? 160 : 128;
         const int tm = (int)((m + 255) / 256);
@@ -1984,7 +2031,8 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
 hipError_t RQ_CAT(launch_qmm_n_b, RQ_BITS)(const void* x, int x_dt, const uint32_t* wq,
                                       const void* scales, const void* biases, int sb_dt,
                                       int64_t m, int64_t rows, int64_t cols, int gs, void* y,
-                                      int y_dt, hipStream_t stream) {
+                                      int y_dt, hipStream_t stream, const LoraArgs* lora) {
+    const LoraArgs lo = lora ? *lora : LoraArgs{nullptr, nullptr, 0, 0.f};
     // warp-specialised transposed GEMM: bf16 dY, 16-bit aligned scales,
     // whole stages of 64 weight rows and 128 output columns
     if (m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 && rows % 64 == 0 &&
@@ -1996,13 +2044,14 @@ hipError_t RQ_CAT(launch_qmm_n_b, RQ_BITS)(const void* x, int x_dt, const uint32
         if (sb_dt == RQ_BF16)
             hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_BF16>), dim3(blocks), dim3(kWsBlock), 0,
                                stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
-                               __builtin_ctz(gs), y, y_dt, tm, tn);
+                               __builtin_ctz(gs), y, y_dt, tm, tn, lo);
         else
             hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_F16>), dim3(blocks), dim3(kWsBlock), 0,
                                stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
-                               __builtin_ctz(gs), y, y_dt, tm, tn);
+                               __builtin_ctz(gs), y, y_dt, tm, tn, lo);
         return hipGetLastError();
     }
+    if (lora) return hipErrorNotSupported;  // the low-rank term rides on the k64 kernels only
     constexpr int BM = 128;
     const dim3 grid((unsigned)((cols + BN - 1) / BN), (unsigned)((m + BM - 1) / BM));
     const int gs_shift = __builtin_ctz(gs);

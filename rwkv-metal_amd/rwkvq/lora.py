@@ -10,6 +10,9 @@
 
 y = base(x) + (alpha/rank) * (x @ A^T) @ B^T with A ~ N(0, 1)/sqrt(in_features)
 and B = 0 (lora.py:54-56).  Only lora_a / lora_b are trainable (lora.py:101-102).
+Over a QuantizedLinear base with bf16 activations the low-rank term is fused
+into the packed-weight GEMMs, forward and dX (rq_qmm_lora, _QLoRAFunction);
+other bases and dtypes compose the ops.
 The model layout is the reference's: model.blocks[i].tmix.{r,k,v,o}_proj and
 model.blocks[i].cmix.{key,value}.
 
@@ -37,6 +40,42 @@ CMIX_TARGETS = ("key", "value")
 
 def _promote(a: torch.dtype, b: torch.dtype) -> torch.dtype:
     return a if a == b else torch.float32
+
+
+class _QLoRAFunction(torch.autograd.Function):
+    """y = base(x) + scale * (x A^T) B^T over a QuantizedLinear base with the
+    low-rank term fused into the packed-weight GEMMs (rq_qmm_lora):
+    forward adds z B^T (z = x A^T) in the transpose=True GEMM's output stage;
+    backward computes u = dY B, dX = dY . W^ + scale * u A in the transpose=False
+    GEMM's output stage, dA = scale * u^T x, dB = scale * dY^T z.  The frozen
+    base gets no gradient."""
+
+    @staticmethod
+    def forward(ctx, x2, lora_a, lora_b, base, scale):
+        z = x2 @ lora_a.t()
+        y = ops.quantized_matmul_lora(x2, base.weight, base.scales, base.biases, z, lora_b, scale,
+                                      True, base.group_size, base.bits)
+        ctx.save_for_backward(x2, z, lora_a, lora_b)
+        ctx.base, ctx.scale = base, scale
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, z, lora_a, lora_b = ctx.saved_tensors
+        base, scale = ctx.base, ctx.scale
+        dy = dy.contiguous().to(x2.dtype)
+        u = dy @ lora_b
+        dx = da = db = None
+        if ctx.needs_input_grad[0]:
+            dx = ops.quantized_matmul_lora(dy, base.weight, base.scales, base.biases, u,
+                                           lora_a.t().contiguous(), scale, False, base.group_size,
+                                           base.bits).to(x2.dtype)
+        # bf16 GEMMs accumulate in fp32; the scale goes on the small results
+        if ctx.needs_input_grad[1]:
+            da = (u.t() @ x2).mul_(scale).to(lora_a.dtype)
+        if ctx.needs_input_grad[2]:
+            db = (dy.t() @ z).mul_(scale).to(lora_b.dtype)
+        return dx, da, db, None, None
 
 
 class LoRALinear(nn.Module):
@@ -71,7 +110,23 @@ class LoRALinear(nn.Module):
             (torch.randn(rank, in_features, device=device) * scale_a).to(dtype))
         self.lora_b = nn.Parameter(torch.zeros(out_features, rank, device=device, dtype=dtype))
 
+    def _fusable(self, x: Tensor) -> bool:
+        """The low-rank term can ride on the packed-weight GEMMs: quantized
+        base, bf16 activations and adapters, a supported rank, no active
+        dropout on z (its mask would have to be saved for the backward)."""
+        return (isinstance(self.linear, QuantizedLinear) and x.is_cuda
+                and x.dtype == self.lora_a.dtype == self.lora_b.dtype == torch.bfloat16
+                and self.rank in (16, 32, 48, 64)
+                and (self.dropout is None or not self.training))
+
     def forward(self, x: Tensor) -> Tensor:
+        if self._fusable(x):
+            lead = x.shape[:-1]
+            x2 = x.reshape(-1, x.shape[-1]).contiguous()
+            y = _QLoRAFunction.apply(x2, self.lora_a, self.lora_b, self.linear, self.scale)
+            if self.linear.bias is not None:
+                y = y + self.linear.bias
+            return y.reshape(*lead, y.shape[-1])
         base = self.linear(x)
         ct = _promote(x.dtype, self.lora_a.dtype)
         z = x.to(ct) @ self.lora_a.to(ct).t()

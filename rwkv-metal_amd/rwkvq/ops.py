@@ -6,6 +6,7 @@
                      group_size, bits)
     pack_codes(codes, bits) / unpack_codes(w_q, bits)     <- the MLX bitstream rule
     quantized_embedding(idx, w_q, scales, biases, ...)    <- nn.QuantizedEmbedding lookup
+    quantized_matmul_lora(x, w_q, s, b, z, lora, scale)   <- LoRALinear over a quantized base
 
 Reference call sites: rwkv_metal/lora/finetune.py:88-89 (nn.quantize),
 rwkv_metal/lora/lora.py:45-46 (QuantizedLinear.from_linear),
@@ -276,6 +277,56 @@ def quantized_matmul(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor,
         raise ValueError(f"x has inner dimension {x.shape[-1]} but the quantized weight expects "
                          f"{n_in} (transpose={transpose})")
     return _qmm_op(x, w_q, scales, biases, bool(transpose), group_size, bits)
+
+
+def _qmm_lora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, z: Tensor,
+                    lora: Tensor, scale: float, transpose: bool, group_size: int, bits: int):
+    """rq_qmm_lora on 2-D operands; None where the fused kernels do not apply."""
+    if not (x.dtype == z.dtype == lora.dtype == torch.bfloat16):
+        return None
+    x, w_q, scales = _ready(x), _ready(w_q), _ready(scales)
+    biases, z, lora = _ready(biases.to(scales.dtype)), _ready(z), _ready(lora)
+    R, K = w_q.shape[0], w_q.shape[1] * 32 // bits
+    m, rank = x.shape[0], z.shape[1]
+    y = torch.empty(m, R if transpose else K, dtype=_promote(x.dtype, scales.dtype),
+                    device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib().rq_qmm_lora(_ptr(x), DTYPE_CODE[x.dtype], _ptr(w_q), _ptr(scales), _ptr(biases),
+                               DTYPE_CODE[scales.dtype], m, R, K, group_size, bits,
+                               1 if transpose else 0, _ptr(z), _ptr(lora), rank, float(scale),
+                               _ptr(y), DTYPE_CODE[y.dtype], _stream(x))
+    if rc == RQ_EUNSUPPORTED:
+        return None
+    check(rc, "quantized_matmul_lora")
+    return y
+
+
+def quantized_matmul_lora(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, z: Tensor,
+                          lora: Tensor, scale: float, transpose: bool = True,
+                          group_size: int = 64, bits: int = 4) -> Tensor:
+    """quantized_matmul(x, ...) + scale * z @ lora^T: the QLoRA layer's low-rank
+    term (rwkv_metal/lora/lora.py:58-63; z = x @ lora_a^T, lora = lora_b; for
+    dX, z = dY @ lora_b and lora = lora_a^T) added in the GEMM's output stage
+    where the 64-wide-stage kernels run (rq_qmm_lora), computed separately
+    otherwise.  z [..., rank], lora [n_out, rank].  No autograd here:
+    rwkvq.lora.LoRALinear differentiates the layer."""
+    _check_args(group_size, bits)
+    w_q = _words(w_q)
+    K = _check_packed(w_q, scales, biases, group_size, bits)
+    n_in, n_out = (K, w_q.shape[0]) if transpose else (w_q.shape[0], K)
+    if x.shape[-1] != n_in or z.shape[:-1] != x.shape[:-1] or tuple(lora.shape) != (n_out, z.shape[-1]):
+        raise ValueError("quantized_matmul_lora: x, z and lora shapes do not agree")
+    _on_gpu(x, w_q, scales, biases, z, lora)
+    lead = x.shape[:-1]
+    x2, z2 = x.reshape(-1, n_in), z.reshape(-1, z.shape[-1])
+    y = None
+    if z2.shape[-1] in (16, 32, 48, 64) and x2.shape[0] > 0:
+        y = _qmm_lora_fused(x2, w_q, scales, biases, z2, lora, scale, transpose, group_size, bits)
+    if y is None:
+        y = quantized_matmul(x2, w_q, scales, biases, transpose, group_size, bits)
+        ct = _promote(y.dtype, z2.dtype)
+        y = (y.to(ct) + scale * (z2.to(ct) @ lora.to(ct).t())).to(y.dtype)
+    return y.reshape(*lead, n_out)
 
 
 class BoundQmm:

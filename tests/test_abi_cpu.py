@@ -28,7 +28,7 @@ def test_header_declares_the_expected_surface():
         "rq_abi_version", "rq_last_error", "rq_quantize", "rq_dequantize", "rq_qmm",
         "rq_pack", "rq_unpack", "rq_qmm_grouped", "rq_grouped_plan_table_bytes",
         "rq_grouped_plan_init", "rq_grouped_plan_run", "rq_embedding", "rq_sb6_dequantize",
-        "rq_sb6_to_affine"])
+        "rq_sb6_to_affine", "rq_qmm_lora"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -69,6 +69,10 @@ def test_invalid_arguments_return_einval(L):
     assert "gw_sb" in _err(L)
     assert L.rq_sb6_to_affine(p, p, p, 4, 64, 32, 1, 0, p, 0, p, None) == -1
     assert L.rq_sb6_to_affine(p + 1, p, p, 4, 64, 32, 1, 0, p, p, p, None) == -2
+    assert L.rq_qmm_lora(p, 0, p, p, p, 0, 300, 64, 64, 64, 4, 1, p, p, 8, 1.0, p, 0, None) == -1
+    assert "rank" in _err(L)
+    assert L.rq_qmm_lora(p, 0, p, p, p, 0, 300, 64, 64, 64, 4, 1, 0, p, 16, 1.0, p, 0, None) == -1
+    assert L.rq_qmm_lora(p, 0, p, p, p, 0, 300, 64, 64, 64, 4, 1, p + 8, p, 16, 1.0, p, 0, None) == -2
 
 
 def test_misaligned_pointers_return_ealign(L):

@@ -515,11 +515,14 @@ def test_autograd_dx_is_transposed_qmm(O, rq, dev):
     rel_check(x.grad, ref, what="dX")
 
 
-def test_qlora_layer_forward_backward(rq, dev):
+@pytest.mark.parametrize("M", [96, 320])
+def test_qlora_layer_forward_backward(rq, dev, M):
     """BASELINE config 4 math at a reduced shape: y = qmm(x,Wq) + (a/r)(xA^T)B^T;
-    grads of x, A, B against an fp32 dense reference on the dequantized base."""
+    grads of x, A, B against an fp32 dense reference on the dequantized base.
+    M=320 runs the fused low-rank term (forward and dX GEMMs), M=96 the
+    composed ops."""
     torch.manual_seed(0)
-    D, R, M, r, alpha = 512, 768, 96, 16, 16.0
+    D, R, r, alpha = 512, 768, 16, 16.0
     lin = torch.nn.Linear(D, R, bias=False).to(dev, torch.bfloat16)
     with torch.no_grad():
         lin.weight.copy_(weights(R, D, 7).to(dev))
@@ -528,10 +531,11 @@ def test_qlora_layer_forward_backward(rq, dev):
     with torch.no_grad():
         layer.lora_a.copy_((torch.randn(r, D, generator=g) / D ** 0.5).to(torch.bfloat16))
         layer.lora_b.copy_((torch.randn(R, r, generator=g) * 0.01).to(torch.bfloat16))
-    x = acts(M, D, 9).to(dev).requires_grad_(True)
-    say("qlora layer")
+    x = acts(M, D, 9).to(dev).reshape(M // 16, 16, D).requires_grad_(True)
+    say(f"qlora layer M={M}")
     y = layer(x)
-    dy = acts(M, R, 800).to(dev)
+    assert y.shape == (M // 16, 16, R)
+    dy = acts(M, R, 800).to(dev).reshape(M // 16, 16, R)
     y.backward(dy)
     wd = layer.linear.dequantized_weight().float()
     xr = x.detach().float().requires_grad_(True)
@@ -822,3 +826,33 @@ def test_add_lora_rwkvq_from_sidecar(O, rq, dev, tmp_path):
     rel_check(y, ref, what="lora over sb6")
     with pytest.raises(NotImplementedError):
         rq.load_sidecar(str(tmp_path / "model.rwkvq"))
+
+
+@pytest.mark.parametrize("transpose,rank", [(True, 16), (True, 32), (True, 64), (False, 16),
+                                            (False, 48)])
+def test_qmm_lora_fused_term(O, rq, dev, transpose, rank):
+    """rq_qmm_lora: the low-rank term scale * z L^T added in the 64-wide-stage
+    GEMMs' output stage, against the oracle product plus the term in float64
+    (partial tiles in both dims); a problem outside those kernels (M=64)
+    returns RQ_EUNSUPPORTED internally and the op composes the same result."""
+    from rwkvq import ops
+    gs, bits, R, K = 64, 4, 320, 1024
+    w = weights(R, K, 71 + rank)
+    wq, s, b = O.quantize(w, gs, bits)
+    n_in, n_out = (K, R) if transpose else (R, K)
+    g = torch.Generator().manual_seed(rank)
+    L = (torch.randn(n_out, rank, generator=g) * 0.05).to(torch.bfloat16)
+    for M in (300, 64):
+        x = acts(M, n_in, M + rank)
+        z = (torch.randn(M, rank, generator=g)).to(torch.bfloat16)
+        say(f"qmm_lora transpose={transpose} rank={rank} M={M}")
+        args = [t.to(dev) for t in (x, wq, s, b, z, L)]
+        fused = ops._qmm_lora_fused(*args, 2.0, transpose, gs, bits)
+        assert (fused is not None) == (M == 300)
+        y = rq.quantized_matmul_lora(*args, 2.0, transpose, gs, bits)
+        ref = O.quantized_matmul(x, wq, s, b, transpose, gs, bits, out_dtype=torch.float32,
+                                 weights="exact").double()
+        ref = ref + 2.0 * (z.double() @ L.double().t())
+        rel_check(y, ref, what=f"qmm_lora t{transpose} r{rank} M{M}")
+        if fused is not None:
+            rel_check(fused, ref, what="fused")
