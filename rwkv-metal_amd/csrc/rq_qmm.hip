@@ -774,6 +774,9 @@ constexpr int kWsBlock = 512;
 #ifndef RQ_K64_PPRIO
 #define RQ_K64_PPRIO 2  // qmm_t_k64: wave priority of the producer waves (0-3; 2 measured +4-6%)
 #endif
+#ifndef RQ_K64_BM128_BELOW
+#define RQ_K64_BM128_BELOW 200  // qmm_t_k64: 128-row tiles when 256-row ones number fewer
+#endif
 #ifndef RQ_K64_CPRIO
 #define RQ_K64_CPRIO 0  // qmm_t_k64: wave priority of the MFMA waves (0-3)
 #endif
@@ -1270,11 +1273,11 @@ RQ_DEV uint32_t pack2_dt(int dt, float lo, float hi) {
 // lane % 16) of 16x16 tile (a, b) holds the outputs of row a*16 + lr at
 // columns b*16 + 4*lg .. +3: four consecutive columns of one row.
 //  * fp32 outputs leave as one 16-byte store per tile and lane.
-//  * 16-bit outputs go through a wave-private LDS strip of 32 rows (stg,
-//    32 * (2*WN + 16) bytes) and leave as whole 16-byte chunks of the row
+//  * 16-bit outputs go through a wave-private LDS strip of 16*SA rows (stg,
+//    16*SA * (2*WN + 16) bytes) and leave as whole 16-byte chunks of the row
 //    segment (2*WN bytes per row), instead of 2-byte scattered stores.
 // Rows >= nrows and columns >= ld are not written.
-template <int TM, int TN>
+template <int TM, int TN, int SA = 2>
 RQ_DEV void store_wave_tile(const f32x4_t (&acc)[TM][TN], uint8_t* stg, void* __restrict__ y,
                             int y_dt, int64_t nrows, int64_t ld, int64_t r0, int64_t c0,
                             int lane) {
@@ -1300,16 +1303,17 @@ RQ_DEV void store_wave_tile(const f32x4_t (&acc)[TM][TN], uint8_t* stg, void* __
             }
         return;
     }
-    constexpr int RB = WN * 2;    // bytes per output row of the wave tile
-    constexpr int SR = RB + 16;   // staging row stride (16-byte aligned)
-    constexpr int CPR = RB / 16;  // 16-byte chunks per row
-    constexpr int NCH = 32 * CPR; // chunks per 32-row strip
+    static_assert(TM % SA == 0, "whole strips of SA 16-row tiles");
+    constexpr int RB = WN * 2;          // bytes per output row of the wave tile
+    constexpr int SR = RB + 16;         // staging row stride (16-byte aligned)
+    constexpr int CPR = RB / 16;        // 16-byte chunks per row
+    constexpr int NCH = 16 * SA * CPR;  // chunks per strip of 16*SA rows
     const bool vec = (((uintptr_t)y & 15) == 0) && (ld & 7) == 0;
     uint16_t* yo = (uint16_t*)y;
 #pragma unroll
-    for (int a2 = 0; a2 < TM; a2 += 2) {
+    for (int a2 = 0; a2 < TM; a2 += SA) {
 #pragma unroll
-        for (int aa = 0; aa < 2; ++aa)
+        for (int aa = 0; aa < SA; ++aa)
 #pragma unroll
             for (int b = 0; b < TN; ++b) {
                 const f32x4_t v = acc[a2 + aa][b];
@@ -1403,14 +1407,15 @@ RQ_DEV void lora_epilogue(f32x4_t (&acc)[TM][TN], const rq::LoraArgs& lo, int64_
 //    software-pipelined by hand (B fragments of the next k-step and A
 //    fragments two MFMA groups ahead), with scheduling barriers keeping the
 //    order: the compiler's own order waited on every fragment read.
-template <int BITS, int SDT, int BN, int GSH>
+template <int BITS, int SDT, int BN, int GSH, int BM>
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, void* __restrict__ y,
     int y_dt, int tiles_m, int tiles_n, rq::LoraArgs lora) {
-    constexpr int BM = 256;
+    static_assert(BM == 256 || BM == 128, "block rows");
     constexpr int WN = BN / 2;
-    constexpr int TM = 8, TN = WN / 16;
+    constexpr int TM = BM / 32, TN = WN / 16;   // 16x16 MFMA tiles per wave (2x2 waves)
+    constexpr int XL = BM / 32;                 // activation loads per producer lane per stage
     constexpr int BLD = 72;                  // bf16 ring row stride (64 + 8 elements)
     constexpr int D = RQ_K64_DEPTH;          // stages of loads in flight per producer thread
     constexpr int P = (8 << GSH) / 64;       // stages per 8-group (scale, bias) chunk: 4, 8, 16
@@ -1447,10 +1452,10 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
         const int pt = tid - 256, pw = wave - 4;
         typedef const __attribute__((address_space(1))) u32x4_t* gv_t;
         typedef const __attribute__((address_space(1))) uint32_t* gw_t;
-        uint32_t xoff[8], xdst[8];
+        uint32_t xoff[XL], xdst[XL];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int row = (pw * 8 + i) * 8 + (lane >> 3);
+        for (int i = 0; i < XL; ++i) {
+            const int row = (pw * XL + i) * 8 + (lane >> 3);
             const int chunk = lane & 7;
             int64_t grow = m0 + row;
             grow = grow < M ? grow : M - 1;
@@ -1476,13 +1481,13 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
         const uint16_t* srow_p = (const uint16_t*)scales + wrow * G;
         const uint16_t* brow_p = (const uint16_t*)biases + wrow * G;
 
-        u32x4_t xv[D][8];
+        u32x4_t xv[D][XL];
         uint32_t cv[D][NJ][JW];
         auto issue = [&](int st, int r) {
             const int sc = st < nst ? st : nst - 1;
             const uint8_t* xb = xbase + (int64_t)sc * 128;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xv[r][i] = *(gv_t)(xb + xoff[i]);
+            for (int i = 0; i < XL; ++i) xv[r][i] = *(gv_t)(xb + xoff[i]);
             const uint32_t* ws = wtile + (int64_t)sc * SW;
 #pragma unroll
             for (int i = 0; i < NJ; ++i) {
@@ -1543,7 +1548,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                     load_sb(per + 2);
                 }
 #pragma unroll
-                for (int i = 0; i < 8; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u % D][i];
+                for (int i = 0; i < XL; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u % D][i];
                 const float* sb = sbf[per & 1] + 2 * ((u * 64) >> GSH);
 #pragma unroll
                 for (int i = 0; i < NJ; ++i) {
@@ -1591,7 +1596,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int a = 0; a < TM; ++a) {
-            const int row = wm * 128 + a * 16 + lr;
+            const int row = wm * (BM / 2) + a * 16 + lr;
             aoff[h][a] = (uint32_t)(row * 128 + (((h * 4 + lg) ^ (row & 7)) * 16));
         }
     const uint32_t boff = (uint32_t)((wn * WN + lr) * BLD + lg * 8);
@@ -1648,9 +1653,12 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
 
     // after the last barrier the ring slot of stage nst - 2 (nst & 1) is read
     // by nobody and written by nobody: 8 KB of it per wave stage the output
-    if (lora.z) lora_epilogue<TM, TN>(acc, lora, M, R, m0 + wm * 128, n0 + wn * WN, lane);
-    store_wave_tile<TM, TN>(acc, ((nst & 1) ? xs1 : xs0) + wave * 8192, y, y_dt, M, R,
-                            m0 + wm * 128, n0 + wn * WN, lane);
+    if (lora.z) lora_epilogue<TM, TN>(acc, lora, M, R, m0 + wm * (BM / 2), n0 + wn * WN, lane);
+    // strips of 32 rows (BM 256: 8 KB of the free slot per wave) or 16 (BM 128: 4 KB)
+    constexpr int SA = BM == 256 ? 2 : 1;
+    static_assert(16 * SA * (BN + 16) <= BM * 32, "a wave's staging strip fits its share of a slot");
+    store_wave_tile<TM, TN, SA>(acc, ((nst & 1) ? xs1 : xs0) + wave * (BM * 32), y, y_dt, M, R,
+                                m0 + wm * (BM / 2), n0 + wn * WN, lane);
 }
 
 
@@ -1941,13 +1949,17 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
         // 160-row tiles (whole rounds over 256 CUs for the 2560-wide RWKV-7 shapes) split
         // evenly into 8-code dequant jobs only at 4 bits
         const int bn = (RQ_BITS == 4 && rows % 160 == 0) ? 160 : 128;
-        const int tm = (int)((m + 255) / 256);
         const int tn = (int)((rows + bn - 1) / bn);
+        // 128-row tiles when 256-row ones leave most CUs idle (small M, narrow R)
+        const int bm = ((m + 255) / 256) * tn < RQ_K64_BM128_BELOW ? 128 : 256;
+        const int tm = (int)((m + bm - 1) / bm);
         const int blocks = ((tm * tn + 7) / 8) * 8;
-#define RQ_K64(SD, BNV, GSHV)                                                                     \
-    hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, BNV, GSHV>), dim3(blocks), dim3(kWsBlock), 0,     \
+#define RQ_K64_BM(SD, BNV, GSHV, BMV)                                                             \
+    hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, BNV, GSHV, BMV>), dim3(blocks), dim3(kWsBlock), 0,\
                        stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols, y, y_dt, tm, tn,  \
                        lo)
+#define RQ_K64(SD, BNV, GSHV)                                                                     \
+    if (bm == 256) { RQ_K64_BM(SD, BNV, GSHV, 256); } else { RQ_K64_BM(SD, BNV, GSHV, 128); }
 #define RQ_K64_GS(SD, BNV)                                                                        \
     switch (gs_shift) {                                                                           \
         case 5: RQ_K64(SD, BNV, 5); break;                                                        \
@@ -1965,6 +1977,7 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
 #endif
 #undef RQ_K64_GS
 #undef RQ_K64
+#undef RQ_K64_BM
         return hipGetLastError();
     }
     if (lora) return hipErrorNotSupported;  // the low-rank term rides on the k64 kernels only

@@ -328,12 +328,14 @@ def _gpu_dense_ref(rq, x, wq, s, b, gs, bits, transpose):
     return x.float() @ (wd.t() if transpose else wd)
 
 
-@pytest.mark.parametrize("M", [512, 2048, 4096])
+@pytest.mark.parametrize("M", [512, 2000, 2048, 4000, 4096])
 @pytest.mark.parametrize("shape", [(2560, 2560), (10240, 2560), (2560, 10240)])
 def test_config3_prefill_full_size(rq, dev, shape, M):
     """2.9B prefill shapes at full size.  The oracle is too slow here, so the
     reference is an fp32 matmul of the dequantized weights (dequantize is
-    bit-exact to the oracle) -- a size-independent consistency check."""
+    bit-exact to the oracle) -- a size-independent consistency check.  The
+    2560-wide shapes at M <= 2048 run 128-row tiles, the rest 256-row ones;
+    M = 2000 / 4000 end in a partial tile of each."""
     R, K = shape
     say(f"config3 {shape} M={M}")
     w = weights(R, K, 3_000_000 + R).to(dev)
