@@ -516,49 +516,9 @@ __global__ __launch_bounds__(kBlock, 1) void qmm_t_big(
 }
 
 
-// ------------------------------------------------------------- qmm_t_dma
-//
-// Large-M forward GEMM for bf16 activations, fed entirely by direct-to-LDS
-// loads (global_load_lds): every stage of 32 contraction elements brings
-//   * the activation tile, 256 rows x 64 bytes, XOR-swizzled by 16-byte chunk
-//     so that MFMA fragment reads are bank-conflict free,
-//   * the packed codes of the BN weight rows (dword-dense [row][word]),
-//   * their scale and bias (one group per row per stage: 32 | group_size),
-// into an NSLOT-slot LDS ring (6 where LDS allows, else 4), NSLOT-1 stages
-// ahead of the MFMAs, without staging registers.  One stage behind the DMA, threads [0, BN) dequantize the stage
-// (fp32 fma, bf16 round) into a 2-slot bf16 ring; the 4 waves (2x2, wave
-// tile 128 x BN/2, 16x16x32 bf16 MFMAs) consume it.  One workgroup barrier
-// per stage, preceded by an explicit wait for this wave's DMAs two stages
-// back, orders the ring.  Every wave issues the same number of DMAs per
-// stage (out-of-range rows and stages past K load clamped addresses into
-// spare slots), so a single wait count is valid for all waves.
+// ------------------------------------------------- direct-to-LDS helpers
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-
-template <int BITS, int SDT, int BN, int NSLOT_>
-struct DmaCfg {
-    static constexpr int BM = 256;
-    static constexpr int NSLOT = NSLOT_;                              // DMA ring depth
-    static constexpr int AHEAD = NSLOT_ - 1;                          // stages in flight ahead
-    static_assert(NSLOT_ % 2 == 0, "the bf16 ring index is derived from the slot index");
-    static constexpr int X_BYTES = BM * 64;                           // 16 KB
-    static constexpr int NX = X_BYTES / (kBlock * 16);                // 4 x-DMAs per thread
-    static constexpr int CODE_DW = BN * BITS;                         // dwords of codes
-    static constexpr int NC = (CODE_DW + kBlock - 1) / kBlock;        // code DMAs per thread
-    static constexpr int C_BYTES = NC * kBlock * 4;
-    static constexpr int SB = SDT == RQ_F32 ? 4 : 2;                  // scale bytes
-    // DMA loads of 4 bytes or fewer land at a 4-byte stride per lane
-    static constexpr int S_BYTES = kBlock * 4;
-    static constexpr int PER_STAGE = NX + NC + 2;                     // DMAs per thread per stage
-    static constexpr int BLD = 40;                                    // bf16 ring row stride (elements)
-    static constexpr int B_BYTES = BN * BLD * 2;
-};
-
-template <int BITS, int SDT, int BN, int NSLOT>
-constexpr int dma_lds_bytes() {
-    typedef DmaCfg<BITS, SDT, BN, NSLOT> C;
-    return NSLOT * (C::X_BYTES + C::C_BYTES + 2 * C::S_BYTES) + 2 * C::B_BYTES;
-}
 
 template <int N>
 RQ_DEV void s_wait_vmcnt_lgkm0() {
@@ -567,200 +527,17 @@ RQ_DEV void s_wait_vmcnt_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
 }
 
-template <int BITS, int SDT, int BN, int NSLOT>
-__global__ __launch_bounds__(kBlock, 1) void qmm_t_dma(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
-    const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
-    void* __restrict__ y, int y_dt, int tiles_m, int tiles_n) {
-    typedef DmaCfg<BITS, SDT, BN, NSLOT> C;
-    constexpr int BM = C::BM;
-    constexpr int WN = BN / 2;
-    constexpr int TM = 8, TN = WN / 16;
-    // One LDS object per ring slot: the compiler's wait insertion can then
-    // tell a read of one slot from a DMA in flight to another (distinct
-    // objects do not alias) instead of draining every DMA before each read.
-    // (Slots past NSLOT are declared but never referenced: no LDS is used.)
-#define RQ_RING(name, bytes)                                                    \
-    __shared__ __attribute__((aligned(16))) uint8_t name##0[bytes];             \
-    __shared__ __attribute__((aligned(16))) uint8_t name##1[bytes];             \
-    __shared__ __attribute__((aligned(16))) uint8_t name##2[bytes];             \
-    __shared__ __attribute__((aligned(16))) uint8_t name##3[bytes];             \
-    __shared__ __attribute__((aligned(16))) uint8_t name##4[bytes];             \
-    __shared__ __attribute__((aligned(16))) uint8_t name##5[bytes];
-    RQ_RING(xr_, C::X_BYTES)
-    RQ_RING(cr_, C::C_BYTES)
-    RQ_RING(sr_, C::S_BYTES)
-    RQ_RING(br_, C::S_BYTES)
-#undef RQ_RING
-    __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * C::BLD];
-    __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * C::BLD];
-#define RQ_PICK(name) \
-    [&](int u) -> uint8_t* { return u == 0 ? name##0 : u == 1 ? name##1 : u == 2 ? name##2 : u == 3 ? name##3 : u == 4 ? name##4 : name##5; }
-    auto xr = RQ_PICK(xr_);
-    auto cr = RQ_PICK(cr_);
-    auto sr = RQ_PICK(sr_);
-    auto br = RQ_PICK(br_);
-#undef RQ_PICK
-    auto bq = [&](int u) -> uint16_t* { return u == 0 ? bq0 : bq1; };
-
-    const int ntiles = tiles_m * tiles_n;
-    const int per_xcd = (ntiles + 7) / 8;
-    const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-    if (t >= ntiles) return;
-    const int64_t m0 = (int64_t)(t / tiles_n) * BM, n0 = (int64_t)(t % tiles_n) * BN;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int lg = lane >> 4, lr = lane & 15;
-    const int64_t runs = K >> 5, wpr = runs * BITS, G = K >> gs_shift;
-    const int nst = (int)runs;
-
-    // Per-thread DMA sources that do not depend on the stage.
-    // x: instruction i of wave w covers tile rows (4w+i)*16 .. +15, 64 B each;
-    // lane l -> row (4w+i)*16 + l/4, stored chunk l%4 holds global chunk
-    // (l%4) ^ ((row/4)%4).
-    const uint16_t* xsrc[C::NX];
-#pragma unroll
-    for (int i = 0; i < C::NX; ++i) {
-        const int row = (wave * C::NX + i) * 16 + (lane >> 2);
-        const int chunk = (lane & 3) ^ ((row >> 2) & 3);
-        int64_t grow = m0 + row;
-        grow = grow < M ? grow : M - 1;
-        xsrc[i] = x + grow * K + chunk * 8;
-    }
-    const uint32_t* csrc[C::NC];
-#pragma unroll
-    for (int i = 0; i < C::NC; ++i) {
-        const int d = tid + kBlock * i;
-        int row = d / BITS;
-        const int word = d - row * BITS;
-        int64_t grow = n0 + (row < BN ? row : BN - 1);
-        grow = grow < R ? grow : R - 1;
-        csrc[i] = wq + grow * wpr + word;
-    }
-    int64_t srow = n0 + (tid < BN ? tid : BN - 1);
-    srow = srow < R ? srow : R - 1;
-    const uint8_t* ssrc = (const uint8_t*)scales + srow * G * C::SB;
-    const uint8_t* bsrc = (const uint8_t*)biases + srow * G * C::SB;
-
-    auto dma = [&](int st, int slot) {
-        const int stc = st < nst ? st : nst - 1;  // past the end: reload the last stage
-#pragma unroll
-        for (int i = 0; i < C::NX; ++i)
-            __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + (int64_t)stc * 32),
-                                             (lds_void_t*)(xr(slot) + (wave * C::NX + i) * 1024),
-                                             16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < C::NC; ++i)
-            __builtin_amdgcn_global_load_lds((const void*)(csrc[i] + (int64_t)stc * BITS),
-                                             (lds_void_t*)(cr(slot) + (i * kBlock + wave * 64) * 4),
-                                             4, 0, 0);
-        const int64_t g = ((int64_t)stc * 32) >> gs_shift;
-        __builtin_amdgcn_global_load_lds((const void*)(ssrc + g * C::SB),
-                                         (lds_void_t*)(sr(slot) + wave * 64 * 4), C::SB, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(bsrc + g * C::SB),
-                                         (lds_void_t*)(br(slot) + wave * 64 * 4), C::SB, 0, 0);
-    };
-
-    // Threads [0, BN) dequantize row tid of a stage into the bf16 ring.
-    auto dequant = [&](int slot, int bslot) {
-        if (tid < BN) {
-            uint32_t words[BITS];
-#pragma unroll
-            for (int w = 0; w < BITS; ++w) words[w] = *(const uint32_t*)(cr(slot) + (tid * BITS + w) * 4);
-            float s, b;
-            if constexpr (SDT == RQ_F32) {
-                s = *(const float*)(sr(slot) + tid * 4);
-                b = *(const float*)(br(slot) + tid * 4);
-            } else {
-                s = dt_traits<SDT>::to_f32(*(const uint16_t*)(sr(slot) + tid * 4));
-                b = dt_traits<SDT>::to_f32(*(const uint16_t*)(br(slot) + tid * 4));
-            }
-            uint32_t d[16];
-            dequant_run_fast<BITS>(words, s, b, d);
-            u32x4_t* dst = (u32x4_t*)(bq(bslot) + tid * C::BLD);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) dst[q] = u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
-        }
-    };
-
-    f32x4_t acc[TM][TN];
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    auto mfma = [&](int slot, int bslot) {
-        bf16x8_t af[TM], bf[TN];
-#pragma unroll
-        for (int a = 0; a < TM; ++a) {
-            const int row = wm * 128 + a * 16 + lr;
-            const int pos = lg ^ ((row >> 2) & 3);
-            af[a] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xr(slot) + row * 64 + pos * 16));
-        }
-#pragma unroll
-        for (int b = 0; b < TN; ++b)
-            bf[b] = __builtin_bit_cast(bf16x8_t,
-                                       *(const u32x4_t*)(bq(bslot) + (wn * WN + b * 16 + lr) * C::BLD + lg * 8));
-#pragma unroll
-        for (int a = 0; a < TM; ++a)
-#pragma unroll
-            for (int b = 0; b < TN; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bf[b], acc[a][b], 0, 0, 0);
-    };
-
-    // Prologue: stages 0..AHEAD-1 in flight; stage 0 dequantized into bf16 slot 0.
-#pragma unroll
-    for (int i = 0; i < C::AHEAD; ++i) dma(i, i);
-    s_wait_vmcnt_lgkm0<(C::AHEAD - 1) * C::PER_STAGE>();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    dequant(0, 0);
-
-    // Main loop, unrolled by the ring size so every slot index is static.
-    // Iteration st: wait for this wave's DMAs of stage st+1 (stages st+2 ..
-    // st+AHEAD-1 may still fly) and for its own LDS traffic; the barrier then
-    // makes stage st+1 (raw) and stage st (bf16) visible and guarantees that
-    // every wave is done with stage st-1, whose ring slot the DMA of stage
-    // st+AHEAD reuses.
-    for (int s = 0; s < nst; s += C::NSLOT) {
-#pragma unroll
-        for (int u = 0; u < C::NSLOT; ++u) {
-            const int st = s + u;
-            s_wait_vmcnt_lgkm0<(C::AHEAD - 2) * C::PER_STAGE>();
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            dma(st + C::AHEAD, (u + C::AHEAD) % C::NSLOT);
-            if (st < nst) {
-                dequant((u + 1) % C::NSLOT, (u + 1) & 1);  // NSLOT is even
-                mfma(u, u & 1);
-            }
-        }
-    }
-    s_wait_vmcnt_lgkm0<0>();
-
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b) {
-            const int64_t n = n0 + wn * WN + b * 16 + lr;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t m = m0 + wm * 128 + a * 16 + 4 * lg + i;
-                if (m < M && n < R) store_dt(y, y_dt, m * R + n, acc[a][b][i]);
-            }
-        }
-}
-
-
 // -------------------------------------------------------------- qmm_t_ws
 //
-// Warp-specialised form of the DMA-fed GEMM (bf16 activations, M >= 256):
-// 8 waves per block.  Waves 0-3 only run MFMAs (2x2, wave tile 128 x BN/2,
-// fp32 accumulators); waves 4-7 ("producers") issue every direct-to-LDS load
-// of the ring and dequantize one stage ahead.  Each SIMD holds one wave of
+// Warp-specialised GEMM fed by direct-to-LDS loads (global_load_lds; bf16
+// activations, M >= 256, the cases qmm_t_k64 does not take: fp32 scales,
+// K not a multiple of 8 groups, unaligned scales).  32-element stages of
+// 256 activation rows x 64 bytes (16-byte chunks XOR-swizzled) and the BN
+// rows' codes and (scale, bias) arrive in an LDS ring, ring-depth-1 stages
+// ahead, with no staging registers.  8 waves per block.  Waves 0-3 only run
+// MFMAs (2x2, wave tile 128 x BN/2, fp32 accumulators); waves 4-7
+// ("producers") issue every direct-to-LDS load of the ring and dequantize one
+// stage ahead.  Each SIMD holds one wave of
 // each kind, so the hardware interleaves the producers' VALU work with the
 // consumers' matrix instructions.  One workgroup barrier per stage of 32
 // contraction elements orders the rings:
@@ -782,12 +559,6 @@ constexpr int kWsBlock = 512;
 #endif
 #ifndef RQ_GEMM_K64
 #define RQ_GEMM_K64 1  // 1: 64-wide stages with whole-line loads (qmm_t_k64) where they apply
-#endif
-#ifndef RQ_GEMM_REG
-#define RQ_GEMM_REG 0  // 1: register-staged producers (qmm_t_wsr); 0: DMA ring (qmm_t_ws)
-#endif
-#ifndef RQ_GEMM_DEPTH
-#define RQ_GEMM_DEPTH 4  // stages of loads in flight per producer thread (even)
 #endif
 #ifndef RQ_WS_SLOTS
 #define RQ_WS_SLOTS 6  // DMA ring slots of qmm_t_ws (4 or 6): RQ_WS_SLOTS-1 stages in flight
@@ -1060,185 +831,6 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_ws(
                 for (int b = 0; b < TN; ++b)
                     bf[b] = __builtin_bit_cast(bf16x8_t,
                                                *(const u32x4_t*)(bq(u & 1) + boff + b * 16 * C::BLD));
-#pragma unroll
-                for (int a = 0; a < TM; ++a)
-#pragma unroll
-                    for (int b = 0; b < TN; ++b)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bf[b], acc[a][b],
-                                                                            0, 0, 0);
-            }
-        }
-    }
-
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b) {
-            const int64_t n = n0 + wn * WN + b * 16 + lr;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t m = m0 + wm * 128 + a * 16 + 4 * lg + i;
-                if (m < M && n < R) store_dt(y, y_dt, m * R + n, acc[a][b][i]);
-            }
-        }
-}
-
-
-// ------------------------------------------------------------- qmm_t_wsr
-//
-// Warp-specialised GEMM with register-staged producers (bf16 activations,
-// M >= 256).  8 waves per block: waves 0-3 run only MFMAs (2x2, wave tile
-// 128 x BN/2, fp32 accumulators); waves 4-7 ("producers") keep D stages of
-// 32 contraction elements in flight in their registers -- the block's 256
-// activation rows (4 x 16 B per thread), their weight row's codes and that
-// row's (scale, bias) -- and per stage write the activations to a 2-slot
-// LDS ring and dequantize the codes straight from registers into a 2-slot
-// bf16 ring.  Ordinary loads (not direct-to-LDS DMA) take the fast
-// register return path and let the compiler track their waits.  One
-// barrier per stage: producers write stage s, barrier s, consumers compute
-// stage s while producers prepare s+1.
-template <int BITS, int SDT, int BN, int D>
-__global__ __launch_bounds__(kWsBlock, 1) void qmm_t_wsr(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
-    const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
-    void* __restrict__ y, int y_dt, int tiles_m, int tiles_n) {
-    constexpr int BM = 256;
-    constexpr int WN = BN / 2;
-    constexpr int TM = 8, TN = WN / 16;
-    constexpr int BLD = 40;  // bf16 ring row stride (elements)
-    static_assert(D % 2 == 0, "the LDS rings are indexed by the unrolled stage parity");
-    static_assert(BN <= 256, "one producer thread dequantizes one weight row");
-    __shared__ __attribute__((aligned(16))) uint8_t xs0[BM * 64];
-    __shared__ __attribute__((aligned(16))) uint8_t xs1[BM * 64];
-    __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * BLD];
-    __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * BLD];
-
-    const int ntiles = tiles_m * tiles_n;
-    const int per_xcd = (ntiles + 7) / 8;
-    const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-    if (t >= ntiles) return;
-    const int64_t m0 = (int64_t)(t / tiles_n) * BM, n0 = (int64_t)(t % tiles_n) * BN;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t runs = K >> 5, wpr = runs * BITS, G = K >> gs_shift;
-    const int nst = (int)runs;
-
-    if (wave >= 4) {
-        // ---------------------------------------------------------- producers
-        const int pt = tid - 256, pw = wave - 4;
-        // activations: chunk i of this thread = row (pw*4+i)*16 + lane/4, 16-byte
-        // chunk (lane&3) ^ ((row>>2)&3) of the stage's 64 bytes; it lands at LDS
-        // byte (pw*4+i)*1024 + 16*lane (the consumers' swizzled fragment layout)
-        typedef const __attribute__((address_space(1))) u32x4_t* gx_t;
-        uint32_t xoff[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = (pw * 4 + i) * 16 + (lane >> 2);
-            const int chunk = (lane & 3) ^ ((row >> 2) & 3);
-            int64_t grow = m0 + row;
-            grow = grow < M ? grow : M - 1;
-            xoff[i] = (uint32_t)((grow - m0) * K * 2 + chunk * 16);
-        }
-        const uint8_t* xbase = (const uint8_t*)(x + m0 * K);
-        const bool has_row = pt < BN;
-        int64_t wrow = n0 + (has_row ? pt : 0);
-        wrow = wrow < R ? wrow : R - 1;
-        const uint32_t* wrow_p = wq + wrow * wpr;
-        const int64_t sb_row = wrow * G;
-
-        u32x4_t xv[D][4];
-        uint32_t cv[D][BITS];
-        uint32_t sv[D], bv[D];
-        auto issue = [&](int st, int r) {
-            const int sc = st < nst ? st : nst - 1;
-            const uint8_t* xb = xbase + (int64_t)sc * 64;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) xv[r][i] = *(gx_t)(xb + xoff[i]);
-            if (has_row) {
-                load_run<BITS>(wrow_p + (int64_t)sc * BITS, cv[r]);
-                const int64_t gi = sb_row + (((int64_t)sc * 32) >> gs_shift);
-                if constexpr (SDT == RQ_F32) {
-                    sv[r] = ((const uint32_t*)scales)[gi];
-                    bv[r] = ((const uint32_t*)biases)[gi];
-                } else {
-                    sv[r] = ((const uint16_t*)scales)[gi];
-                    bv[r] = ((const uint16_t*)biases)[gi];
-                }
-            }
-        };
-#pragma unroll
-        for (int r = 0; r < D; ++r) issue(r, r);
-
-        for (int s0 = 0; s0 < nst; s0 += D) {
-#pragma unroll
-            for (int u = 0; u < D; ++u) {
-                const int st = s0 + u;
-                uint8_t* xs = (u & 1) ? xs1 : xs0;
-                uint16_t* bq = (u & 1) ? bq1 : bq0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) *(u32x4_t*)(xs + (pw * 4 + i) * 1024 + 16 * lane) = xv[u][i];
-                if (has_row) {
-                    float sf, bf;
-                    if constexpr (SDT == RQ_F32) {
-                        sf = __uint_as_float(sv[u]);
-                        bf = __uint_as_float(bv[u]);
-                    } else {
-                        sf = dt_traits<SDT>::to_f32((uint16_t)sv[u]);
-                        bf = dt_traits<SDT>::to_f32((uint16_t)bv[u]);
-                    }
-                    uint32_t d[16];
-                    dequant_run_fast<BITS>(cv[u], sf, bf, d);
-                    u32x4_t* dst = (u32x4_t*)(bq + pt * BLD);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        dst[q] = u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
-                }
-                issue(st + D, u);
-                // this stage's LDS writes are complete before the barrier
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-                asm volatile("" ::: "memory");
-                __builtin_amdgcn_s_barrier();
-                asm volatile("" ::: "memory");
-            }
-        }
-        return;
-    }
-
-    // -------------------------------------------------------------- consumers
-    const int wm = wave >> 1, wn = wave & 1;
-    const int lg = lane >> 4, lr = lane & 15;
-    f32x4_t acc[TM][TN];
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    uint32_t aoff[TM];
-#pragma unroll
-    for (int a = 0; a < TM; ++a) {
-        const int row = wm * 128 + a * 16 + lr;
-        aoff[a] = (uint32_t)(row * 64 + ((lg ^ ((row >> 2) & 3)) * 16));
-    }
-    const uint32_t boff = (uint32_t)((wn * WN + lr) * BLD + lg * 8);
-
-    for (int s0 = 0; s0 < nst; s0 += D) {
-#pragma unroll
-        for (int u = 0; u < D; ++u) {
-            const int st = s0 + u;
-            // own LDS reads of the previous stage are done, then wait for stage st
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            if (st < nst) {
-                const uint8_t* xs = (u & 1) ? xs1 : xs0;
-                const uint16_t* bq = (u & 1) ? bq1 : bq0;
-                bf16x8_t af[TM], bf[TN];
-#pragma unroll
-                for (int a = 0; a < TM; ++a)
-                    af[a] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[a]));
-#pragma unroll
-                for (int b = 0; b < TN; ++b)
-                    bf[b] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(bq + boff + b * 16 * BLD));
 #pragma unroll
                 for (int a = 0; a < TM; ++a)
 #pragma unroll
@@ -1981,20 +1573,6 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
         return hipGetLastError();
     }
     if (lora) return hipErrorNotSupported;  // the low-rank term rides on the k64 kernels only
-    if (m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_REG) {
-        const int bn = rows % 160 == 0 ? 160 : 128;
-        const int tm = (int)((m + 255) / 256);
-        const int tn = (int)((rows + bn - 1) / bn);
-        const int blocks = ((tm * tn + 7) / 8) * 8;
-#define RQ_WSR(BNV)                                                                              \
-    RQ_DISPATCH_DT(sb_dt, SD,                                                                    \
-        hipLaunchKernelGGL((qmm_t_wsr<RQ_BITS, SD, BNV, RQ_GEMM_DEPTH>), dim3(blocks),           \
-                           dim3(kWsBlock), 0, stream, (const uint16_t*)x, wq, scales, biases, m,  \
-                           rows, cols, gs_shift, y, y_dt, tm, tn))
-        if (bn == 160) { RQ_WSR(160); } else { RQ_WSR(128); }
-#undef RQ_WSR
-        return hipGetLastError();
-    }
     if (m >= 256 && x_dt == RQ_BF16) {
         const int bn = rows % 160 == 0 ? 160 : 128;
         const int tm = (int)((m + 255) / 256);
