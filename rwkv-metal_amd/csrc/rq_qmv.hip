@@ -661,10 +661,10 @@ hipError_t launch_cfg(const QmvArgs& a, int sb_dt, int nmc, bool xlds, int block
 //    lane L's accumulator rows need only its own row's (scale, bias) and
 //    the activation sums X of its own group(s).  M > 4 runs ceil(M/4)
 //    passes over the same codes.
-//  * Every 4 stages a wave loads the (scale, bias) values of those stages
-//    for its 16 rows with one vector load per lane (lane groups 0/2 take
-//    scales, 1/3 biases), one iteration ahead, and parks them in its own LDS
-//    window (wave-private, no barrier).
+//  * Once per 64 groups a wave loads the (scale, bias) values of those
+//    groups for its 16 rows (lane groups 0/2 take scales, 1/3 biases), one
+//    window ahead, and parks them in its own LDS window (wave-private, no
+//    barrier).
 //  * Only x (pair-permuted bf16) and its sums X over 32-element (gs=32) or
 //    64-element slices -- a lane group's k-slice never spans two groups and
 //    at gs=128 covers half of one -- are staged per block, behind one
@@ -676,13 +676,27 @@ hipError_t launch_cfg(const QmvArgs& a, int sb_dt, int nmc, bool xlds, int block
 //    arguments.
 constexpr int kZeroElems = 64;  // zero line at the start of LDS: 128 B (8 A fragments)
 
+#ifndef RQ_QMV_WIN_G
+#define RQ_QMV_WIN_G 32
+#endif
+// (scale, bias) windows: a window is RQ_QMV_WIN_G groups of a row (64 B of
+// each array at 16-bit scales), loaded once for the IPW iterations that read
+// it.  Loaded in 32-B parts one iteration apart, a 128-B line was often
+// evicted from L2 in between and fetched again: an iteration takes about as
+// long as the streamed codes need to turn the L2 over.  64 groups (whole
+// lines) would remove the rest of the refetch at K >= 4096 but need 8 more
+// VGPRs per lane, one wave per SIMD less at 4 bits.
 template <int GSH>
 struct StreamWin {
     static constexpr int GPS = 256 >> GSH;             // groups per stage: 8, 4, 2
     static constexpr int GPI = 4 * GPS;                // groups per iteration: 32, 16, 8
-    static constexpr int WB = GPI * 2;                 // bytes per array per row per iteration
-    static constexpr int LB = WB / 2;                  // bytes one lane loads: 32, 16, 8
-    static constexpr int ROWB = GSH == 5 ? 144 : (GSH == 6 ? 80 : 48);  // LDS row stride
+    static constexpr int WG = RQ_QMV_WIN_G;            // groups per window
+    static constexpr int WW = WG * 2;                  // bytes per array per row per window
+    static constexpr int IPW = WG / GPI;               // iterations per window: 2, 4, 8
+    static constexpr int PB = GSH == 7 ? 8 : 16;       // load size: K % 512 == 0 keeps a row's
+                                                       // array a multiple of PB bytes
+    static constexpr int NP = WW / 2 / PB;             // loads per lane and window
+    static constexpr int ROWB = 2 * WW + 16;           // LDS row stride (spreads the banks)
     static constexpr int WAVE_BYTES = 16 * ROWB;
 };
 
@@ -753,8 +767,7 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
     typedef StreamWin<GSH> W;
     constexpr int NS = 4;  // stages per iteration; NS-1 stages of codes in flight
-    typedef typename std::conditional<W::LB == 32, Words<8>,
-            typename std::conditional<W::LB == 16, Words<4>, Words<2>>::type>::type win_t;
+    typedef Words<W::WW / 2 / 4> win_t;  // a lane's half of one array's window row
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lg = lane >> 4, lr = lane & 15;
@@ -768,25 +781,26 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
 
     // ---- first loads: window 0, then codes of stages 0..NS-2
     const gptr_u16 sbrow = (gptr_u16)((lg & 1) ? P.biases : P.scales) + rowc * G;
-    const int part = (lg >> 1) * (W::GPI / 2);
-    auto load_win = [&](int it) -> win_t {
-        int g0 = it * W::GPI + part;
-        g0 = g0 < G - W::GPI / 2 ? g0 : G - W::GPI / 2;  // past the last stage: any valid data
+    const int part = (lg >> 1) * (W::WG / 2);
+    constexpr int GP = W::PB / 2;  // groups per load
+    auto load_win = [&](int w) -> win_t {
         win_t v;
-        // The window after the last iteration is never read: load the staged
+        // The window after the last one is never read: load the staged
         // activations instead (L2-resident, 16-byte aligned, >= 1 KB), so the
         // load stays unconditional without fetching scale lines again.
-        const gptr_u16 src = it < niter ? sbrow + g0 : (gptr_u16)P.x;
-        if constexpr (W::LB == 32) {
-            const u32x4_t a = *(const RQ_GLOBAL u32x4_t*)src, b = *((const RQ_GLOBAL u32x4_t*)src + 1);
-            v.w[0] = a[0]; v.w[1] = a[1]; v.w[2] = a[2]; v.w[3] = a[3];
-            v.w[4] = b[0]; v.w[5] = b[1]; v.w[6] = b[2]; v.w[7] = b[3];
-        } else if constexpr (W::LB == 16) {
-            const u32x4_t a = *(const RQ_GLOBAL u32x4_t*)src;
-            v.w[0] = a[0]; v.w[1] = a[1]; v.w[2] = a[2]; v.w[3] = a[3];
-        } else {
-            const u32x2_t a = *(const RQ_GLOBAL u32x2_t*)src;
-            v.w[0] = a[0]; v.w[1] = a[1];
+        const bool live = w * W::WG < G;
+#pragma unroll
+        for (int q = 0; q < W::NP; ++q) {
+            int g = w * W::WG + part + q * GP;
+            g = g < G - GP ? g : G - GP;  // past the row's end (G < 64): any valid data
+            const gptr_u16 src = live ? sbrow + g : (gptr_u16)P.x;
+            if constexpr (W::PB == 16) {
+                const u32x4_t a = *(const RQ_GLOBAL u32x4_t*)src;
+                v.w[4 * q] = a[0]; v.w[4 * q + 1] = a[1]; v.w[4 * q + 2] = a[2]; v.w[4 * q + 3] = a[3];
+            } else {
+                const u32x2_t a = *(const RQ_GLOBAL u32x2_t*)src;
+                v.w[2 * q] = a[0]; v.w[2 * q + 1] = a[1];
+            }
         }
         return v;
     };
@@ -884,7 +898,7 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
             g_idx[c][i] = act ? xsum_f + (uint32_t)(m * GX + xlane) : 0u;
             g_step[c][i] = act ? (uint32_t)(256 >> XSH) : 0u;
         }
-    uint8_t* win_w = win + lr * W::ROWB + (lg & 1) * W::WB + (lg >> 1) * W::LB;
+    uint8_t* win_w = win + lr * W::ROWB + (lg & 1) * W::WW + (lg >> 1) * (W::WW / 2);
     const uint8_t* win_r = win + lr * W::ROWB + glane * 2;
 
     f32x4_t acc[NMC];
@@ -892,10 +906,13 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
     for (int c = 0; c < NMC; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     for (int it = 0; it < niter; ++it) {
-        // this iteration's (scale, bias) window into LDS, the next one into registers
-        *(win_t*)win_w = wv;  // read below by other lanes of this wave (LDS runs in order)
-        __builtin_amdgcn_wave_barrier();
-        wv = load_win(it + 1);
+        const int itw = it % W::IPW;
+        if (itw == 0) {
+            // this window of (scale, bias) values into LDS, the next one into registers
+            *(win_t*)win_w = wv;  // read below by other lanes of this wave (LDS runs in order)
+            __builtin_amdgcn_wave_barrier();
+            wv = load_win(it / W::IPW + 1);
+        }
 #pragma unroll
         for (int t = 0; t < NS; ++t) {
             const int st = it * NS + t;
@@ -905,8 +922,9 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
                 float sc[GL], cb[GL], cl[GL];
 #pragma unroll
                 for (int q = 0; q < GL; ++q) {
-                    const uint16_t sr = *(const uint16_t*)(win_r + (t * W::GPS + q) * 2);
-                    const uint16_t br = *(const uint16_t*)(win_r + W::WB + (t * W::GPS + q) * 2);
+                    const int gw = itw * W::GPI + t * W::GPS + q;  // group within the window
+                    const uint16_t sr = *(const uint16_t*)(win_r + gw * 2);
+                    const uint16_t br = *(const uint16_t*)(win_r + W::WW + gw * 2);
                     sc[q] = raw_to_f32<SDT>(sr);
                     const float bi = raw_to_f32<SDT>(br);
                     cb[q] = (BITS == 8) ? bi : fmaf(sc[q], -128.f, bi);
