@@ -358,8 +358,9 @@ int rq_grouped_plan_init(const rq_problem* problems, int n, rq_dtype x_dt, rq_dt
         if (!rq::qmv_stream_covers(problems[i], sb_dt, m, group_size, bits))
             return fail(RQ_EUNSUPPORTED,
                         "rq_grouped_plan_init: problem %d is outside the planned GEMV (needs "
-                        "m <= 4, 16-bit scales, cols %% 512 == 0, 16-byte aligned scales/biases, "
-                        "m*cols*2 bytes of activations within the LDS budget); use rq_qmm_grouped",
+                        "16-bit scales, cols %% 512 == 0, 16-byte aligned scales/biases, and "
+                        "either m <= 4 with m*cols*2 bytes of activations within the LDS budget "
+                        "or 4 < m <= 16 with 4- or 8-bit codes); use rq_qmm_grouped",
                         i);
         if ((problems[i].rows + rq::kQmvRowsPerBlock - 1) / rq::kQmvRowsPerBlock > 65536)
             return fail(RQ_EUNSUPPORTED, "rq_grouped_plan_init: problem %d has too many rows", i);

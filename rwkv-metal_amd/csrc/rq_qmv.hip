@@ -83,8 +83,8 @@ constexpr int kBlock = 64 * kWaves;
 #ifndef RQ_QMV_BIG_RB
 #define RQ_QMV_BIG_RB 1  // 16-row blocks per wave for big launches
 #endif
-#ifndef RQ_QMV_STREAM_MMAX
-#define RQ_QMV_STREAM_MMAX 4  // largest m the streamed-scale GEMV takes
+#ifndef RQ_QMV_WIDE
+#define RQ_QMV_WIDE 1  // 0: never use the wide GEMV (4 < m <= 16)
 #endif
 #ifndef RQ_QMV_STREAM
 #define RQ_QMV_STREAM 1  // 0: never use the streamed-scale GEMV
@@ -659,8 +659,9 @@ hipError_t launch_cfg(const QmvArgs& a, int sb_dt, int nmc, bool xlds, int block
 //    slice only): D row 4g+i sums exactly lane group g's codes, i.e. one
 //    group (two at gs=32: the stage's two MFMA halves are kept apart), and
 //    lane L's accumulator rows need only its own row's (scale, bias) and
-//    the activation sums X of its own group(s).  M > 4 runs ceil(M/4)
-//    passes over the same codes.
+//    the activation sums X of its own group(s).  This kernel takes m <= 4;
+//    larger m runs the wide kernel below, whose MFMA rows are all
+//    activation rows.
 //  * Once per 64 groups a wave loads the (scale, bias) values of those
 //    groups for its 16 rows (lane groups 0/2 take scales, 1/3 biases), one
 //    window ahead, and parks them in its own LDS window (wave-private, no
@@ -675,6 +676,7 @@ hipError_t launch_cfg(const QmvArgs& a, int sb_dt, int nmc, bool xlds, int block
 //    host.  qmv_stream_inline takes up to RQ_MAX_GROUPED problems in its
 //    arguments.
 constexpr int kZeroElems = 64;  // zero line at the start of LDS: 128 B (8 A fragments)
+constexpr int kStreamSlotsMax = 4;  // largest m of the slotted streamed kernel; above: the wide one
 
 #ifndef RQ_QMV_WIN_G
 #define RQ_QMV_WIN_G 32
@@ -761,6 +763,66 @@ RQ_DEV void load_two_runs(gptr_u32 p, uint32_t* out) {
     }
 }
 
+// One (scale, bias) window load of a lane: NP loads of PB bytes of the row
+// array `sbrow` (scales for lane groups 0/2, biases for 1/3) starting at
+// group w*WG + part.  The window after the last one is never read: it loads
+// `spare` instead (the activations: L2-resident, 16-byte aligned, >= 1 KB),
+// so the load stays unconditional without fetching scale lines again.
+template <int GSH>
+RQ_DEV Words<StreamWin<GSH>::WW / 8> load_sb_window(gptr_u16 sbrow, int part, int G, int w,
+                                                     const void* spare) {
+    typedef StreamWin<GSH> W;
+    constexpr int GP = W::PB / 2;  // groups per load
+    Words<W::WW / 8> v;
+    const bool live = w * W::WG < G;
+#pragma unroll
+    for (int q = 0; q < W::NP; ++q) {
+        int g = w * W::WG + part + q * GP;
+        g = g < G - GP ? g : G - GP;  // past the row's end (G < 64): any valid data
+        const gptr_u16 src = live ? sbrow + g : (gptr_u16)spare;
+        if constexpr (W::PB == 16) {
+            const u32x4_t a = *(const RQ_GLOBAL u32x4_t*)src;
+            v.w[4 * q] = a[0]; v.w[4 * q + 1] = a[1]; v.w[4 * q + 2] = a[2]; v.w[4 * q + 3] = a[3];
+        } else {
+            const u32x2_t a = *(const RQ_GLOBAL u32x2_t*)src;
+            v.w[2 * q] = a[0]; v.w[2 * q + 1] = a[1];
+        }
+    }
+    return v;
+}
+
+// Eight consecutive activations as loaded (16 B of bf16/f16, 32 B of f32) and
+// their conversion to four bf16-pair dwords in natural order.
+struct XRaw {
+    u32x4_t lo, hi;
+};
+RQ_DEV XRaw load_x8(const void* x, int x_dt, int64_t e) {  // e: index of the 8-element piece
+    XRaw r;
+    if (x_dt == RQ_F32) {
+        const RQ_GLOBAL u32x4_t* p = (const RQ_GLOBAL u32x4_t*)x + 2 * e;
+        r.lo = p[0];
+        r.hi = p[1];
+    } else {
+        r.lo = ((const RQ_GLOBAL u32x4_t*)x)[e];
+        r.hi = r.lo;
+    }
+    return r;
+}
+RQ_DEV void x8_to_bf16(const XRaw& r, int x_dt, uint32_t* d) {
+    if (x_dt == RQ_BF16) {
+        d[0] = r.lo[0]; d[1] = r.lo[1]; d[2] = r.lo[2]; d[3] = r.lo[3];
+    } else if (x_dt == RQ_F32) {
+        d[0] = pack_bf16x2(__uint_as_float(r.lo[0]), __uint_as_float(r.lo[1]));
+        d[1] = pack_bf16x2(__uint_as_float(r.lo[2]), __uint_as_float(r.lo[3]));
+        d[2] = pack_bf16x2(__uint_as_float(r.hi[0]), __uint_as_float(r.hi[1]));
+        d[3] = pack_bf16x2(__uint_as_float(r.hi[2]), __uint_as_float(r.hi[3]));
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            d[q] = pack_bf16x2(f16_bits_to_f32(r.lo[q] & 0xffffu), f16_bits_to_f32(r.lo[q] >> 16));
+    }
+}
+
 template <int BITS, int SDT, int NMC, int MI, int GSH>
 RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, int y_dt) {
     static_assert(SDT != RQ_F32, "streamed scales are 16-bit");
@@ -782,28 +844,7 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
     // ---- first loads: window 0, then codes of stages 0..NS-2
     const gptr_u16 sbrow = (gptr_u16)((lg & 1) ? P.biases : P.scales) + rowc * G;
     const int part = (lg >> 1) * (W::WG / 2);
-    constexpr int GP = W::PB / 2;  // groups per load
-    auto load_win = [&](int w) -> win_t {
-        win_t v;
-        // The window after the last one is never read: load the staged
-        // activations instead (L2-resident, 16-byte aligned, >= 1 KB), so the
-        // load stays unconditional without fetching scale lines again.
-        const bool live = w * W::WG < G;
-#pragma unroll
-        for (int q = 0; q < W::NP; ++q) {
-            int g = w * W::WG + part + q * GP;
-            g = g < G - GP ? g : G - GP;  // past the row's end (G < 64): any valid data
-            const gptr_u16 src = live ? sbrow + g : (gptr_u16)P.x;
-            if constexpr (W::PB == 16) {
-                const u32x4_t a = *(const RQ_GLOBAL u32x4_t*)src;
-                v.w[4 * q] = a[0]; v.w[4 * q + 1] = a[1]; v.w[4 * q + 2] = a[2]; v.w[4 * q + 3] = a[3];
-            } else {
-                const u32x2_t a = *(const RQ_GLOBAL u32x2_t*)src;
-                v.w[2 * q] = a[0]; v.w[2 * q + 1] = a[1];
-            }
-        }
-        return v;
-    };
+    auto load_win = [&](int w) -> win_t { return load_sb_window<GSH>(sbrow, part, G, w, P.x); };
     const gptr_u32 wqr = (gptr_u32)P.w_q + rowc * wpr + lg * 2 * BITS;
     auto load_codes = [&](int st, uint32_t* words) {
         const int sc = st < nst ? st : nst - 1;
@@ -833,21 +874,7 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
         const int64_t n8 = (int64_t)M * K / 8;
         for (int64_t e = threadIdx.x; e < n8; e += kBlock) {
             uint32_t d[4];
-            if (x_dt == RQ_BF16) {
-                const u32x4_t v = ((const RQ_GLOBAL u32x4_t*)x)[e];
-                d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
-            } else if (x_dt == RQ_F32) {
-                const RQ_GLOBAL f32x4_t* xf = (const RQ_GLOBAL f32x4_t*)x + 2 * e;
-                const f32x4_t lo = xf[0], hi = xf[1];
-                d[0] = pack_bf16x2(lo[0], lo[1]); d[1] = pack_bf16x2(lo[2], lo[3]);
-                d[2] = pack_bf16x2(hi[0], hi[1]); d[3] = pack_bf16x2(hi[2], hi[3]);
-            } else {
-                const u32x4_t v = ((const RQ_GLOBAL u32x4_t*)x)[e];
-                const uint32_t h[4] = {v[0], v[1], v[2], v[3]};
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    d[q] = pack_bf16x2(f16_bits_to_f32(h[q] & 0xffffu), f16_bits_to_f32(h[q] >> 16));
-            }
+            x8_to_bf16(load_x8(x, x_dt, e), x_dt, d);
             uint32_t pr[4];
             reorder_pairs(d, pr);
             *(u32x4_t*)&xs[e * 8] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
@@ -1020,6 +1047,262 @@ __global__ __launch_bounds__(kBlock) RQ_STREAM_OCC void qmv_stream_table(const r
     qmv_stream_body<BITS, SDT, NMC, MI, GSH>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
 }
 
+// ------------------------------------------------------------ wide GEMV
+//
+// qmv_wide_*: the decode GEMV for 4 < m <= 16 on the streamed layout (same
+// stages, lane loads, (scale, bias) windows and launch forms as
+// qmv_stream_*), with every A row of the MFMA an activation row:
+//
+//  * After its loads arrive, the 4 x 4 block (lane group g, 8-code piece j)
+//    of each run half of a stage is transposed across lane groups with
+//    v_permlane32_swap and v_permlane16_swap (4 swaps per 4 words): lane
+//    group g then holds piece g of run 2t+h of every lane group t, so MFMA
+//    (t, h) contracts exactly run 2t+h -- 32 codes of ONE group -- for 16
+//    activation rows m and 16 weight rows n.  No slots: one pass for any
+//    m <= 16 (the slotted kernel needs ceil(m/4)).
+//  * The activation sums over the same 32 codes come from a second MFMA of
+//    the same A fragment with a constant B (bf16 1.0), so only the
+//    pair-permuted bf16 x is staged: per group, acc += s D + (b - 128 s) X
+//    (8-bit: b X), the lane reading its row's GPS (scale, bias) values of the
+//    stage from the wave's window.
+//  * x is staged in chunks of one iteration (4 stages, 1024 columns) into a
+//    two-slot LDS ring: the next chunk's loads are issued at the start of an
+//    iteration and written after its MFMAs, behind one barrier per
+//    iteration, so LDS does not grow with K.  Rows m >= M of the ring are
+//    zero.
+//  * Lane L's accumulator holds D rows m = 4(L/16) + i of weight row L%16.
+// 4- and 8-bit codes: their pieces are whole words.
+constexpr int kWideNS = 4;                // stages per iteration = per staged x chunk
+constexpr int kWideKC = 256 * kWideNS;    // x columns per chunk
+constexpr int kWideRow = kWideKC + 8;     // LDS row stride in elements (+16 B spreads the banks)
+
+// 4 x 4 transpose of (lane group, register): afterwards register j of lane
+// group g holds what register g of lane group j held.
+RQ_DEV void transpose_lane_groups(uint32_t& a, uint32_t& b, uint32_t& c, uint32_t& d) {
+    const auto r0 = __builtin_amdgcn_permlane32_swap(a, c, false, false);  // rows 2,3 of a <-> rows 0,1 of c
+    const auto r1 = __builtin_amdgcn_permlane32_swap(b, d, false, false);
+    const auto r2 = __builtin_amdgcn_permlane16_swap(r0[0], r1[0], false, false);  // odd rows of a <-> even rows of b
+    const auto r3 = __builtin_amdgcn_permlane16_swap(r0[1], r1[1], false, false);
+    a = r2[0]; b = r2[1]; c = r3[0]; d = r3[1];
+}
+
+template <int MP, int GSH>
+struct WideLds {
+    static constexpr int X_ELEMS = 2 * MP * kWideRow;                 // x ring
+    static constexpr int BYTES = 2 * X_ELEMS + kWaves * StreamWin<GSH>::WAVE_BYTES;
+};
+
+template <int BITS, int SDT, int MP, int GSH>
+RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int y_dt) {
+    static_assert(BITS == 4 || BITS == 8, "wide GEMV: codes whose 8-code pieces are whole words");
+    static_assert(SDT != RQ_F32, "streamed scales are 16-bit");
+    typedef StreamWin<GSH> W;
+    typedef WideLds<MP, GSH> L;
+    __shared__ __attribute__((aligned(16))) uint16_t xring[L::X_ELEMS];
+    __shared__ __attribute__((aligned(16))) uint8_t wins[kWaves * W::WAVE_BYTES];
+    constexpr int NS = kWideNS;
+    constexpr int PW = BITS / 4;                                       // words per 8-code piece
+    constexpr int GPS = W::GPS;                                        // groups per stage
+    constexpr int XQ = (MP * (kWideKC / 8) + kBlock - 1) / kBlock;     // x pieces per thread per chunk
+    typedef Words<W::WW / 8> win_t;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lg = lane >> 4, lr = lane & 15;
+    const int64_t R = P.rows, K = P.cols;
+    const int G = (int)(K >> GSH);
+    const int nst = (int)(K >> 8);
+    const int niter = (nst + NS - 1) / NS;
+    const int64_t row0 = (int64_t)lblock * 64 + wave * 16;
+    const int64_t rowc = (row0 + lr) < R ? (row0 + lr) : R - 1;
+    const int64_t wpr = (K >> 5) * BITS;
+
+    // ---- first loads: window 0, then codes of stages 0..NS-2
+    const gptr_u16 sbrow = (gptr_u16)((lg & 1) ? P.biases : P.scales) + rowc * G;
+    const int part = (lg >> 1) * (W::WG / 2);
+    win_t wv = load_sb_window<GSH>(sbrow, part, G, 0, P.x);
+    const gptr_u32 wqr = (gptr_u32)P.w_q + rowc * wpr + lg * 2 * BITS;
+    auto load_codes = [&](int st, uint32_t* words) {
+        const int sc = st < nst ? st : nst - 1;
+        load_two_runs<BITS>(wqr + sc * (8 * BITS), words);
+    };
+    uint32_t cw[NS][2 * BITS];
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i) {
+        load_codes(i, cw[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- x chunks: piece e of a chunk is row e / 128, columns 8 (e % 128) ..
+    const int npc = M * (kWideKC / 8);
+    const int64_t k8 = K >> 3;
+    auto load_chunk = [&](int c, XRaw* xr) {
+#pragma unroll
+        for (int q = 0; q < XQ; ++q) {
+            const int e = threadIdx.x + q * kBlock;
+            const int64_t col8 = (int64_t)c * (kWideKC / 8) + (e & 127);
+            const bool ok = e < npc && col8 < k8;
+            xr[q] = load_x8(P.x, x_dt, ok ? (int64_t)(e >> 7) * k8 + col8 : 0);
+        }
+    };
+    auto store_chunk = [&](int slot, const XRaw* xr) {
+#pragma unroll
+        for (int q = 0; q < XQ; ++q) {
+            const int e = threadIdx.x + q * kBlock;
+            if (e < npc) {
+                uint32_t d[4], pr[4];
+                x8_to_bf16(xr[q], x_dt, d);
+                reorder_pairs(d, pr);
+                *(u32x4_t*)&xring[slot * MP * kWideRow + (e >> 7) * kWideRow + (e & 127) * 8] =
+                    u32x4_t{pr[0], pr[1], pr[2], pr[3]};
+            }
+        }
+    };
+    XRaw xr[XQ];
+    load_chunk(0, xr);
+    // rows M..MP-1 of both slots stay zero (A rows without an activation row)
+    for (int e = threadIdx.x; e < 2 * (MP - M) * (kWideRow / 8); e += kBlock) {
+        const int slot = e / ((MP - M) * (kWideRow / 8)), r = e % ((MP - M) * (kWideRow / 8));
+        *(u32x4_t*)&xring[slot * MP * kWideRow + M * kWideRow + r * 8] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+    store_chunk(0, xr);
+    __syncthreads();
+
+    // ---- per-lane constants
+    const PairConsts kc = pair_consts();
+    constexpr uint32_t kOne = 0x3F803F80u;  // bf16 1.0 pairs
+    const bf16x8_t ones = as_bf16x8(kOne, kOne, kOne, kOne);
+    const uint32_t a_off = (uint32_t)(lr * kWideRow + lg * 8);
+    uint8_t* win = wins + wave * W::WAVE_BYTES;
+    uint8_t* win_w = win + lr * W::ROWB + (lg & 1) * W::WW + (lg >> 1) * (W::WW / 2);
+    const uint8_t* win_r = win + lr * W::ROWB;
+
+    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < niter; ++it) {
+        const int itw = it % W::IPW;
+        if (itw == 0) {
+            // this window of (scale, bias) values into LDS, the next one into registers
+            *(win_t*)win_w = wv;  // read below by other lanes of this wave (LDS runs in order)
+            __builtin_amdgcn_wave_barrier();
+            wv = load_sb_window<GSH>(sbrow, part, G, it / W::IPW + 1, P.x);
+        }
+        const bool more = it + 1 < niter;
+        if (more) load_chunk(it + 1, xr);
+        const uint16_t* xs = xring + (it & 1) * MP * kWideRow + a_off;
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            const int st = it * NS + t;
+            load_codes(st + NS - 1, cw[(t + NS - 1) % NS]);
+            if (st < nst) {
+                // (scale, bias) of the stage's GPS groups for row lr
+                float sc[GPS], cb[GPS];
+                {
+                    const int gw = itw * W::GPI + t * W::GPS;  // first group of the stage in the window
+                    uint32_t sr[(GPS + 1) / 2], br[(GPS + 1) / 2];
+                    if constexpr (GPS == 8) {
+                        const u32x4_t a = *(const u32x4_t*)(win_r + gw * 2);
+                        const u32x4_t b = *(const u32x4_t*)(win_r + W::WW + gw * 2);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) { sr[q] = a[q]; br[q] = b[q]; }
+                    } else if constexpr (GPS == 4) {
+                        const u32x2_t a = *(const u32x2_t*)(win_r + gw * 2);
+                        const u32x2_t b = *(const u32x2_t*)(win_r + W::WW + gw * 2);
+                        sr[0] = a[0]; sr[1] = a[1]; br[0] = b[0]; br[1] = b[1];
+                    } else {
+                        sr[0] = *(const uint32_t*)(win_r + gw * 2);
+                        br[0] = *(const uint32_t*)(win_r + W::WW + gw * 2);
+                    }
+#pragma unroll
+                    for (int q = 0; q < GPS; ++q) {
+                        const uint32_t sb = (q & 1) ? sr[q >> 1] >> 16 : sr[q >> 1] & 0xffffu;
+                        const uint32_t bb = (q & 1) ? br[q >> 1] >> 16 : br[q >> 1] & 0xffffu;
+                        sc[q] = raw_to_f32<SDT>(sb);
+                        const float bi = raw_to_f32<SDT>(bb);
+                        cb[q] = (BITS == 8) ? bi : fmaf(sc[q], -128.f, bi);
+                    }
+                }
+                uint32_t* w = cw[t];
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int p = 0; p < PW; ++p)
+                        transpose_lane_groups(w[h * BITS + p], w[h * BITS + PW + p],
+                                              w[h * BITS + 2 * PW + p], w[h * BITS + 3 * PW + p]);
+                f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f}, xsum = d;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {  // run u = 2 t2 + h of the stage
+                    const int t2 = u >> 1, h = u & 1;
+                    uint32_t pr[4];
+                    codes_to_bf16_pairs<BITS>(w + h * BITS, t2, pr, kc);
+                    const u32x4_t av = *(const u32x4_t*)&xs[t * 256 + 32 * u];
+                    const bf16x8_t a = as_bf16x8(av[0], av[1], av[2], av[3]);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        a, as_bf16x8(pr[0], pr[1], pr[2], pr[3]), d, 0, 0, 0);
+                    xsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xsum, 0, 0, 0);
+                    const int gi = (32 * u) >> GSH;
+                    if (u == 7 || ((32 * (u + 1)) >> GSH) != gi) {  // the group ends with this run
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            acc[i] = fmaf(sc[gi], d[i], fmaf(cb[gi], xsum[i], acc[i]));
+                        d = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                        xsum = d;
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (more) store_chunk((it + 1) & 1, xr);  // that slot was last read before the previous barrier
+        __syncthreads();
+    }
+
+    const int64_t row = row0 + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * lg + i;
+        if (m < M && row < R) store_dt(P.y, y_dt, (int64_t)m * R + row, acc[i]);
+    }
+}
+
+template <int BITS, int SDT, int MP, int GSH>
+__global__ __launch_bounds__(kBlock) void qmv_wide_inline(const QmvArgs args) {
+    const int bid = blockIdx.x;
+    int lo = 0, hi = args.n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (args.block_start[mid] <= bid) lo = mid; else hi = mid - 1;
+    }
+    qmv_wide_body<BITS, SDT, MP, GSH>(args.p[lo], bid - args.block_start[lo], args.m, args.x_dt,
+                                      args.y_dt);
+}
+
+template <int BITS, int SDT, int MP, int GSH>
+__global__ __launch_bounds__(kBlock) void qmv_wide_table(const rq::QmvTable a) {
+    const uint32_t e = a.blocks[blockIdx.x];
+    const rq_problem P = a.descs[e >> 16];
+    qmv_wide_body<BITS, SDT, MP, GSH>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
+}
+
+// F is called with integral_constant-typed (SDT, MP, GSH).
+template <typename F>
+hipError_t wide_dispatch(int sb_dt, int64_t m, int gs, F&& f) {
+    const int gsh = __builtin_ctz(gs);
+    typedef std::integral_constant<int, RQ_BF16> BF;
+    typedef std::integral_constant<int, RQ_F16> FH;
+#define RQ_W_GSH(SD, MPV)                                                                      \
+    switch (gsh) {                                                                             \
+        case 5: return f(SD(), std::integral_constant<int, MPV>(), std::integral_constant<int, 5>()); \
+        case 6: return f(SD(), std::integral_constant<int, MPV>(), std::integral_constant<int, 6>()); \
+        case 7: return f(SD(), std::integral_constant<int, MPV>(), std::integral_constant<int, 7>()); \
+        default: return hipErrorInvalidValue;                                                  \
+    }
+#define RQ_W_MP(SD)                      \
+    if (m <= 8) { RQ_W_GSH(SD, 8) }      \
+    RQ_W_GSH(SD, 16)
+    if (sb_dt == RQ_BF16) { RQ_W_MP(BF) }
+    RQ_W_MP(FH)
+#undef RQ_W_MP
+#undef RQ_W_GSH
+}
+
 // Template dispatch shared by both launch forms: F is called with
 // integral_constant-typed (SDT, NMC, MI, GSH).
 template <typename F>
@@ -1045,8 +1328,6 @@ hipError_t stream_dispatch(int sb_dt, int64_t m, int gs, F&& f) {
         case 9: RQ_S_GSH(SD, 1, 1)                   \
         case 10: RQ_S_GSH(SD, 1, 2)                  \
         case 12: RQ_S_GSH(SD, 1, 4)                  \
-        case 20: RQ_S_GSH(SD, 2, 4)                  \
-        case 36: RQ_S_GSH(SD, 4, 4)                  \
         default: return hipErrorInvalidValue;        \
     }
     if (sb_dt == RQ_BF16) { RQ_S_NMI(BF) }
@@ -1057,6 +1338,17 @@ hipError_t stream_dispatch(int sb_dt, int64_t m, int gs, F&& f) {
 
 hipError_t launch_stream_inline(const QmvArgs& a, int blocks, int sb_dt, int gs, size_t lds,
                                 hipStream_t stream) {
+    if (a.m > kStreamSlotsMax) {
+        if constexpr (RQ_BITS == 4 || RQ_BITS == 8) {
+            return wide_dispatch(sb_dt, a.m, gs, [&](auto sd, auto mp, auto gsh) {
+                hipLaunchKernelGGL((qmv_wide_inline<RQ_BITS, decltype(sd)::value, decltype(mp)::value,
+                                                    decltype(gsh)::value>),
+                                   dim3(blocks), dim3(kBlock), 0, stream, a);
+                return hipGetLastError();
+            });
+        }
+        return hipErrorInvalidValue;
+    }
     return stream_dispatch(sb_dt, a.m, gs, [&](auto sd, auto nmc, auto mi, auto gsh) {
         hipLaunchKernelGGL((qmv_stream_inline<RQ_BITS, decltype(sd)::value, decltype(nmc)::value,
                                               decltype(mi)::value, decltype(gsh)::value>),
@@ -1067,6 +1359,17 @@ hipError_t launch_stream_inline(const QmvArgs& a, int blocks, int sb_dt, int gs,
 
 hipError_t launch_stream_table(const rq::QmvTable& a, int blocks, int sb_dt, int gs, size_t lds,
                                hipStream_t stream) {
+    if (a.m > kStreamSlotsMax) {
+        if constexpr (RQ_BITS == 4 || RQ_BITS == 8) {
+            return wide_dispatch(sb_dt, a.m, gs, [&](auto sd, auto mp, auto gsh) {
+                hipLaunchKernelGGL((qmv_wide_table<RQ_BITS, decltype(sd)::value, decltype(mp)::value,
+                                                   decltype(gsh)::value>),
+                                   dim3(blocks), dim3(kBlock), 0, stream, a);
+                return hipGetLastError();
+            });
+        }
+        return hipErrorInvalidValue;
+    }
     return stream_dispatch(sb_dt, a.m, gs, [&](auto sd, auto nmc, auto mi, auto gsh) {
         hipLaunchKernelGGL((qmv_stream_table<RQ_BITS, decltype(sd)::value, decltype(nmc)::value,
                                              decltype(mi)::value, decltype(gsh)::value>),
@@ -1166,6 +1469,7 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
 
 #if RQ_BITS == 4  // bit-width independent helpers: defined in one unit only
 size_t qmv_stream_lds(int64_t m, int64_t cols, int gs, int bits) {
+    if (m > kStreamSlotsMax) return 0;  // the wide kernel's LDS is static
     const int wave_bytes = gs == 32 ? StreamWin<5>::WAVE_BYTES
                          : (gs == 64 ? StreamWin<6>::WAVE_BYTES : StreamWin<7>::WAVE_BYTES);
     const int xg = gs < 64 ? gs : 64;  // elements per activation sum
@@ -1174,12 +1478,12 @@ size_t qmv_stream_lds(int64_t m, int64_t cols, int gs, int bits) {
            nsum * (((size_t)m * (cols / xg) * 4 + 15) & ~(size_t)15) + 4 * (size_t)wave_bytes;
 }
 bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs, int bits) {
-    // m > 4 takes ceil(m/4) passes of 4 slots here; the LDS-staged kernel's
-    // 8-row slots (gs 64) do less MFMA work there
-    return m <= RQ_QMV_STREAM_MMAX && sb_dt != RQ_F32 && p.cols % 512 == 0 &&
-           p.rows <= (int64_t)65536 * kQmvRowsPerBlock &&
-           (((uintptr_t)p.scales | (uintptr_t)p.biases) & 15) == 0 &&
-           qmv_stream_lds(m, p.cols, gs, bits) <= (size_t)kQmvLdsBudget;
+    const bool layout = sb_dt != RQ_F32 && p.cols % 512 == 0 &&
+                        p.rows <= (int64_t)65536 * kQmvRowsPerBlock &&
+                        (((uintptr_t)p.scales | (uintptr_t)p.biases) & 15) == 0;
+    if (m > kStreamSlotsMax)  // the wide kernel (static LDS, chunked x)
+        return RQ_QMV_WIDE && layout && m <= 16 && (bits == 4 || bits == 8);
+    return layout && qmv_stream_lds(m, p.cols, gs, bits) <= (size_t)kQmvLdsBudget;
 }
 #endif
 

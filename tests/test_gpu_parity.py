@@ -459,8 +459,35 @@ def test_planned_qmv_dtypes(O, rq, dev, xdt, sdt):
         rel_check(y, ref, what=f"planned {xdt} {sdt}")
 
 
+# The wide kernel (4 < m <= 16, 4- and 8-bit codes): x staged in chunks of
+# 1024 columns, so contractions of one partial chunk (512), whole chunks
+# (1024, 2048, 8192) and a partial last chunk (1536) are all covered; row
+# counts that end mid-block; m = 5 and 9 leave zero A rows in the ring.
+WIDE_SHAPES = [(100, 512), (64, 1024), (17, 2048), (40, 1536), (33, 8192)]
+
+
+@pytest.mark.parametrize("M", [5, 8, 9, 16])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", [4, 8])
+def test_planned_wide_qmv_parity(O, rq, dev, bits, gs, M):
+    say(f"planned wide qmv bits={bits} gs={gs} M={M}")
+    plan, refs, _, _ = _planned(O, rq, dev, WIDE_SHAPES, M, gs, bits, 5300 + 10 * bits + gs + M)
+    for y, ref in zip(plan.run(), refs):
+        rel_check(y, ref, what=f"planned wide b{bits} g{gs} M{M}")
+
+
+@pytest.mark.parametrize("xdt,sdt", [(torch.float32, torch.bfloat16), (torch.float16, torch.float16),
+                                     (torch.bfloat16, torch.float16)])
+def test_planned_wide_qmv_dtypes(O, rq, dev, xdt, sdt):
+    say(f"planned wide qmv x={xdt} s={sdt}")
+    plan, refs, _, _ = _planned(O, rq, dev, WIDE_SHAPES, 8, 64, 4, 5950, xdt, sdt)
+    for y, ref in zip(plan.run(), refs):
+        rel_check(y, ref, what=f"planned wide {xdt} {sdt}")
+
+
 def test_planned_rejects_uncovered_sets(O, rq, dev):
-    """m > 4 or a cols not multiple of 512: planned=True raises, auto falls back."""
+    """cols not a multiple of 512, or 4 < m <= 16 with codes other than 4- or
+    8-bit: planned=True raises, auto falls back."""
     from rwkvq._lib import RwkvqError
     w = weights(64, 768, 1)
     wq, s, b = (t.to(dev) for t in O.quantize(w, 64, 4))
@@ -468,6 +495,12 @@ def test_planned_rejects_uncovered_sets(O, rq, dev):
     with pytest.raises(RwkvqError):
         rq.GroupedQmv([x], [(wq, s, b)], 64, 4, planned=True)
     assert rq.GroupedQmv([x], [(wq, s, b)], 64, 4).plan is None
+    w = weights(64, 1024, 2)
+    wq, s, b = (t.to(dev) for t in O.quantize(w, 64, 3))
+    x = acts(8, 1024, 2).to(dev)
+    with pytest.raises(RwkvqError):
+        rq.GroupedQmv([x], [(wq, s, b)], 64, 3, planned=True)
+    assert rq.GroupedQmv([x], [(wq, s, b)], 64, 3).plan is None
 
 
 def test_planned_many_problems_one_launch(O, rq, dev):
@@ -487,12 +520,12 @@ def test_planned_many_problems_one_launch(O, rq, dev):
         rel_check(y, ref, what=f"planned150 rerun {i}")
 
 
-@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("M", [1, 4, 8, 16])
 @pytest.mark.parametrize("bits", [3, 4, 8])
 def test_streamed_single_launch_path(O, rq, dev, bits, M):
     """A single problem big enough (>= 2048 16-row blocks) for the streamed
     kernel through rq_qmm itself (3-bit: codes straddling words, the
-    mixed-offset pair extraction)."""
+    mixed-offset pair extraction; M > 4 at 4 and 8 bits: the wide kernel)."""
     R, K = 32768 + 40, 1024
     w = weights(R, K, 8100 + bits)
     wq, s, b = O.quantize(w, 64, bits)
