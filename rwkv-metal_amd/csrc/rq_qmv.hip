@@ -803,8 +803,7 @@ RQ_DEV XRaw load_x8(const void* x, int x_dt, int64_t e) {  // e: index of the 8-
         r.lo = p[0];
         r.hi = p[1];
     } else {
-        r.lo = ((const RQ_GLOBAL u32x4_t*)x)[e];
-        r.hi = r.lo;
+        r.lo = ((const RQ_GLOBAL u32x4_t*)x)[e];  // r.hi unused
     }
     return r;
 }
@@ -1051,26 +1050,32 @@ __global__ __launch_bounds__(kBlock) RQ_STREAM_OCC void qmv_stream_table(const r
 //
 // qmv_wide_*: the decode GEMV for 4 < m <= 16 on the streamed layout (same
 // stages, lane loads, (scale, bias) windows and launch forms as
-// qmv_stream_*), with every A row of the MFMA an activation row:
+// qmv_stream_*).  Lane group g of a wave holds the 64 codes (eight 8-code
+// pieces) of 64-code unit g of a stage for its row.  After the loads
+// arrive, pieces are exchanged between lane groups with v_permlane32_swap
+// and v_permlane16_swap so that each MFMA's 32-element contraction holds
+// codes of as few groups as the activation rows allow:
 //
-//  * After its loads arrive, the 4 x 4 block (lane group g, 8-code piece j)
-//    of each run half of a stage is transposed across lane groups with
-//    v_permlane32_swap and v_permlane16_swap (4 swaps per 4 words): lane
-//    group g then holds piece g of run 2t+h of every lane group t, so MFMA
-//    (t, h) contracts exactly run 2t+h -- 32 codes of ONE group -- for 16
-//    activation rows m and 16 weight rows n.  No slots: one pass for any
-//    m <= 16 (the slotted kernel needs ceil(m/4)).
-//  * The activation sums over the same 32 codes come from a second MFMA of
-//    the same A fragment with a constant B (bf16 1.0), so only the
-//    pair-permuted bf16 x is staged: per group, acc += s D + (b - 128 s) X
-//    (8-bit: b X), the lane reading its row's GPS (scale, bias) values of the
-//    stage from the wave's window.
-//  * x is staged in chunks of one iteration (4 stages, 1024 columns) into a
-//    two-slot LDS ring: the next chunk's loads are issued at the start of an
-//    iteration and written after its MFMAs, behind one barrier per
-//    iteration, so LDS does not grow with K.  Rows m >= M of the ring are
-//    zero.
-//  * Lane L's accumulator holds D rows m = 4(L/16) + i of weight row L%16.
+//  * m <= 8 (MP = 8, two slots): one swap per piece pair moves lane-group
+//    bit 1 into the register index.  MFMA (P, v) then holds in lane group
+//    2b + c piece 2v + b of unit 2P + c: A rows 0-7 carry x[m] on the units
+//    2P pieces (lane groups 0 and 2), rows 8-15 on the 2P+1 pieces (lane
+//    groups 1 and 3), zero elsewhere, so D rows 0-7 sum unit 2P and rows
+//    8-15 unit 2P+1, and lane L's accumulator rows belong to one unit:
+//    2P + (L/32).  Four MFMAs cover two units; the halves are summed across
+//    lane groups g, g^2 at the end.
+//  * m <= 16 (MP = 16, no slots): a full 4 x 4 transpose of (lane group,
+//    piece) per run half (4 swaps per 4 words) makes MFMA (t, h) contract
+//    exactly run 2t+h of the stage, with 16 activation rows.
+//  * The activation sums over the same codes come from a second MFMA of the
+//    same A fragment with a constant B (bf16 1.0), so only the pair-permuted
+//    bf16 x is staged: per group, acc += s D + (b - 128 s) X (8-bit: b X).
+//  * x lives in a two-slot LDS ring of 1024-column chunks (one iteration of
+//    4 stages each).  K <= 2048 is staged whole up front (no barrier in the
+//    loop); longer rows stream chunks: the next chunk's loads are issued at
+//    the start of an iteration and written after its MFMAs, behind one
+//    barrier per iteration, so LDS does not grow with K.  Rows m >= M of
+//    the ring are zero, and so is a 1024-column line that idle A lanes read.
 // 4- and 8-bit codes: their pieces are whole words.
 constexpr int kWideNS = 4;                // stages per iteration = per staged x chunk
 constexpr int kWideKC = 256 * kWideNS;    // x columns per chunk
@@ -1086,23 +1091,53 @@ RQ_DEV void transpose_lane_groups(uint32_t& a, uint32_t& b, uint32_t& c, uint32_
     a = r2[0]; b = r2[1]; c = r3[0]; d = r3[1];
 }
 
-template <int MP, int GSH>
+// codes_to_bf16_pairs<4> of two words at once: the shifted copies of both
+// come from 64-bit shifts of the pair (3 shifts for 2 words instead of 6;
+// bits shifted in from the other word fall outside the 0x000F000F mask).
+#ifndef RQ_QMV_SHIFT64
+#define RQ_QMV_SHIFT64 1
+#endif
+RQ_DEV void codes4_to_bf16_pairs_x2(uint32_t w0, uint32_t w1, uint32_t* o0, uint32_t* o1,
+                                    const PairConsts& k) {
+#if RQ_QMV_SHIFT64
+    const uint64_t ww = ((uint64_t)w1 << 32) | w0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint64_t t = ww >> (4 * i);
+        o0[i] = ((uint32_t)t & k.mask) | k.magic;
+        o1[i] = ((uint32_t)(t >> 32) & k.mask) | k.magic;
+    }
+#else
+    const uint32_t ws[2] = {w0, w1};
+    codes_to_bf16_pairs<4>(ws, 0, o0, k);
+    codes_to_bf16_pairs<4>(ws, 1, o1, k);
+#endif
+}
+
+// Swap of lane groups 2, 3 of a with lane groups 0, 1 of b.
+RQ_DEV void swap_lane_halves(uint32_t& a, uint32_t& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    a = r[0]; b = r[1];
+}
+
+template <int MP>
 struct WideLds {
-    static constexpr int X_ELEMS = 2 * MP * kWideRow;                 // x ring
-    static constexpr int BYTES = 2 * X_ELEMS + kWaves * StreamWin<GSH>::WAVE_BYTES;
+    static constexpr int ZERO = 2 * MP * kWideRow;   // zero line read by idle A lanes (MP = 8)
+    static constexpr int DUMMY = ZERO + (MP == 8 ? kWideKC : 0);  // 16-B sink for idle stores
+    static constexpr int X_ELEMS = DUMMY + 8;
 };
 
-template <int BITS, int SDT, int MP, int GSH>
+template <int BITS, int SDT, int MP, int GSH, bool XF32>
 RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int y_dt) {
     static_assert(BITS == 4 || BITS == 8, "wide GEMV: codes whose 8-code pieces are whole words");
     static_assert(SDT != RQ_F32, "streamed scales are 16-bit");
+    static_assert(MP == 8 || MP == 16, "");
     typedef StreamWin<GSH> W;
-    typedef WideLds<MP, GSH> L;
+    typedef WideLds<MP> L;
     __shared__ __attribute__((aligned(16))) uint16_t xring[L::X_ELEMS];
     __shared__ __attribute__((aligned(16))) uint8_t wins[kWaves * W::WAVE_BYTES];
     constexpr int NS = kWideNS;
     constexpr int PW = BITS / 4;                                       // words per 8-code piece
-    constexpr int GPS = W::GPS;                                        // groups per stage
     constexpr int XQ = (MP * (kWideKC / 8) + kBlock - 1) / kBlock;     // x pieces per thread per chunk
     typedef Words<W::WW / 8> win_t;
 
@@ -1133,136 +1168,221 @@ RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int 
     }
 
     // ---- x chunks: piece e of a chunk is row e / 128, columns 8 (e % 128) ..
+    // Loads and stores of a chunk are unconditional (a chunk past the last
+    // reloads the last, idle pieces go to a sink): the compiler's wait
+    // analysis is path-insensitive, so loads left unconsumed on any path
+    // around the loop made it wait at the loop head for every load issued
+    // after them, the code pipeline included.  (x_dt is a template choice
+    // between f32 and 16-bit here for the same reason.)
     const int npc = M * (kWideKC / 8);
     const int64_t k8 = K >> 3;
     auto load_chunk = [&](int c, XRaw* xr) {
+        c = c < niter ? c : niter - 1;
 #pragma unroll
         for (int q = 0; q < XQ; ++q) {
             const int e = threadIdx.x + q * kBlock;
             const int64_t col8 = (int64_t)c * (kWideKC / 8) + (e & 127);
             const bool ok = e < npc && col8 < k8;
-            xr[q] = load_x8(P.x, x_dt, ok ? (int64_t)(e >> 7) * k8 + col8 : 0);
+            const int64_t i = ok ? (int64_t)(e >> 7) * k8 + col8 : 0;
+            if constexpr (XF32) {
+                const RQ_GLOBAL u32x4_t* src = (const RQ_GLOBAL u32x4_t*)P.x + 2 * i;
+                xr[q].lo = src[0];
+                xr[q].hi = src[1];
+            } else {
+                xr[q].lo = ((const RQ_GLOBAL u32x4_t*)P.x)[i];
+            }
         }
     };
     auto store_chunk = [&](int slot, const XRaw* xr) {
 #pragma unroll
         for (int q = 0; q < XQ; ++q) {
             const int e = threadIdx.x + q * kBlock;
-            if (e < npc) {
-                uint32_t d[4], pr[4];
-                x8_to_bf16(xr[q], x_dt, d);
-                reorder_pairs(d, pr);
-                *(u32x4_t*)&xring[slot * MP * kWideRow + (e >> 7) * kWideRow + (e & 127) * 8] =
-                    u32x4_t{pr[0], pr[1], pr[2], pr[3]};
-            }
+            uint32_t d[4], pr[4];
+            x8_to_bf16(xr[q], XF32 ? RQ_F32 : x_dt, d);
+            reorder_pairs(d, pr);
+            const int off = e < npc ? slot * MP * kWideRow + (e >> 7) * kWideRow + (e & 127) * 8
+                                    : L::DUMMY;
+            *(u32x4_t*)&xring[off] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
         }
     };
-    XRaw xr[XQ];
-    load_chunk(0, xr);
-    // rows M..MP-1 of both slots stay zero (A rows without an activation row)
-    for (int e = threadIdx.x; e < 2 * (MP - M) * (kWideRow / 8); e += kBlock) {
-        const int slot = e / ((MP - M) * (kWideRow / 8)), r = e % ((MP - M) * (kWideRow / 8));
-        *(u32x4_t*)&xring[slot * MP * kWideRow + M * kWideRow + r * 8] = u32x4_t{0u, 0u, 0u, 0u};
+    const bool whole = niter <= 2;  // K <= 2048: both chunks staged up front
+    {
+        XRaw xr0[XQ], xr1[XQ];
+        load_chunk(0, xr0);
+        load_chunk(whole ? 1 : 0, xr1);  // streaming: chunk 0 again (slot 0 is written twice)
+        // rows M..MP-1 of both slots and the zero line
+        const int zr = (MP - M) * (kWideRow / 8);
+        for (int e = threadIdx.x; e < 2 * zr; e += kBlock) {
+            const int slot = e >= zr, r = e - slot * zr;
+            *(u32x4_t*)&xring[slot * MP * kWideRow + M * kWideRow + r * 8] = u32x4_t{0u, 0u, 0u, 0u};
+        }
+        if constexpr (MP == 8) {
+            for (int e = threadIdx.x; e < kWideKC / 8; e += kBlock)
+                *(u32x4_t*)&xring[L::ZERO + e * 8] = u32x4_t{0u, 0u, 0u, 0u};
+        }
+        store_chunk(0, xr0);
+        store_chunk(whole ? 1 : 0, xr1);
     }
-    store_chunk(0, xr);
     __syncthreads();
 
     // ---- per-lane constants
     const PairConsts kc = pair_consts();
     constexpr uint32_t kOne = 0x3F803F80u;  // bf16 1.0 pairs
     const bf16x8_t ones = as_bf16x8(kOne, kOne, kOne, kOne);
-    const uint32_t a_off = (uint32_t)(lr * kWideRow + lg * 8);
+    // A fragment addresses (elements) in slot 0 and slot 1
+    uint32_t a_base[2];
+    if constexpr (MP == 8) {
+        // lane (lg, lr): A row lr of slot lr/8 has x[lr % 8] on the pieces of
+        // lane groups with (lg & 1) == lr/8: piece 8 (lg >> 1) of unit lg & 1
+        const bool act = ((lr >> 3) == (lg & 1)) && (lr & 7) < M;
+        const uint32_t col = (uint32_t)(64 * (lg & 1) + 8 * (lg >> 1));
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+            a_base[s] = act ? (uint32_t)(s * MP * kWideRow + (lr & 7) * kWideRow) + col
+                            : (uint32_t)L::ZERO + col;
+    } else {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) a_base[s] = (uint32_t)(s * MP * kWideRow + lr * kWideRow + lg * 8);
+    }
     uint8_t* win = wins + wave * W::WAVE_BYTES;
     uint8_t* win_w = win + lr * W::ROWB + (lg & 1) * W::WW + (lg >> 1) * (W::WW / 2);
     const uint8_t* win_r = win + lr * W::ROWB;
 
+    auto sb_at = [&](int gw, float& s, float& cb) {  // group gw of the window, row lr
+        s = raw_to_f32<SDT>(*(const uint16_t*)(win_r + gw * 2));
+        const float b = raw_to_f32<SDT>(*(const uint16_t*)(win_r + W::WW + gw * 2));
+        cb = (BITS == 8) ? b : fmaf(s, -128.f, b);
+    };
+
     f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    for (int it = 0; it < niter; ++it) {
-        const int itw = it % W::IPW;
-        if (itw == 0) {
-            // this window of (scale, bias) values into LDS, the next one into registers
-            *(win_t*)win_w = wv;  // read below by other lanes of this wave (LDS runs in order)
-            __builtin_amdgcn_wave_barrier();
-            wv = load_sb_window<GSH>(sbrow, part, G, it / W::IPW + 1, P.x);
-        }
-        const bool more = it + 1 < niter;
-        if (more) load_chunk(it + 1, xr);
-        const uint16_t* xs = xring + (it & 1) * MP * kWideRow + a_off;
-#pragma unroll
-        for (int t = 0; t < NS; ++t) {
-            const int st = it * NS + t;
-            load_codes(st + NS - 1, cw[(t + NS - 1) % NS]);
-            if (st < nst) {
-                // (scale, bias) of the stage's GPS groups for row lr
-                float sc[GPS], cb[GPS];
-                {
-                    const int gw = itw * W::GPI + t * W::GPS;  // first group of the stage in the window
-                    uint32_t sr[(GPS + 1) / 2], br[(GPS + 1) / 2];
-                    if constexpr (GPS == 8) {
-                        const u32x4_t a = *(const u32x4_t*)(win_r + gw * 2);
-                        const u32x4_t b = *(const u32x4_t*)(win_r + W::WW + gw * 2);
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) { sr[q] = a[q]; br[q] = b[q]; }
-                    } else if constexpr (GPS == 4) {
-                        const u32x2_t a = *(const u32x2_t*)(win_r + gw * 2);
-                        const u32x2_t b = *(const u32x2_t*)(win_r + W::WW + gw * 2);
-                        sr[0] = a[0]; sr[1] = a[1]; br[0] = b[0]; br[1] = b[1];
-                    } else {
-                        sr[0] = *(const uint32_t*)(win_r + gw * 2);
-                        br[0] = *(const uint32_t*)(win_r + W::WW + gw * 2);
-                    }
-#pragma unroll
-                    for (int q = 0; q < GPS; ++q) {
-                        const uint32_t sb = (q & 1) ? sr[q >> 1] >> 16 : sr[q >> 1] & 0xffffu;
-                        const uint32_t bb = (q & 1) ? br[q >> 1] >> 16 : br[q >> 1] & 0xffffu;
-                        sc[q] = raw_to_f32<SDT>(sb);
-                        const float bi = raw_to_f32<SDT>(bb);
-                        cb[q] = (BITS == 8) ? bi : fmaf(sc[q], -128.f, bi);
-                    }
-                }
-                uint32_t* w = cw[t];
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int p = 0; p < PW; ++p)
-                        transpose_lane_groups(w[h * BITS + p], w[h * BITS + PW + p],
-                                              w[h * BITS + 2 * PW + p], w[h * BITS + 3 * PW + p]);
-                f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f}, xsum = d;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {  // run u = 2 t2 + h of the stage
-                    const int t2 = u >> 1, h = u & 1;
-                    uint32_t pr[4];
-                    codes_to_bf16_pairs<BITS>(w + h * BITS, t2, pr, kc);
-                    const u32x4_t av = *(const u32x4_t*)&xs[t * 256 + 32 * u];
-                    const bf16x8_t a = as_bf16x8(av[0], av[1], av[2], av[3]);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        a, as_bf16x8(pr[0], pr[1], pr[2], pr[3]), d, 0, 0, 0);
-                    xsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xsum, 0, 0, 0);
-                    const int gi = (32 * u) >> GSH;
-                    if (u == 7 || ((32 * (u + 1)) >> GSH) != gi) {  // the group ends with this run
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            acc[i] = fmaf(sc[gi], d[i], fmaf(cb[gi], xsum[i], acc[i]));
-                        d = f32x4_t{0.f, 0.f, 0.f, 0.f};
-                        xsum = d;
-                    }
-                }
+    auto run = [&](auto streaming) {
+        for (int it = 0; it < niter; ++it) {
+            const int itw = it % W::IPW;
+            if (itw == 0) {
+                // this window of (scale, bias) values into LDS, the next one into registers
+                *(win_t*)win_w = wv;  // read below by other lanes of this wave (LDS runs in order)
+                __builtin_amdgcn_wave_barrier();
+                wv = load_sb_window<GSH>(sbrow, part, G, it / W::IPW + 1, P.x);
             }
-            __builtin_amdgcn_sched_barrier(0);
+            XRaw xr[XQ];
+            if constexpr (decltype(streaming)::value) load_chunk(it + 1, xr);
+            const uint16_t* xs = xring + a_base[it & 1];
+#pragma unroll
+            for (int t = 0; t < NS; ++t) {
+                const int st = it * NS + t;
+                load_codes(st + NS - 1, cw[(t + NS - 1) % NS]);
+                if (st < nst) {
+                    const int gw0 = itw * W::GPI + t * W::GPS;  // first group of the stage in the window
+                    uint32_t* w = cw[t];
+                    if constexpr (MP == 8) {
+                        // (scale, bias) of this lane's groups, read before the MFMAs so
+                        // that the LDS latency is hidden: unit 2 Pp + (lg >> 1) of pair Pp
+                        constexpr int NG = GSH == 5 ? 4 : 2;
+                        float sc[NG], cb[NG];
+#pragma unroll
+                        for (int q = 0; q < NG; ++q) {
+                            const int Pp = GSH == 5 ? q >> 1 : q, unit = 2 * Pp + (lg >> 1);
+                            const int g = GSH == 5 ? 2 * unit + (q & 1) : (GSH == 6 ? unit : unit >> 1);
+                            sb_at(gw0 + g, sc[q], cb[q]);
+                        }
+#pragma unroll
+                        for (int v = 0; v < 4; ++v)
+#pragma unroll
+                            for (int p = 0; p < PW; ++p) swap_lane_halves(w[2 * v * PW + p], w[(2 * v + 1) * PW + p]);
+                        f32x4_t d[2], xsum[2];
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            uint32_t pr[2][4];
+                            if constexpr (BITS == 4) {
+                                codes4_to_bf16_pairs_x2(w[2 * v], w[2 * v + 1], pr[0], pr[1], kc);
+                            } else {
+                                codes_to_bf16_pairs<BITS>(w, 2 * v, pr[0], kc);
+                                codes_to_bf16_pairs<BITS>(w, 2 * v + 1, pr[1], kc);
+                            }
+#pragma unroll
+                            for (int Pp = 0; Pp < 2; ++Pp) {
+                                const u32x4_t av = *(const u32x4_t*)&xs[t * 256 + 128 * Pp + 16 * v];
+                                const bf16x8_t a = as_bf16x8(av[0], av[1], av[2], av[3]);
+                                const f32x4_t z = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                                const bool first = GSH == 5 ? (v & 1) == 0 : v == 0;
+                                d[Pp] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                    a, as_bf16x8(pr[Pp][0], pr[Pp][1], pr[Pp][2], pr[Pp][3]),
+                                    first ? z : d[Pp], 0, 0, 0);
+                                xsum[Pp] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, first ? z : xsum[Pp], 0, 0, 0);
+                            }
+                            // gs 32: pieces 2v + b of v < 2 are a unit's first run
+                            if (GSH != 5 ? v == 3 : (v & 1) == 1) {
+#pragma unroll
+                                for (int Pp = 0; Pp < 2; ++Pp) {
+                                    const int q = GSH == 5 ? 2 * Pp + (v >> 1) : Pp;
+#pragma unroll
+                                    for (int i = 0; i < 4; ++i)
+                                        acc[i] = fmaf(sc[q], d[Pp][i], fmaf(cb[q], xsum[Pp][i], acc[i]));
+                                }
+                            }
+                        }
+                    } else {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+#pragma unroll
+                            for (int p = 0; p < PW; ++p)
+                                transpose_lane_groups(w[h * BITS + p], w[h * BITS + PW + p],
+                                                      w[h * BITS + 2 * PW + p], w[h * BITS + 3 * PW + p]);
+                        float sc[W::GPS], cb[W::GPS];
+#pragma unroll
+                        for (int q = 0; q < W::GPS; ++q) sb_at(gw0 + q, sc[q], cb[q]);
+                        f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f}, xsum = d;
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {  // run u = 2 t2 + h of the stage
+                            const int t2 = u >> 1, h = u & 1;
+                            uint32_t pr[4];
+                            codes_to_bf16_pairs<BITS>(w + h * BITS, t2, pr, kc);
+                            const u32x4_t av = *(const u32x4_t*)&xs[t * 256 + 32 * u];
+                            const bf16x8_t a = as_bf16x8(av[0], av[1], av[2], av[3]);
+                            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                a, as_bf16x8(pr[0], pr[1], pr[2], pr[3]), d, 0, 0, 0);
+                            xsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xsum, 0, 0, 0);
+                            const int gi = (32 * u) >> GSH;
+                            if (u == 7 || ((32 * (u + 1)) >> GSH) != gi) {  // the group ends with this run
+#pragma unroll
+                                for (int i = 0; i < 4; ++i)
+                                    acc[i] = fmaf(sc[gi], d[i], fmaf(cb[gi], xsum[i], acc[i]));
+                                d = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                                xsum = d;
+                            }
+                        }
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (decltype(streaming)::value) {
+                store_chunk((it + 1) & 1, xr);  // that slot was last read before the previous barrier
+                __syncthreads();
+            }
         }
-        if (more) store_chunk((it + 1) & 1, xr);  // that slot was last read before the previous barrier
-        __syncthreads();
-    }
+    };
+    if (whole) run(std::integral_constant<bool, false>());
+    else run(std::integral_constant<bool, true>());
 
     const int64_t row = row0 + lr;
+    if constexpr (MP == 8) {
+        // rows m = 4 (lg & 1) + i: lane groups g and g ^ 2 hold the two slots' parts
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = 4 * lg + i;
-        if (m < M && row < R) store_dt(P.y, y_dt, (int64_t)m * R + row, acc[i]);
+        for (int i = 0; i < 4; ++i) {
+            const float v = acc[i] + __shfl_xor(acc[i], 32, 64);
+            const int m = 4 * lg + i;
+            if (lg < 2 && m < M && row < R) store_dt(P.y, y_dt, (int64_t)m * R + row, v);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * lg + i;
+            if (m < M && row < R) store_dt(P.y, y_dt, (int64_t)m * R + row, acc[i]);
+        }
     }
 }
 
-template <int BITS, int SDT, int MP, int GSH>
+template <int BITS, int SDT, int MP, int GSH, bool XF32>
 __global__ __launch_bounds__(kBlock) void qmv_wide_inline(const QmvArgs args) {
     const int bid = blockIdx.x;
     int lo = 0, hi = args.n - 1;
@@ -1270,36 +1390,45 @@ __global__ __launch_bounds__(kBlock) void qmv_wide_inline(const QmvArgs args) {
         const int mid = (lo + hi + 1) >> 1;
         if (args.block_start[mid] <= bid) lo = mid; else hi = mid - 1;
     }
-    qmv_wide_body<BITS, SDT, MP, GSH>(args.p[lo], bid - args.block_start[lo], args.m, args.x_dt,
-                                      args.y_dt);
+    qmv_wide_body<BITS, SDT, MP, GSH, XF32>(args.p[lo], bid - args.block_start[lo], args.m,
+                                            args.x_dt, args.y_dt);
 }
 
-template <int BITS, int SDT, int MP, int GSH>
+template <int BITS, int SDT, int MP, int GSH, bool XF32>
 __global__ __launch_bounds__(kBlock) void qmv_wide_table(const rq::QmvTable a) {
     const uint32_t e = a.blocks[blockIdx.x];
     const rq_problem P = a.descs[e >> 16];
-    qmv_wide_body<BITS, SDT, MP, GSH>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
+    qmv_wide_body<BITS, SDT, MP, GSH, XF32>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
 }
 
-// F is called with integral_constant-typed (SDT, MP, GSH).
+// F is called with integral_constant-typed (SDT, MP, GSH, XF32).
 template <typename F>
-hipError_t wide_dispatch(int sb_dt, int64_t m, int gs, F&& f) {
+hipError_t wide_dispatch(int sb_dt, int64_t m, int gs, int x_dt, F&& f) {
     const int gsh = __builtin_ctz(gs);
     typedef std::integral_constant<int, RQ_BF16> BF;
     typedef std::integral_constant<int, RQ_F16> FH;
-#define RQ_W_GSH(SD, MPV)                                                                      \
-    switch (gsh) {                                                                             \
-        case 5: return f(SD(), std::integral_constant<int, MPV>(), std::integral_constant<int, 5>()); \
-        case 6: return f(SD(), std::integral_constant<int, MPV>(), std::integral_constant<int, 6>()); \
-        case 7: return f(SD(), std::integral_constant<int, MPV>(), std::integral_constant<int, 7>()); \
-        default: return hipErrorInvalidValue;                                                  \
+    typedef std::integral_constant<bool, true> XF;
+    typedef std::integral_constant<bool, false> XH;
+#define RQ_W_GSH(SD, MPV, XV)                                                          \
+    switch (gsh) {                                                                     \
+        case 5: return f(SD(), std::integral_constant<int, MPV>(),                     \
+                         std::integral_constant<int, 5>(), XV());                      \
+        case 6: return f(SD(), std::integral_constant<int, MPV>(),                     \
+                         std::integral_constant<int, 6>(), XV());                      \
+        case 7: return f(SD(), std::integral_constant<int, MPV>(),                     \
+                         std::integral_constant<int, 7>(), XV());                      \
+        default: return hipErrorInvalidValue;                                          \
     }
+#define RQ_W_X(SD, MPV)                                  \
+    if (x_dt == RQ_F32) { RQ_W_GSH(SD, MPV, XF) }        \
+    RQ_W_GSH(SD, MPV, XH)
 #define RQ_W_MP(SD)                      \
-    if (m <= 8) { RQ_W_GSH(SD, 8) }      \
-    RQ_W_GSH(SD, 16)
+    if (m <= 8) { RQ_W_X(SD, 8) }        \
+    RQ_W_X(SD, 16)
     if (sb_dt == RQ_BF16) { RQ_W_MP(BF) }
     RQ_W_MP(FH)
 #undef RQ_W_MP
+#undef RQ_W_X
 #undef RQ_W_GSH
 }
 
@@ -1340,9 +1469,9 @@ hipError_t launch_stream_inline(const QmvArgs& a, int blocks, int sb_dt, int gs,
                                 hipStream_t stream) {
     if (a.m > kStreamSlotsMax) {
         if constexpr (RQ_BITS == 4 || RQ_BITS == 8) {
-            return wide_dispatch(sb_dt, a.m, gs, [&](auto sd, auto mp, auto gsh) {
+            return wide_dispatch(sb_dt, a.m, gs, a.x_dt, [&](auto sd, auto mp, auto gsh, auto xf) {
                 hipLaunchKernelGGL((qmv_wide_inline<RQ_BITS, decltype(sd)::value, decltype(mp)::value,
-                                                    decltype(gsh)::value>),
+                                                    decltype(gsh)::value, decltype(xf)::value>),
                                    dim3(blocks), dim3(kBlock), 0, stream, a);
                 return hipGetLastError();
             });
@@ -1361,9 +1490,9 @@ hipError_t launch_stream_table(const rq::QmvTable& a, int blocks, int sb_dt, int
                                hipStream_t stream) {
     if (a.m > kStreamSlotsMax) {
         if constexpr (RQ_BITS == 4 || RQ_BITS == 8) {
-            return wide_dispatch(sb_dt, a.m, gs, [&](auto sd, auto mp, auto gsh) {
+            return wide_dispatch(sb_dt, a.m, gs, a.x_dt, [&](auto sd, auto mp, auto gsh, auto xf) {
                 hipLaunchKernelGGL((qmv_wide_table<RQ_BITS, decltype(sd)::value, decltype(mp)::value,
-                                                   decltype(gsh)::value>),
+                                                   decltype(gsh)::value, decltype(xf)::value>),
                                    dim3(blocks), dim3(kBlock), 0, stream, a);
                 return hipGetLastError();
             });
