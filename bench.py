@@ -10,7 +10,8 @@ a single launch over the 145 independent GEMVs.  `value` = effective weight-stre
 (R*K*bits/8 + 2*R*(K/gs)*2 bytes summed over the sweep) / step time, with all
 inputs resident in HBM.
 
-Alongside: the same sweep at M=8, one GEMV launch per projection, the prefill
+Alongside: the same sweep at M=8, one GEMV launch per projection (eagerly, and
+replayed from one HIP graph), the prefill
 GEMM (RWKV-7 2.9B shapes, M=4096/2048/512) and its
 transposed product in TFLOP/s, the QLoRA dX product at config-4 shapes, the
 config-5 mixed-bit model (7.2B shapes, 3-bit layers + 8-bit head: decode
@@ -476,6 +477,14 @@ def main():
                 f()
         tpc = time_region(torch, per_call, max(3, args.steps // 4), 1)
         extra["decode_m1_one_launch_per_projection_gbs"] = round(total_wbytes / tpc / 1e9, 2)
+        # the same 145 launches captured once in a HIP graph and replayed:
+        # one graph launch per decode step instead of 145 host dispatches
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            per_call()
+        tgr = time_region(torch, graph.replay, max(3, args.steps // 4), 3)
+        extra["decode_m1_one_launch_per_projection_hip_graph_gbs"] = round(total_wbytes / tgr / 1e9, 2)
+        del graph
         # prefill GEMM, config 3 (RWKV-7 2.9B shapes) at M = 4096 (aggregate) and
         # 2048 / 512; the transposed product (QLoRA dX) at M = 4096
         pre = {}

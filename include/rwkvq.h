@@ -199,9 +199,10 @@ int rq_qmm_grouped(const rq_problem* problems, int n, rq_dtype x_dt, rq_dtype sb
  * rq_grouped_plan_init: validates, orders the problems longest contraction
  *   first, uploads the table to `table` and SYNCHRONISES `stream` (the host
  *   staging copy does not outlive the call).  Returns RQ_EUNSUPPORTED for
- *   problems outside the planned kernel (m <= 4; scales must be 16-bit and
- *   16-byte aligned, cols % 512 == 0, m*cols*2 bytes of activations within
- *   the LDS budget); rq_qmm_grouped covers those.  Small sets (fewer than
+ *   problems outside the planned kernels (scales must be 16-bit and
+ *   16-byte aligned, cols % 512 == 0, and either m <= 4 with m*cols*2 bytes
+ *   of activations within the LDS budget or 4 < m <= 16 with 4- or 8-bit
+ *   codes); rq_qmm_grouped covers those.  Small sets (fewer than
  *   about 1024 blocks of 64 rows) run faster on rq_qmm_grouped, which splits
  *   them along K. 
  * rq_grouped_plan_run: one launch on `stream`.  The table and every pointer

@@ -535,6 +535,51 @@ def test_streamed_single_launch_path(O, rq, dev, bits, M):
     rel_check(y, O.quantized_matmul(x, wq, s, b, True, 64, bits, out_dtype=torch.float32, weights="exact"))
 
 
+@pytest.mark.parametrize("M", [1, 8])
+def test_decode_launches_in_a_hip_graph(O, rq, dev, M):
+    """A decode step of per-projection launches (rq_qmm_grouped's K-split
+    kernel) plus one planned launch, captured once in a HIP graph: every
+    replay -- with new activations written in place and eager work between
+    replays -- matches the eager launches bit for bit, and the oracle."""
+    shapes = [(256, 1024), (512, 2048), (2048, 512)]
+    xs, ws = [], []
+    for i, (R, K) in enumerate(shapes):
+        wq, s, b = O.quantize(weights(R, K, 9100 + i), 64, 4)
+        ws.append((wq.to(dev), s.to(dev), b.to(dev)))
+        xs.append(acts(M, K, 9100 + i).to(dev))
+    singles = [rq.GroupedQmv([x], [w], 64, 4) for x, w in zip(xs, ws)]
+    assert all(g.plan is None for g in singles)
+    planned = rq.GroupedQmv(xs, ws, 64, 4, planned=True)
+    outs = [o for g in singles + [planned] for o in g.outs]
+
+    def step():
+        for g in singles + [planned]:
+            g.run()
+
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for rep in range(3):
+        say(f"hip graph M={M} replay {rep}")
+        for i, x in enumerate(xs):
+            x.copy_(acts(M, x.shape[-1], 9200 + 10 * rep + i).to(dev))
+        step()
+        torch.cuda.synchronize()
+        eager = [o.clone() for o in outs]
+        for o in outs:
+            o.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert bits_equal(o, e), f"replay {rep} differs from the eager launches"
+        for i, (x, (wq, s, b)) in enumerate(zip(xs, ws)):
+            ref = O.quantized_matmul(x.cpu(), wq.cpu(), s.cpu(), b.cpu(), True, 64, 4,
+                                     out_dtype=torch.float32, weights="exact")
+            rel_check(outs[i], ref, what=f"graph replay {rep} problem {i}")
+
+
 # ---------------------------------------------- autograd / modules / LoRA
 
 def test_autograd_dx_is_transposed_qmm(O, rq, dev):
