@@ -160,6 +160,25 @@ def test_qmv_parity_dtypes(O, rq, dev, bits, gs, xdt, sdt):
     rel_check(y, ref, what="qmv dtypes")
 
 
+# Small single launches (the K-split kernel) over contraction lengths from
+# one 256-code stage to 16384, rows ending mid-tile.
+SMALL_SHAPES = [(200, 256), (37, 768), (130, 2048), (64, 2304), (100, 8192), (17, 16384)]
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_qmv_small_launch_shapes(O, rq, dev, bits, gs, M):
+    for R, K in SMALL_SHAPES:
+        w = weights(R, K, 7 * bits + gs + K)
+        wq, s, b = O.quantize(w, gs, bits)
+        x = acts(M, K, M + K)
+        say(f"qmv small bits={bits} gs={gs} M={M} R={R} K={K}")
+        y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
+        ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
+        rel_check(y, ref, what=f"small b{bits} g{gs} M{M} {R}x{K}")
+
+
 def test_qmv_edge_shapes(O, rq, dev):
     cases = [(1, 32, 32, 4, 1), (17, 96, 32, 3, 4), (5, 160, 32, 6, 7), (33, 128, 128, 8, 16),
              (1, 64, 64, 2, 1), (250, 96, 32, 5, 3)]
