@@ -196,10 +196,11 @@ def read_traffic():
 
 def make_sweep(rq, torch, dev, M, bits=4, gs=64):
     """Quantize the config-2 weights on the GPU (seed per layer/projection).
-    Also returns the quantize kernel's GB/s on the head weight (R*K*2 bytes
-    read + packed bytes written), timed as one region of repeated calls."""
+    Also returns the quantize and dequantize kernels' GB/s on the head weight
+    (R*K*2 bytes of bf16 weights + the packed bytes, read or written), each
+    timed as one region of repeated calls."""
     probs = []
-    qgbs = None
+    qgbs = dgbs = None
     for layer in range(LAYERS + 1):
         items = PROJ if layer < LAYERS else [("head", VOCAB, D)]
         for name, R, K in items:
@@ -208,13 +209,14 @@ def make_sweep(rq, torch, dev, M, bits=4, gs=64):
             w = (torch.randn(R, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
             wq, s, b = rq.quantize(w, gs, bits)
             if name == "head":
-                t = time_region(torch, lambda: rq.quantize(w, gs, bits), 10, 2)
-                qgbs = (R * K * 2 + weight_bytes(R, K, bits, gs)) / t / 1e9
+                nb = R * K * 2 + weight_bytes(R, K, bits, gs)
+                qgbs = nb / time_region(torch, lambda: rq.quantize(w, gs, bits), 20, 5) / 1e9
+                dgbs = nb / time_region(torch, lambda: rq.dequantize(wq, s, b, gs, bits), 20, 5) / 1e9
             del w
             gx = torch.Generator(device=dev).manual_seed(seed + 500)
             x = torch.randn(M, K, generator=gx, device=dev).to(torch.bfloat16)
             probs.append((name, x, (wq, s, b)))
-    return probs, qgbs
+    return probs, (qgbs, dgbs)
 
 
 def config5(torch, rq, dev, args):
@@ -407,7 +409,7 @@ def main():
         return
 
     # ---------------- headline: config-2 decode sweep, M=1, grouped launches
-    probs, quant_gbs = make_sweep(rwkvq, torch, dev, M=1)
+    probs, (quant_gbs, dequant_gbs) = make_sweep(rwkvq, torch, dev, M=1)
     total_wbytes = sum(weight_bytes(w[0].shape[0], x.shape[1]) for _, x, w in probs)
     xs = [x for _, x, _ in probs]
     ws = [w for _, _, w in probs]
@@ -461,6 +463,7 @@ def main():
     if not args.no_extra:
         extra = {}
         extra["quantize_gbs"] = round(quant_gbs, 1)
+        extra["dequantize_gbs"] = round(dequant_gbs, 1)
         # M=8 sweep
         xs8 = [torch.randn(8, x.shape[1], device=dev).to(torch.bfloat16) for x in xs]
         outs8 = [torch.empty(8, w[0].shape[0], dtype=torch.bfloat16, device=dev) for w in ws]
