@@ -65,10 +65,21 @@ __global__ __launch_bounds__(kBlock) void quantize_kernel(
         bias = edge;
     }
 
+    // code = clip(rint((w - bias) / scale)) with the IEEE quotient.  The
+    // quotient only matters through rint, so it is first approximated as
+    // (w - bias) * rcp(scale): v_rcp_f32 is within 1 ulp, so for |quotient|
+    // <= 512 the product is within 2^-13 of the exact quotient, and where it
+    // lies more than 2^-11 away from a half-integer both round to the same
+    // integer (ties included: a tie has the product within 2^-13 of .5).
+    // Only the rest take the IEEE division.
+    const float rs = __builtin_amdgcn_rcpf(scale);
     uint32_t codes[32];
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-        float q = rintf((v[j] - bias) / scale);
+        const float d = v[j] - bias;
+        float a = d * rs;
+        if (!(fabsf(a) <= 512.0f && fabsf(a - floorf(a) - 0.5f) > 0x1p-11f)) a = d / scale;
+        float q = rintf(a);
         q = fminf(fmaxf(q, 0.0f), n_bins);
         codes[j] = (uint32_t)q;
     }

@@ -74,6 +74,31 @@ def say(*a):
 
 # ------------------------------------------------------------ quantize
 
+@pytest.mark.parametrize("bits", BITS)
+def test_quantize_near_ties_bit_exact(O, rq, dev, bits):
+    """The quantizer rounds an approximate quotient unless it lies within
+    2^-11 of a half-integer, where it takes the IEEE division: groups whose
+    values sit at k + 1/2 + delta steps of their own scale (delta from 0 to
+    +-3e-4, a few steps out of range) must give the oracle's codes exactly."""
+    g = torch.Generator().manual_seed(4242 + bits)
+    nb = (1 << bits) - 1
+    rows = []
+    for _ in range(256):
+        c = float(torch.exp(torch.empty(1).uniform_(-12, 4, generator=g)))
+        off = float(torch.empty(1).uniform_(-2, 2, generator=g))
+        k = torch.randint(-1, nb + 1, (64,), generator=g).double()
+        delta = torch.tensor([0.0, 1e-7, -1e-7, 3e-6, -3e-6, 3e-5, -3e-5, 3e-4, -3e-4])[
+            torch.randint(0, 9, (64,), generator=g)].double()
+        v = (k + 0.5 + delta) * c + off
+        v[0], v[1] = off, off + nb * c  # the group's extremes
+        rows.append(v)
+    w = torch.stack(rows).float()
+    owq, os_, ob = O.quantize(w, 64, bits)
+    wq, s, b = rq.quantize(w.to(dev), 64, bits)
+    assert bits_equal(wq, owq), f"codes differ near ties at {bits} bits"
+    assert bits_equal(s, os_) and bits_equal(b, ob)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("gs", GROUPS)
 @pytest.mark.parametrize("bits", BITS)
