@@ -554,6 +554,9 @@ constexpr int kWsBlock = 512;
 #ifndef RQ_K64_BM128_BELOW
 #define RQ_K64_BM128_BELOW 200  // qmm_t_k64: 128-row tiles when 256-row ones number fewer
 #endif
+#ifndef RQ_K64_BM64_BELOW
+#define RQ_K64_BM64_BELOW 128  // qmm_t_k64, 4 bits: 64 x 96 tiles when 128-row ones number fewer
+#endif
 #ifndef RQ_K64_CPRIO
 #define RQ_K64_CPRIO 0  // qmm_t_k64: wave priority of the MFMA waves (0-3)
 #endif
@@ -1004,7 +1007,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, void* __restrict__ y,
     int y_dt, int tiles_m, int tiles_n, rq::LoraArgs lora) {
-    static_assert(BM == 256 || BM == 128, "block rows");
+    static_assert(BM == 256 || BM == 128 || BM == 64, "block rows");
     constexpr int WN = BN / 2;
     constexpr int TM = BM / 32, TN = WN / 16;   // 16x16 MFMA tiles per wave (2x2 waves)
     constexpr int XL = BM / 32;                 // activation loads per producer lane per stage
@@ -1032,7 +1035,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     const int nper = (nst + P - 1) / P;
 
     constexpr int SW = 2 * BITS;                              // packed words per row per stage
-    constexpr int JW = (BITS == 4 && BN == 160) ? 1 : BITS;   // words per dequant job
+    constexpr int JW = (BITS == 4 && (BN == 160 || BN == 96)) ? 1 : BITS;  // words per dequant job
     constexpr int JPR = SW / JW;                              // jobs per row per stage
     constexpr int NJ = BN * JPR / 256;                        // jobs per producer thread
     constexpr int JC = 32 * JW / BITS;                        // codes per job
@@ -1227,7 +1230,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                     for (int a = 0; a < TM; ++a) {
                         const int q = h * TM + a + 2;   // the (h, a) index read now
                         if (q < 2 * TM) af[q % 3] = rdA(q / TM, q % TM);
-                        if (h == 0 && a == 2) {
+                        if (h == 0 && a == (TM > 2 ? 2 : TM - 1)) {
 #pragma unroll
                             for (int b = 0; b < TN; ++b) bf[1][b] = rdB(1, b);
                         }
@@ -1500,7 +1503,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                     for (int a = 0; a < TM; ++a) {
                         const int q = h * TM + a + 2;
                         if (q < 2 * TM) af[q % 3] = rdA(q / TM, q % TM);
-                        if (h == 0 && a == 2) {
+                        if (h == 0 && a == (TM > 2 ? 2 : TM - 1)) {
 #pragma unroll
                             for (int b = 0; b < TN; ++b) bf[1][b] = rdB(1, b);
                         }
@@ -1540,10 +1543,17 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
         (cols / gs) % 8 == 0 && (((uintptr_t)scales | (uintptr_t)biases) & 15) == 0) {
         // 160-row tiles (whole rounds over 256 CUs for the 2560-wide RWKV-7 shapes) split
         // evenly into 8-code dequant jobs only at 4 bits
-        const int bn = (RQ_BITS == 4 && rows % 160 == 0) ? 160 : 128;
-        const int tn = (int)((rows + bn - 1) / bn);
+        int bn = (RQ_BITS == 4 && rows % 160 == 0) ? 160 : 128;
+        int tn = (int)((rows + bn - 1) / bn);
         // 128-row tiles when 256-row ones leave most CUs idle (small M, narrow R)
-        const int bm = ((m + 255) / 256) * tn < RQ_K64_BM128_BELOW ? 128 : 256;
+        int bm = ((m + 255) / 256) * tn < RQ_K64_BM128_BELOW ? 128 : 256;
+        // and at 4 bits 64 x 96 tiles when 128-row ones still leave half of them idle
+        // (M = 512 with 2560 outputs: 216 tiles instead of 64)
+        if (RQ_BITS == 4 && bm == 128 && ((m + 127) / 128) * tn < RQ_K64_BM64_BELOW) {
+            bm = 64;
+            bn = 96;
+            tn = (int)((rows + bn - 1) / bn);
+        }
         const int tm = (int)((m + bm - 1) / bm);
         const int blocks = ((tm * tn + 7) / 8) * 8;
 #define RQ_K64_BM(SD, BNV, GSHV, BMV)                                                             \
@@ -1559,11 +1569,20 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
         default: RQ_K64(SD, BNV, 7); break;                                                       \
     }
 #if RQ_BITS == 4
-        if (sb_dt == RQ_BF16) {
+#define RQ_K64_SMALL(SD)                                                                          \
+    switch (gs_shift) {                                                                           \
+        case 5: RQ_K64_BM(SD, 96, 5, 64); break;                                                  \
+        case 6: RQ_K64_BM(SD, 96, 6, 64); break;                                                  \
+        default: RQ_K64_BM(SD, 96, 7, 64); break;                                                 \
+    }
+        if (bm == 64) {
+            if (sb_dt == RQ_BF16) { RQ_K64_SMALL(RQ_BF16) } else { RQ_K64_SMALL(RQ_F16) }
+        } else if (sb_dt == RQ_BF16) {
             if (bn == 160) { RQ_K64_GS(RQ_BF16, 160) } else { RQ_K64_GS(RQ_BF16, 128) }
         } else {
             if (bn == 160) { RQ_K64_GS(RQ_F16, 160) } else { RQ_K64_GS(RQ_F16, 128) }
         }
+#undef RQ_K64_SMALL
 #else
         if (sb_dt == RQ_BF16) { RQ_K64_GS(RQ_BF16, 128) } else { RQ_K64_GS(RQ_F16, 128) }
 #endif

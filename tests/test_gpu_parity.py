@@ -378,8 +378,9 @@ def test_config3_prefill_full_size(rq, dev, shape, M):
     """2.9B prefill shapes at full size.  The oracle is too slow here, so the
     reference is an fp32 matmul of the dequantized weights (dequantize is
     bit-exact to the oracle) -- a size-independent consistency check.  The
-    2560-wide shapes at M <= 2048 run 128-row tiles, the rest 256-row ones;
-    M = 2000 / 4000 end in a partial tile of each."""
+    2560-wide shapes run 64 x 96 tiles at M = 512 (the last column tile
+    partial: 2560 = 26 * 96 + 64), 128-row tiles at M = 2000 / 2048, and
+    256-row ones above; M = 2000 / 4000 end in a partial row tile."""
     R, K = shape
     say(f"config3 {shape} M={M}")
     w = weights(R, K, 3_000_000 + R).to(dev)
