@@ -11,7 +11,8 @@ a single launch over the 145 independent GEMVs.  `value` = effective weight-stre
 inputs resident in HBM.
 
 Alongside: the same sweep at M=8, one GEMV launch per projection (eagerly, and
-replayed from one HIP graph), the prefill
+replayed from one HIP graph), config 1 (0.1B FFN key: quantize, dequantize,
+GEMV at M=1/16 as single calls), the prefill
 GEMM (RWKV-7 2.9B shapes, M=4096/2048/512) and its
 transposed product in TFLOP/s, the QLoRA dX product at config-4 shapes, the
 config-5 mixed-bit model (7.2B shapes, 3-bit layers + 8-bit head: decode
@@ -217,6 +218,28 @@ def make_sweep(rq, torch, dev, M, bits=4, gs=64):
             x = torch.randn(M, K, generator=gx, device=dev).to(torch.bfloat16)
             probs.append((name, x, (wq, s, b)))
     return probs, (qgbs, dgbs)
+
+
+def config1(torch, rq, dev, args):
+    """BASELINE config 1 (RWKV-7 0.1B FFN key, W [3072, 768], 4-bit g64): the
+    quantize -> dequantize round trip and y = x . W^T at M = 1 and 16, each
+    timed as back-to-back single calls (launch-latency-bound at this size:
+    1.3 MB of packed weights)."""
+    R, K, gs, bits = 3072, 768, 64, 4
+    g = torch.Generator(device=dev).manual_seed(1_000_004)
+    w = (torch.randn(R, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    wq, s, b = rq.quantize(w, gs, bits)
+    out = {}
+    n = max(20, args.steps)
+    out["quantize_us"] = round(time_region(torch, lambda: rq.quantize(w, gs, bits), n, 10) * 1e6, 2)
+    out["dequantize_us"] = round(time_region(torch, lambda: rq.dequantize(wq, s, b, gs, bits), n, 10) * 1e6, 2)
+    for M in (1, 16):
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        bq = rq.BoundQmm(x, wq, s, b, True, gs, bits)
+        t = time_region(torch, bq.run, n, 10)
+        out[f"qmm_m{M}_us"] = round(t * 1e6, 2)
+        out[f"qmm_m{M}_weight_gbs"] = round(weight_bytes(R, K, bits, gs) / t / 1e9, 1)
+    return out
 
 
 def config5(torch, rq, dev, args):
@@ -526,6 +549,7 @@ def main():
         extra["qlora_dx_m4096_tflops"] = bwd
         extra["qlora_step_config4"] = qlora_step(torch, rwkvq, dev, ws, args)
         del ws, xs, xs8, outs8, plan8, singles
+        extra["config1_ffn_key_0.1b"] = config1(torch, rwkvq, dev, args)
         extra["config5_mixed_bit"] = config5(torch, rwkvq, dev, args)
         result["extra"] = extra
 

@@ -76,8 +76,44 @@ def _words(w_q: Tensor) -> Tensor:
     return w_q
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream_on(device: torch.device) -> int:
+    """Raw handle of the current stream on `device`.  Read without building a
+    torch.cuda.Stream object: that lookup cost more host time than a small
+    decode kernel runs on the GPU."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(idx)
+    return torch.cuda.current_stream(idx).cuda_stream
+
+
 def _stream(t: Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return _stream_on(t.device)
+
+
+class _DeviceGuard:
+    """torch.cuda.device(idx) that switches only when idx is not current
+    (the common case costs one device query)."""
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, device: torch.device):
+        self.idx = device.index if device.index is not None else torch.cuda.current_device()
+        self.prev = -1
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.idx:
+            self.prev = cur
+            torch.cuda.set_device(self.idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev >= 0:
+            torch.cuda.set_device(self.prev)
+            self.prev = -1
+        return False
 
 
 def _ptr(t: Tensor) -> int:
@@ -96,7 +132,7 @@ def _quantize_op(w: Tensor, group_size: int, bits: int) -> Tuple[Tensor, Tensor,
     wq = torch.empty(*lead, K * bits // 32, dtype=torch.int32, device=w.device)
     s = torch.empty(*lead, K // group_size, dtype=w.dtype, device=w.device)
     b = torch.empty_like(s)
-    with torch.cuda.device(w.device):
+    with _DeviceGuard(w.device):
         rc = lib().rq_quantize(_ptr(w), DTYPE_CODE[w.dtype], R, K, group_size, bits, _ptr(wq),
                                _ptr(s), _ptr(b), _stream(w))
     check(rc, "quantize")
@@ -133,7 +169,7 @@ def _dequantize_op(w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int,
     K = w_q.shape[-1] * 32 // bits
     R = w_q.numel() // w_q.shape[-1] if w_q.shape[-1] else 0
     out = torch.empty(*w_q.shape[:-1], K, dtype=scales.dtype, device=w_q.device)
-    with torch.cuda.device(w_q.device):
+    with _DeviceGuard(w_q.device):
         rc = lib().rq_dequantize(_ptr(w_q), _ptr(scales), _ptr(biases), DTYPE_CODE[scales.dtype],
                                  R, K, group_size, bits, _ptr(out), DTYPE_CODE[out.dtype],
                                  _stream(w_q))
@@ -182,7 +218,7 @@ def _embedding_op(idx: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, grou
     out = torch.empty(*idx.shape, K, dtype=scales.dtype, device=w_q.device)
     if out.numel() == 0:
         return out
-    with torch.cuda.device(w_q.device):
+    with _DeviceGuard(w_q.device):
         rc = lib().rq_embedding(_ptr(flat), flat.numel(), _ptr(w_q), _ptr(scales), _ptr(biases),
                                 DTYPE_CODE[scales.dtype], R, K, group_size, bits, _ptr(out),
                                 DTYPE_CODE[out.dtype], _stream(w_q))
@@ -227,7 +263,7 @@ def _qmm_op(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, transpose: b
     y = torch.empty(*x.shape[:-1], n_out, dtype=out_dtype, device=x.device)
     if y.numel() == 0:
         return y
-    with torch.cuda.device(x.device):
+    with _DeviceGuard(x.device):
         rc = lib().rq_qmm(_ptr(x), DTYPE_CODE[x.dtype], _ptr(w_q), _ptr(scales), _ptr(biases),
                           DTYPE_CODE[scales.dtype], m, R, K, group_size, bits,
                           1 if transpose else 0, _ptr(y), DTYPE_CODE[out_dtype], _stream(x))
@@ -290,7 +326,7 @@ def _qmm_lora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, z: T
     m, rank = x.shape[0], z.shape[1]
     y = torch.empty(m, R if transpose else K, dtype=_promote(x.dtype, scales.dtype),
                     device=x.device)
-    with torch.cuda.device(x.device):
+    with _DeviceGuard(x.device):
         rc = lib().rq_qmm_lora(_ptr(x), DTYPE_CODE[x.dtype], _ptr(w_q), _ptr(scales), _ptr(biases),
                                DTYPE_CODE[scales.dtype], m, R, K, group_size, bits,
                                1 if transpose else 0, _ptr(z), _ptr(lora), rank, float(scale),
@@ -371,12 +407,14 @@ class BoundQmm:
                       biases.data_ptr(), DTYPE_CODE[scales.dtype], m, R, K, group_size, bits,
                       1 if transpose else 0, y.data_ptr(), DTYPE_CODE[ydt])
         self._empty = y.numel() == 0
+        self._guard, self._fn = _DeviceGuard(self.device), lib().rq_qmm
 
     def run(self) -> Tensor:
         if not self._empty:
-            with torch.cuda.device(self.device):
-                rc = lib().rq_qmm(*self._args, torch.cuda.current_stream(self.device).cuda_stream)
-            check(rc, "quantized_matmul")
+            with self._guard:
+                rc = self._fn(*self._args, _stream_on(self.device))
+            if rc:
+                check(rc, "quantized_matmul")
         return self.out
 
 
@@ -439,24 +477,26 @@ class GroupedQmv:
         check(nbytes if nbytes < 0 else 0, "grouped_qmv plan")
         table = torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=self.device)
         plan = RqGroupedPlan()
-        with torch.cuda.device(self.device):
+        with _DeviceGuard(self.device):
             rc = L.rq_grouped_plan_init(self.probs, self.n, *self.codes, self.m, group_size, bits,
                                         table.data_ptr(), table.numel(), ctypes.byref(plan),
-                                        torch.cuda.current_stream(self.device).cuda_stream)
+                                        _stream_on(self.device))
         if rc == RQ_EUNSUPPORTED and not planned:
             return
         check(rc, "grouped_qmv plan")
         self.plan, self._table = plan, table
+        self._plan_ref = ctypes.byref(self.plan)
 
     def run(self) -> List[Tensor]:
-        with torch.cuda.device(self.device):
-            stream = torch.cuda.current_stream(self.device).cuda_stream
+        with _DeviceGuard(self.device):
+            stream = _stream_on(self.device)
             if self.plan is not None:
-                rc = lib().rq_grouped_plan_run(ctypes.byref(self.plan), stream)
+                rc = lib().rq_grouped_plan_run(self._plan_ref, stream)
             else:
                 rc = lib().rq_qmm_grouped(self.probs, self.n, *self.codes, self.m,
                                           self.group_size, self.bits, stream)
-        check(rc, "grouped_qmv")
+        if rc:
+            check(rc, "grouped_qmv")
         return self.outs
 
 
@@ -478,7 +518,7 @@ def _pack_op(codes: Tensor, bits: int) -> Tensor:
     K = codes.shape[-1]
     R = codes.numel() // K if K else 0
     wq = torch.empty(*codes.shape[:-1], K * bits // 32, dtype=torch.int32, device=codes.device)
-    with torch.cuda.device(codes.device):
+    with _DeviceGuard(codes.device):
         rc = lib().rq_pack(_ptr(codes), R, K, bits, _ptr(wq), _stream(codes))
     check(rc, "pack_codes")
     return wq
@@ -496,7 +536,7 @@ def _unpack_op(w_q: Tensor, bits: int) -> Tensor:
     K = w_q.shape[-1] * 32 // bits
     R = w_q.numel() // w_q.shape[-1] if w_q.shape[-1] else 0
     codes = torch.empty(*w_q.shape[:-1], K, dtype=torch.uint8, device=w_q.device)
-    with torch.cuda.device(w_q.device):
+    with _DeviceGuard(w_q.device):
         rc = lib().rq_unpack(_ptr(w_q), R, K, bits, _ptr(codes), _stream(w_q))
     check(rc, "unpack_codes")
     return codes

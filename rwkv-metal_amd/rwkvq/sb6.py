@@ -28,6 +28,7 @@ import torch
 from torch import Tensor, nn
 
 from . import ops
+from .ops import _DeviceGuard, _stream_on
 from ._lib import DTYPE_CODE, check, lib
 from .lora import TMIX_TARGETS, LoRALinear, _param_stats, _unfreeze_adapters
 
@@ -75,10 +76,10 @@ def _to_affine(lin: "RwkvqLinear", codes: bool = True):
     wq = torch.empty(OUT, NB * bits, dtype=torch.int32, device=dev) if codes else None
     sc = torch.empty(OUT, NB, dtype=torch.float32, device=dev)
     bi = torch.empty_like(sc)
-    with torch.cuda.device(dev):
+    with _DeviceGuard(dev):
         rc = lib().rq_sb6_to_affine(*_sb6_args(lin), _dev_ptr(wq) if codes else None,
                                     _dev_ptr(sc), _dev_ptr(bi),
-                                    torch.cuda.current_stream(dev).cuda_stream)
+                                    _stream_on(dev))
     check(rc, "sb6_to_affine")
     return wq, sc, bi
 
@@ -115,9 +116,9 @@ class RwkvqLinear(nn.Module):
         ops._on_gpu(self.qblk)
         dev = self.qblk.device
         out = torch.empty(self.out_features, self.in_features, dtype=dtype, device=dev)
-        with torch.cuda.device(dev):
+        with _DeviceGuard(dev):
             rc = lib().rq_sb6_dequantize(*_sb6_args(self), _dev_ptr(out), DTYPE_CODE[dtype],
-                                         torch.cuda.current_stream(dev).cuda_stream)
+                                         _stream_on(dev))
         check(rc, "sb6_dequantize")
         return out
 
