@@ -1289,8 +1289,11 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
     __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * BLD];
     __shared__ __attribute__((aligned(16))) uint32_t cs0[64 * CW];
     __shared__ __attribute__((aligned(16))) uint32_t cs1[64 * CW];
-    __shared__ __attribute__((aligned(16))) uint16_t ss0[2 * 64 * 4];  // [scale|bias][row][<=4 groups]
-    __shared__ __attribute__((aligned(16))) uint16_t ss1[2 * 64 * 4];
+    // fp32 (scale, bias) pairs [row][<=4 groups][2]: one 8-byte read per row in
+    // the dequantization (16-bit values read and converted separately cost
+    // twice the LDS reads there; the producers bound this kernel)
+    __shared__ __attribute__((aligned(16))) float ss0[64 * 4 * 2];
+    __shared__ __attribute__((aligned(16))) float ss1[64 * 4 * 2];
 
     const int ntiles = tiles_m * tiles_n;
     const int per_xcd = (ntiles + 7) / 8;
@@ -1322,13 +1325,14 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
         const uint8_t* xbase = (const uint8_t*)(x + m0 * R);
         // code chunks: chunk c = pt + 256 j -> weight row c / CCH, 16-byte chunk c % CCH
         const uint32_t* wtile = wq + (k0 >> 5) * BITS;
-        // (scale, bias): thread pt < 128 loads row pt/2's ng values of array pt%2
-        const int srow = pt >> 1, sarr = pt & 1;
-        const uint16_t* sbsrc = (const uint16_t*)(sarr ? biases : scales) + g_first;
+        // (scale, bias): thread pt < 64 loads row pt's ng values of both arrays
+        const int srow = pt;
+        const uint16_t* ssrc = (const uint16_t*)scales + g_first;
+        const uint16_t* bsrc = (const uint16_t*)biases + g_first;
 
         u32x4_t xv[2][8];
         u32x4_t cv[2][NCL];
-        uint32_t sv[2][2];
+        uint32_t sv[2][4];  // raw: scales words 0-1, biases words 2-3
         auto load_x = [&](int st, int r) {
             const int sc = st < nst ? st : nst - 1;
             const uint8_t* xb = xbase + (int64_t)sc * 128;
@@ -1345,34 +1349,43 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                     cv[r][j] = *(gv_t)(wtile + row * wpr + (c % CCH) * 4);
                 }
             }
-            if (pt < 128) {
+            if (pt < 64) {
                 const int64_t row = (int64_t)sc * 64 + srow;
-                const uint16_t* src = sbsrc + row * G;
-                if (ng == 4) {
-                    const uint2 v = *(const uint2*)src;
-                    sv[r][0] = v.x; sv[r][1] = v.y;
-                } else if (ng == 2) {
-                    sv[r][0] = *(const uint32_t*)src; sv[r][1] = 0u;
-                } else {
-                    sv[r][0] = *src; sv[r][1] = 0u;
+#pragma unroll
+                for (int a = 0; a < 2; ++a) {
+                    const uint16_t* src = (a ? bsrc : ssrc) + row * G;
+                    if (ng == 4) {
+                        const uint2 v = *(const uint2*)src;
+                        sv[r][2 * a] = v.x; sv[r][2 * a + 1] = v.y;
+                    } else if (ng == 2) {
+                        sv[r][2 * a] = *(const uint32_t*)src; sv[r][2 * a + 1] = 0u;
+                    } else {
+                        sv[r][2 * a] = *src; sv[r][2 * a + 1] = 0u;
+                    }
                 }
             }
         };
-        auto put_c = [&](int r, uint32_t* cs, uint16_t* ss) {
+        auto put_c = [&](int r, uint32_t* cs, float* ss) {
 #pragma unroll
             for (int j = 0; j < NCL; ++j) {
                 const int c = pt + 256 * j;
                 if (c < 64 * CCH) *(u32x4_t*)(cs + (c / CCH) * CW + (c % CCH) * 4) = cv[r][j];
             }
-            if (pt < 128) {
-                uint32_t* d = (uint32_t*)(ss + sarr * 256 + srow * 4);
-                d[0] = sv[r][0];
-                d[1] = sv[r][1];
+            if (pt < 64) {
+                typedef float f32x2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const uint32_t sw = sv[r][g >> 1], bw = sv[r][2 + (g >> 1)];
+                    const int sh = 16 * (g & 1);
+                    *(f32x2_t*)(ss + (srow * 4 + g) * 2) =
+                        f32x2_t{dt_traits<SDT>::to_f32((uint16_t)(sw >> sh)),
+                                dt_traits<SDT>::to_f32((uint16_t)(bw >> sh))};
+                }
             }
         };
         // dequantization unit: rows 4*rq .. 4*rq+3, columns 8*kc .. 8*kc+7
         const int rq = pt & 15, kc = pt >> 4;
-        auto dequant = [&](const uint32_t* cs, const uint16_t* ss, uint16_t* bq) {
+        auto dequant = [&](const uint32_t* cs, const float* ss, uint16_t* bq) {
             const int gl = (kc * 8) >> gs_shift;  // group of these columns within the tile
             float v[4][8];
 #pragma unroll
@@ -1382,8 +1395,9 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                 const uint32_t* wr = cs + row * CW + (bit >> 5);
                 const uint64_t win = (uint64_t)wr[0] | ((bit & 31) + 8 * BITS > 32 ? (uint64_t)wr[1] << 32 : 0ull);
                 const int off = bit & 31;
-                const float sf = dt_traits<SDT>::to_f32(ss[row * 4 + gl]);
-                const float bf = dt_traits<SDT>::to_f32(ss[256 + row * 4 + gl]);
+                typedef float f32x2_t __attribute__((ext_vector_type(2)));
+                const f32x2_t sbv = *(const f32x2_t*)(ss + (row * 4 + gl) * 2);
+                const float sf = sbv[0], bf = sbv[1];
                 float cf[8];
                 if constexpr (BITS == 4) {
                     // one word = the 8 codes; byte converts on the nibble halves
