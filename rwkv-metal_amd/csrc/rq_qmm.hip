@@ -1281,17 +1281,21 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
     constexpr int BLD = 72;                 // bf16 tile row stride (64 + 8 elements)
     constexpr int CW = BN * BITS / 32;      // packed words per weight row per stage
     constexpr int CCH = CW / 4;             // 16-byte chunks per row (BITS of them)
+    // LDS row stride of the code tile: odd, so that the 16 row quads a
+    // dequantization read spans (rows 4q + i) fall in 16 different banks (a
+    // stride of CW words put all 16 in one bank)
+    constexpr int CWP = CW + 1;
     constexpr int NCL = (64 * CCH + 255) / 256;  // code chunks per producer thread
     static_assert(SDT != RQ_F32, "16-bit scales");
     __shared__ __attribute__((aligned(16))) uint8_t xs0[BM * 128];
     __shared__ __attribute__((aligned(16))) uint8_t xs1[BM * 128];
     __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * BLD];
     __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * BLD];
-    __shared__ __attribute__((aligned(16))) uint32_t cs0[64 * CW];
-    __shared__ __attribute__((aligned(16))) uint32_t cs1[64 * CW];
-    // fp32 (scale, bias) pairs [row][<=4 groups][2]: one 8-byte read per row in
-    // the dequantization (16-bit values read and converted separately cost
-    // twice the LDS reads there; the producers bound this kernel)
+    __shared__ __attribute__((aligned(16))) uint32_t cs0[64 * CWP];
+    __shared__ __attribute__((aligned(16))) uint32_t cs1[64 * CWP];
+    // fp32 (scale, bias) pairs [group][row % 4][row / 4][2]: one 8-byte read
+    // per row in the dequantization, the 16 row quads of a read in
+    // consecutive pairs
     __shared__ __attribute__((aligned(16))) float ss0[64 * 4 * 2];
     __shared__ __attribute__((aligned(16))) float ss1[64 * 4 * 2];
 
@@ -1369,7 +1373,10 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
 #pragma unroll
             for (int j = 0; j < NCL; ++j) {
                 const int c = pt + 256 * j;
-                if (c < 64 * CCH) *(u32x4_t*)(cs + (c / CCH) * CW + (c % CCH) * 4) = cv[r][j];
+                if (c < 64 * CCH) {
+                    uint32_t* d = cs + (c / CCH) * CWP + (c % CCH) * 4;
+                    d[0] = cv[r][j][0]; d[1] = cv[r][j][1]; d[2] = cv[r][j][2]; d[3] = cv[r][j][3];
+                }
             }
             if (pt < 64) {
                 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -1377,7 +1384,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                 for (int g = 0; g < 4; ++g) {
                     const uint32_t sw = sv[r][g >> 1], bw = sv[r][2 + (g >> 1)];
                     const int sh = 16 * (g & 1);
-                    *(f32x2_t*)(ss + (srow * 4 + g) * 2) =
+                    *(f32x2_t*)(ss + ((g * 4 + (srow & 3)) * 16 + (srow >> 2)) * 2) =
                         f32x2_t{dt_traits<SDT>::to_f32((uint16_t)(sw >> sh)),
                                 dt_traits<SDT>::to_f32((uint16_t)(bw >> sh))};
                 }
@@ -1392,11 +1399,11 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
             for (int i = 0; i < 4; ++i) {
                 const int row = rq * 4 + i;
                 const int bit = kc * 8 * BITS;
-                const uint32_t* wr = cs + row * CW + (bit >> 5);
+                const uint32_t* wr = cs + row * CWP + (bit >> 5);
                 const uint64_t win = (uint64_t)wr[0] | ((bit & 31) + 8 * BITS > 32 ? (uint64_t)wr[1] << 32 : 0ull);
                 const int off = bit & 31;
                 typedef float f32x2_t __attribute__((ext_vector_type(2)));
-                const f32x2_t sbv = *(const f32x2_t*)(ss + (row * 4 + gl) * 2);
+                const f32x2_t sbv = *(const f32x2_t*)(ss + ((gl * 4 + i) * 16 + rq) * 2);
                 const float sf = sbv[0], bf = sbv[1];
                 float cf[8];
                 if constexpr (BITS == 4) {
