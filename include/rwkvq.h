@@ -23,6 +23,7 @@
  *   rq_qmm_lora    <- LoRALinear.__call__ over a quantized base (rwkv_metal/lora/lora.py:58-63)
  *                     and its dX (finetune.py:141): the low-rank term fused into rq_qmm's
  *                     output stage
+ *   rq_lora_down   <- its x . A^T and the backward's dY . B (the same lines)
  *   rq_sb6_dequantize / rq_sb6_to_affine
  *                  <- the .rwkvq (rwkv-quant sb6) base: RwkvqLinear's fused dequant
  *                     (rwkv_metal/lora/rwkvq_kernel.py) and RwkvqNativeLinear's repack into
@@ -138,6 +139,14 @@ int rq_sb6_dequantize(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* 
 int rq_sb6_to_affine(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, int64_t rows,
                      int64_t cols, int gw_gs, int gw_sb, int xbits, uint32_t* w_q, float* scales,
                      float* biases, void* stream);
+
+/* The QLoRA layer's low-rank down-projection: z[m, rank] = x[m, k] . a[rank, k]^T,
+ * bf16 in and out, fp32 accumulation; rank 16, 32, 48 or 64; k a multiple of 32;
+ * x and a 16-byte aligned.  LoRALinear.__call__ (rwkv_metal/lora/lora.py:58-63)
+ * computes z = x . A^T in the forward; MLX autograd computes u = dY . B in the
+ * backward (a = B^T, [rank, out_features]).  Replaces those two mx.matmul nodes. */
+int rq_lora_down(const void* x, int64_t m, int64_t k, const void* a, int64_t rank, void* z,
+                 void* stream);
 
 /* The QLoRA layer over a quantized base (LoRALinear.__call__,
  * rwkv_metal/lora/lora.py:58-63: base(x) + scale * (x A^T) B^T) with the

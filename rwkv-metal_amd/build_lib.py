@@ -38,6 +38,7 @@ FLAGS = [
 
 def _units():
     units = [("rq_quant.hip", [], "rq_quant.o"), ("rq_sb6.hip", [], "rq_sb6.o"),
+             ("rq_lora.hip", [], "rq_lora.o"),
              ("rq_abi.cpp", ["-x", "hip"], "rq_abi.o")]
     for b in BITS:
         # MFMA results straight into VGPRs: the GEMV consumes every MFMA

@@ -267,6 +267,20 @@ int rq_qmm(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales
     return launch_status(e, "rq_qmm");
 }
 
+int rq_lora_down(const void* x, int64_t m, int64_t k, const void* a, int64_t rank, void* z,
+                 void* stream) {
+    if (m < 0 || k < 0) return fail(RQ_EINVAL, "rq_lora_down: negative size");
+    if (rank < 16 || rank > 64 || rank % 16)
+        return fail(RQ_EINVAL, "rq_lora_down: rank must be 16, 32, 48 or 64 (got %lld)", (long long)rank);
+    if (k % 32) return fail(RQ_EINVAL, "rq_lora_down: k must be a multiple of 32 (got %lld)", (long long)k);
+    if (m == 0) return ok();
+    if (k == 0) return fail(RQ_EINVAL, "rq_lora_down: empty contraction is not supported");
+    if (!x || !a || !z) return fail(RQ_EINVAL, "rq_lora_down: NULL pointer");
+    if (!aligned16(x) || !aligned16(a)) return fail(RQ_EALIGN, "rq_lora_down: x and a must be 16-byte aligned");
+    return launch_status(rq::launch_lora_down(x, m, k, a, (int)rank, z, (hipStream_t)stream),
+                         "rq_lora_down");
+}
+
 int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
                 const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
                 int group_size, int bits, int transpose, const void* z, const void* lora,

@@ -68,6 +68,11 @@ struct LoraArgs {
     float scale;
 };
 
+// Low-rank down-projection z[m, rank] = x[m, k] . a[rank, k]^T, bf16 (rank
+// 16, 32, 48 or 64; k a multiple of 32).
+hipError_t launch_lora_down(const void* x, int64_t m, int64_t k, const void* a, int rank, void* z,
+                            hipStream_t stream);
+
 // MFMA GEMM, transpose=True: y[m, rows] = x[m, cols] . W^T.
 hipError_t launch_qmm_t(const void* x, int x_dt, const uint32_t* wq, const void* scales,
                         const void* biases, int sb_dt, int64_t m, int64_t rows, int64_t cols,

@@ -53,6 +53,7 @@ SIGNATURES = {
                _i32),
     "rq_qmm_lora": ([_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _vp,
                      _i64, ctypes.c_float, _vp, _i32, _vp], _i32),
+    "rq_lora_down": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp], _i32),
     "rq_embedding": ([_vp, _i64, _vp, _vp, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _i32, _vp],
                      _i32),
     "rq_sb6_dequantize": ([_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _i32, _vp], _i32),

@@ -52,7 +52,7 @@ class _QLoRAFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x2, lora_a, lora_b, base, scale):
-        z = x2 @ lora_a.t()
+        z = ops.lora_down(x2, lora_a)
         y = ops.quantized_matmul_lora(x2, base.weight, base.scales, base.biases, z, lora_b, scale,
                                       True, base.group_size, base.bits)
         ctx.save_for_backward(x2, z, lora_a, lora_b)
@@ -64,7 +64,7 @@ class _QLoRAFunction(torch.autograd.Function):
         x2, z, lora_a, lora_b = ctx.saved_tensors
         base, scale = ctx.base, ctx.scale
         dy = dy.contiguous().to(x2.dtype)
-        u = dy @ lora_b
+        u = ops.lora_down(dy, lora_b.t().contiguous())
         dx = da = db = None
         if ctx.needs_input_grad[0]:
             dx = ops.quantized_matmul_lora(dy, base.weight, base.scales, base.biases, u,

@@ -315,6 +315,30 @@ def quantized_matmul(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor,
     return _qmm_op(x, w_q, scales, biases, bool(transpose), group_size, bits)
 
 
+def lora_down(x: Tensor, a: Tensor) -> Tensor:
+    """x @ a^T for the QLoRA layer's low-rank products (rank = a.shape[0]):
+    z = x A^T in the forward, u = dY B (a = B^T) in the backward
+    (rwkv_metal/lora/lora.py:58-63).  bf16 CUDA operands with a rank of 16,
+    32, 48 or 64 and an inner size that is a multiple of 32 run rq_lora_down
+    (one HIP launch); other operands take torch's matmul."""
+    if x.shape[-1] != a.shape[-1]:
+        raise ValueError(f"lora_down: x has inner size {x.shape[-1]}, a has {a.shape[-1]}")
+    rank, k = a.shape[0], a.shape[-1]
+    if not (x.is_cuda and x.dtype == a.dtype == torch.bfloat16 and rank in (16, 32, 48, 64)
+            and k % 32 == 0 and k > 0):
+        return x @ a.t()
+    x2 = _ready(x.reshape(-1, k))
+    a = _ready(a)
+    z = torch.empty(x2.shape[0], rank, dtype=torch.bfloat16, device=x.device)
+    if x2.shape[0]:
+        with _DeviceGuard(x.device):
+            rc = lib().rq_lora_down(_ptr(x2), x2.shape[0], k, _ptr(a), rank, _ptr(z),
+                                    _stream_on(x.device))
+        if rc:
+            check(rc, "lora_down")
+    return z.reshape(*x.shape[:-1], rank)
+
+
 def _qmm_lora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, z: Tensor,
                     lora: Tensor, scale: float, transpose: bool, group_size: int, bits: int):
     """rq_qmm_lora on 2-D operands; None where the fused kernels do not apply."""

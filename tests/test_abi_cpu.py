@@ -28,7 +28,7 @@ def test_header_declares_the_expected_surface():
         "rq_abi_version", "rq_last_error", "rq_quantize", "rq_dequantize", "rq_qmm",
         "rq_pack", "rq_unpack", "rq_qmm_grouped", "rq_grouped_plan_table_bytes",
         "rq_grouped_plan_init", "rq_grouped_plan_run", "rq_embedding", "rq_sb6_dequantize",
-        "rq_sb6_to_affine", "rq_qmm_lora"])
+        "rq_sb6_to_affine", "rq_qmm_lora", "rq_lora_down"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -73,6 +73,13 @@ def test_invalid_arguments_return_einval(L):
     assert "rank" in _err(L)
     assert L.rq_qmm_lora(p, 0, p, p, p, 0, 300, 64, 64, 64, 4, 1, 0, p, 16, 1.0, p, 0, None) == -1
     assert L.rq_qmm_lora(p, 0, p, p, p, 0, 300, 64, 64, 64, 4, 1, p + 8, p, 16, 1.0, p, 0, None) == -2
+    assert L.rq_lora_down(p, 64, 64, p, 8, p, None) == -1
+    assert "rank" in _err(L)
+    assert L.rq_lora_down(p, 64, 48, p, 16, p, None) == -1
+    assert "multiple of 32" in _err(L)
+    assert L.rq_lora_down(p, 64, 64, 0, 16, p, None) == -1
+    assert L.rq_lora_down(p + 8, 64, 64, p, 16, p, None) == -2
+    assert L.rq_lora_down(p, 0, 64, p, 16, p, None) == 0  # nothing to do
 
 
 def test_misaligned_pointers_return_ealign(L):

@@ -625,6 +625,22 @@ def test_decode_launches_in_a_hip_graph(O, rq, dev, M):
             rel_check(outs[i], ref, what=f"graph replay {rep} problem {i}")
 
 
+@pytest.mark.parametrize("rank", [16, 32, 48, 64])
+def test_lora_down_matches_fp32(rq, dev, rank):
+    """rq_lora_down (z = x . a^T, the QLoRA layer's rank products) against an
+    fp32 product of the same bf16 operands: rows ending mid-tile, contractions
+    of one k-step to 256, a wave's k-steps past the end (K = 96)."""
+    for M, K in [(1, 32), (17, 96), (300, 2048), (4096, 2048), (513, 8192)]:
+        g = torch.Generator().manual_seed(M * 7 + K + rank)
+        x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+        a = (torch.randn(rank, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+        say(f"lora_down M={M} K={K} rank={rank}")
+        z = rq.lora_down(x.to(dev), a.to(dev))
+        assert z.dtype == torch.bfloat16 and tuple(z.shape) == (M, rank)
+        ref = x.float() @ a.float().t()
+        rel_check(z, ref, what=f"lora_down {M}x{K} r{rank}")
+
+
 # ---------------------------------------------- autograd / modules / LoRA
 
 def test_autograd_dx_is_transposed_qmm(O, rq, dev):
