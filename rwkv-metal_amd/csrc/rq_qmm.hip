@@ -990,7 +990,9 @@ RQ_DEV void lora_epilogue(f32x4_t (&acc)[TM][TN], const rq::LoraArgs& lo, int64_
 // (2x2, wave tile 128 x BN/2, two k-steps of 32 per stage); waves 4-7 keep
 // D stages of loads in flight in registers, write the activations to a
 // 2-slot LDS ring (16-byte chunks XOR-swizzled by row) and dequantize the
-// stage's codes straight from registers into a 2-slot bf16 ring.  One
+// stage's codes straight from registers into a 2-slot bf16 ring (128-byte
+// rows, the same chunk swizzle; a padded 144-byte row measured 1-6 %
+// slower).  One
 // barrier per stage.
 //  * A wave64 VALU op costs ~6-8 cycles and runs beside the MFMA wave on
 //    the same SIMD, so the dequantization is split evenly over all 256
@@ -1011,7 +1013,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     constexpr int WN = BN / 2;
     constexpr int TM = BM / 32, TN = WN / 16;   // 16x16 MFMA tiles per wave (2x2 waves)
     constexpr int XL = BM / 32;                 // activation loads per producer lane per stage
-    constexpr int BLD = 72;                  // bf16 ring row stride (64 + 8 elements)
+    constexpr int BLD = 64;                  // bf16 ring row: 8 chunks of 16 B, XOR-swizzled by row & 7
     constexpr int D = RQ_K64_DEPTH;          // stages of loads in flight per producer thread
     constexpr int P = (8 << GSH) / 64;       // stages per 8-group (scale, bias) chunk: 4, 8, 16
     static_assert(P % D == 0, "the register ring index is the unrolled stage index mod D");
@@ -1060,13 +1062,14 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
         const uint8_t* xbase = (const uint8_t*)(x + m0 * K);
         // dequant jobs: job j = pt + 256 i is part j % JPR (JW words) of tile row j / JPR
         const uint32_t* wtile = wq + n0 * wpr;
-        uint32_t coff[NJ], qoff[NJ], soff[NJ];
+        uint32_t coff[NJ], qoff[NJ], soff[NJ], qc0[NJ];
 #pragma unroll
         for (int i = 0; i < NJ; ++i) {
             const int j = pt + 256 * i, row = j / JPR, part = j % JPR;
             const int rr = n0 + row < R ? row : (int)(R - 1 - n0);
             coff[i] = (uint32_t)(rr * wpr + part * JW);
-            qoff[i] = (uint32_t)(row * BLD + part * JC);
+            qoff[i] = (uint32_t)(row * BLD);
+            qc0[i] = (uint32_t)((part * (JC / 8)) | ((row & 7) << 8));  // first chunk, row key
             soff[i] = (uint32_t)(row * 16 + (GSH == 5 ? 2 * ((part * JC) >> 5) : 0));
         }
         // (scale, bias) staging: thread pt < BN converts row pt's 8 groups of a period
@@ -1165,7 +1168,8 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                     u32x4_t* dst = (u32x4_t*)(bq + qoff[i]);
 #pragma unroll
                     for (int q = 0; q < JC / 8; ++q)
-                        dst[q] = u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
+                        dst[((qc0[i] & 0xff) + q) ^ (qc0[i] >> 8)] =
+                            u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
                 }
                 issue(st + D, u % D);
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this stage's LDS writes are done
@@ -1194,7 +1198,12 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
             const int row = wm * (BM / 2) + a * 16 + lr;
             aoff[h][a] = (uint32_t)(row * 128 + (((h * 4 + lg) ^ (row & 7)) * 16));
         }
-    const uint32_t boff = (uint32_t)((wn * WN + lr) * BLD + lg * 8);
+    // B fragment rows wn*WN + 16 b + lr all have key lr & 7 (WN % 8 == 0)
+    static_assert(WN % 8 == 0, "a fragment row's swizzle key is lr & 7");
+    uint32_t boff[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        boff[h] = (uint32_t)((wn * WN + lr) * BLD + (((h * 4 + lg) ^ (lr & 7)) * 8));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();  // the producers' prologue barrier
     asm volatile("" ::: "memory");
@@ -1218,7 +1227,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                     return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
                 };
                 auto rdB = [&](int h, int b) {
-                    return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(bq + boff + b * 16 * BLD + h * 32));
+                    return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(bq + boff[h] + b * 16 * BLD));
                 };
 #pragma unroll
                 for (int b = 0; b < TN; ++b) bf[0][b] = rdB(0, b);
