@@ -170,7 +170,7 @@ def kt_report(d):
         per = {}
         with open(traces[0], newline="") as fh:
             for r in csv.DictReader(fh):
-                if not any(k in r["Kernel_Name"] for k in ("qmv_", "qmm_", "quantize_kernel")):
+                if not any(k in r["Kernel_Name"] for k in ("qmv_", "qmm_", "quantize_kernel", "lora_down")):
                     continue
                 key = (r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0],
                        int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])))

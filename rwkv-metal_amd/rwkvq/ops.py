@@ -48,11 +48,16 @@ def _check_args(group_size: int, bits: int) -> None:
 
 
 def _on_gpu(*ts: Tensor) -> None:
+    """Every operand on the same GPU: the kernels take raw pointers and run on
+    the first operand's device."""
     for t in ts:
         if t.device.type != "cuda":
             raise RuntimeError(
                 "rwkvq ops run only on a ROCm GPU (HIP library); got a tensor on "
                 f"'{t.device}'. There is no CPU implementation.")
+        if t.device != ts[0].device:
+            raise ValueError(f"rwkvq ops take every operand on one device; got '{ts[0].device}' "
+                             f"and '{t.device}'")
 
 
 def _float(t: Tensor, name: str) -> None:
@@ -327,6 +332,7 @@ def lora_down(x: Tensor, a: Tensor) -> Tensor:
     if not (x.is_cuda and x.dtype == a.dtype == torch.bfloat16 and rank in (16, 32, 48, 64)
             and k % 32 == 0 and k > 0):
         return x @ a.t()
+    _on_gpu(x, a)
     x2 = _ready(x.reshape(-1, k))
     a = _ready(a)
     z = torch.empty(x2.shape[0], rank, dtype=torch.bfloat16, device=x.device)
@@ -470,7 +476,7 @@ class GroupedQmv:
         self.probs = (RqProblem * len(xs))()
         self._keep, self.outs = [], []
         for i, (x, (w_q, s, b)) in enumerate(zip(xs, ws)):
-            _on_gpu(x, w_q, s, b)
+            _on_gpu(x0, x, w_q, s, b)
             w_q = _words(w_q)
             K = _check_packed(w_q, s, b, group_size, bits)
             if x.dtype != x0.dtype or s.dtype != sdt or x.numel() // x.shape[-1] != m:

@@ -50,6 +50,17 @@ def test_ops_refuse_cpu_tensors(rq):
         rq.dequantize(wq, s, s, 64, 4)
 
 
+def test_ops_refuse_operands_on_two_devices():
+    from types import SimpleNamespace
+    from rwkvq import ops
+    on = lambda d: SimpleNamespace(device=torch.device(d))  # only .device is read
+    ops._on_gpu(on("cuda:0"), on("cuda:0"))
+    with pytest.raises(ValueError, match="one device"):
+        ops._on_gpu(on("cuda:0"), on("cuda:0"), on("cuda:1"))
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops._on_gpu(on("cuda:0"), on("cpu"))
+
+
 def test_argument_validation(rq):
     w = torch.empty(8, 64, device="meta")
     with pytest.raises(ValueError):
