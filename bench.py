@@ -65,10 +65,13 @@ def parse():
                     help="bounded CPU-baseline sample length")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline sweep only")
-    ap.add_argument("--pmc-workload", action="store_true",
-                    help="run the headline plan 3x then 3 calibration copies, print nothing")
+    ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm"),
+                    help="run the headline plan (gemv) or the config-3 [10240, 2560] prefill "
+                         "GEMM at M=4096 (gemm) 3x, then 3 calibration copies; print nothing")
     ap.add_argument("--pmc-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="reduce two rocprofv3 --pmc csv outputs of --pmc-workload")
+    ap.add_argument("--pmc-kernel", default=None,
+                    help="kernel name the report reduces (default: the workload's own)")
     ap.add_argument("--kt-report", metavar="DIR",
                     help="print rocprofv3 --kernel-trace --stats csv output as a table")
     return ap.parse_args()
@@ -80,14 +83,25 @@ PMC_RUNS, COPY_BYTES, COPY_RUNS = 3, 1 << 30, 3
 HEAD_KERNEL = "qmv_stream_table"
 
 
-def pmc_workload(torch, rq, dev):
-    """What the counter passes profile: the headline plan (one launch) PMC_RUNS
-    times, then COPY_RUNS copies of COPY_BYTES (read COPY_BYTES, write
-    COPY_BYTES) as the last dispatches of the process."""
-    probs, _ = make_sweep(rq, torch, dev, M=1)
-    plan = rq.GroupedQmv([x for _, x, _ in probs], [w for _, _, w in probs], 64, 4)
+GEMM_KERNEL = "qmm_t_k64"
+PMC_GEMM = (4096, 10240, 2560)  # M, R, K: config 3's ffn_key-shaped prefill
+
+
+def pmc_workload(torch, rq, dev, which="gemv"):
+    """What the counter passes profile: the headline plan (one launch), or one
+    config-3 prefill GEMM, PMC_RUNS times, then COPY_RUNS copies of COPY_BYTES
+    (read COPY_BYTES, write COPY_BYTES) as the last dispatches of the process."""
+    if which == "gemm":
+        M, R, K = PMC_GEMM
+        w = (torch.randn(R, K, device=dev) * 0.02).to(torch.bfloat16)
+        run = rq.BoundQmm(torch.randn(M, K, device=dev).to(torch.bfloat16),
+                          *rq.quantize(w, 64, 4), True, 64, 4).run
+    else:
+        probs, _ = make_sweep(rq, torch, dev, M=1)
+        run = rq.GroupedQmv([x for _, x, _ in probs], [w for _, _, w in probs], 64, 4).run
+    torch.cuda.synchronize()
     for _ in range(PMC_RUNS):
-        plan.run()
+        run()
     torch.cuda.synchronize()
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
@@ -116,7 +130,7 @@ def _pmc_rows(d):
     return [(did, *per[did]) for did in sorted(per)]
 
 
-def pmc_report(fetch_dir, write_dir):
+def pmc_report(fetch_dir, write_dir, kernel=HEAD_KERNEL):
     """Print the calibrated HBM traffic of the headline kernel per step and
     per launch.  FETCH_SIZE / WRITE_SIZE are KiB per dispatch; the factor that
     turns them into bytes is COPY_BYTES over what the calibration copies read
@@ -125,9 +139,9 @@ def pmc_report(fetch_dir, write_dir):
     for tag, d in (("fetch", fetch_dir), ("write", write_dir)):
         rows = _pmc_rows(d)
         copies = rows[-COPY_RUNS:]
-        head = [r for r in rows if HEAD_KERNEL in r[1]]
-        if len(head) % PMC_RUNS:
-            raise SystemExit(f"{tag}: {len(head)} {HEAD_KERNEL} dispatches, not a multiple of "
+        head = [r for r in rows if kernel in r[1]]
+        if not head or len(head) % PMC_RUNS:
+            raise SystemExit(f"{tag}: {len(head)} {kernel} dispatches, not a multiple of "
                              f"{PMC_RUNS}")
         copy_kib = sum(r[2] for r in copies) / len(copies)
         factor = COPY_BYTES / copy_kib
@@ -412,7 +426,7 @@ def cpu_baseline(torch, seconds):
 def main():
     args = parse()
     if args.pmc_report:
-        pmc_report(*args.pmc_report)
+        pmc_report(*args.pmc_report, kernel=args.pmc_kernel or HEAD_KERNEL)
         return
     if args.kt_report:
         kt_report(args.kt_report)
@@ -428,7 +442,7 @@ def main():
     torch.cuda.set_device(dev)
     bits, gs = 4, 64
     if args.pmc_workload:
-        pmc_workload(torch, rwkvq, dev)
+        pmc_workload(torch, rwkvq, dev, args.pmc_workload)
         return
 
     # ---------------- headline: config-2 decode sweep, M=1, grouped launches
