@@ -560,6 +560,24 @@ constexpr int kWsBlock = 512;
 #ifndef RQ_K64_CPRIO
 #define RQ_K64_CPRIO 0  // qmm_t_k64: wave priority of the MFMA waves (0-3)
 #endif
+#ifndef RQ_K64_GROUP
+#define RQ_K64_GROUP 2  // qmm_t_k64: row tiles per group of the tile order (1: row-major)
+#endif
+// tile index -> (row tile, column tile): groups of RQ_K64_GROUP row tiles
+// walked column by column (a bijection; the last group may be shorter)
+__device__ __forceinline__ void k64_tile(int t, int tiles_m, int tiles_n, int& mt, int& nt) {
+    constexpr int G = RQ_K64_GROUP;
+    if (G == 1) {
+        mt = t / tiles_n;
+        nt = t % tiles_n;
+        return;
+    }
+    const int group = t / (G * tiles_n), first = group * G;
+    const int gsz = tiles_m - first < G ? tiles_m - first : G;
+    const int r = t - group * G * tiles_n;
+    mt = first + r % gsz;
+    nt = r / gsz;
+}
 #ifndef RQ_GEMM_K64
 #define RQ_GEMM_K64 1  // 1: 64-wide stages with whole-line loads (qmm_t_k64) where they apply
 #endif
@@ -1029,7 +1047,9 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     const int per_xcd = (ntiles + 7) / 8;
     const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
     if (t >= ntiles) return;
-    const int64_t m0 = (int64_t)(t / tiles_n) * BM, n0 = (int64_t)(t % tiles_n) * BN;
+    int mt, nt;
+    k64_tile(t, tiles_m, tiles_n, mt, nt);
+    const int64_t m0 = (int64_t)mt * BM, n0 = (int64_t)nt * BN;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t wpr = (K >> 5) * BITS, G = K >> GSH;
