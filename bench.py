@@ -433,7 +433,7 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(the sharding design is described in DESIGN.md)"}))
+                                   "(multi-GPU sharding is a design, not code, here)"}))
         sys.exit(2)
     import torch
     import rwkvq
