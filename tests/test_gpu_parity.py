@@ -303,6 +303,22 @@ def test_qmm_k64_output_tiles(O, rq, dev, transpose, R, sdt):
     assert (err <= 1e-2 * ref.double().abs().max() + 1e-3).all()
 
 
+def test_qmm_t_k64_tile_order_covers_every_tile(rq, dev):
+    """256 x 160 tiles walked in pairs of row tiles per column: M = 1200 gives
+    5 row tiles (the last pair holds one) by 64 column tiles.  Every output
+    element against an fp32 product of the HIP-dequantized weights."""
+    M, R, K, gs, bits = 1200, 10240, 2560, 64, 4
+    w = weights(R, K, 31).to(dev)
+    wq, s, b = rq.quantize(w, gs, bits)
+    x = acts(M, K, 37).to(dev)
+    say(f"qmm_t k64 tile order M={M} R={R} K={K}")
+    y = rq.quantized_matmul(x, wq, s, b, True, gs, bits)
+    ref = x.float() @ rq.dequantize(wq, s, b, gs, bits).float().t()
+    rel_check(y, ref, what="qmm_t k64 tile order")
+    err = (y.float() - ref).abs()
+    assert bool((err <= 1e-2 * ref.abs().max() + 1e-3).all())
+
+
 @pytest.mark.parametrize("R", [130, 77, 64])
 def test_qmm_n_unaligned_rows(O, rq, dev, R):
     """Row counts whose activation rows are not 16-byte multiples (scalar loads)."""
