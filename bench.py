@@ -41,6 +41,7 @@ for _p in (ROOT, os.path.join(ROOT, "rwkv-metal_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+XCDS, CUS = 8, 256             # MI355X: 8 XCDs x 32 CUs
 BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 flop/clk)
 GEMM_WARMUP = 10               # untimed GEMM launches before each timed GEMM region
 D, FFN, VOCAB, LAYERS = 2048, 8192, 65536, 24
@@ -65,9 +66,14 @@ def parse():
                     help="bounded CPU-baseline sample length")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline sweep only")
-    ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm"),
+    ap.add_argument("--pmc-workload", nargs="?", const="gemv",
+                    choices=("gemv", "gemm", "gemm_pair"),
                     help="run the headline plan (gemv) or the config-3 [10240, 2560] prefill "
-                         "GEMM at M=4096 (gemm) 3x, then 3 calibration copies; print nothing")
+                         "GEMM at M=4096 (gemm) 3x, then 3 calibration copies; gemm_pair: "
+                         "qmm_t_k64 and qmm_n_k64 on [2048, 2048] at M=4096 and qmm_t_k64 on "
+                         "[10240, 2560] at M=4096, 3x each; print nothing")
+    ap.add_argument("--pmc-counters", metavar="DIR",
+                    help="per-kernel averages of every counter in a rocprofv3 --pmc csv output")
     ap.add_argument("--pmc-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="reduce two rocprofv3 --pmc csv outputs of --pmc-workload")
     ap.add_argument("--pmc-kernel", default=None,
@@ -91,6 +97,20 @@ def pmc_workload(torch, rq, dev, which="gemv"):
     """What the counter passes profile: the headline plan (one launch), or one
     config-3 prefill GEMM, PMC_RUNS times, then COPY_RUNS copies of COPY_BYTES
     (read COPY_BYTES, write COPY_BYTES) as the last dispatches of the process."""
+    if which == "gemm_pair":
+        runs = []
+        for (R, K), transposes in (((2048, 2048), (True, False)), ((10240, 2560), (True,))):
+            w = (torch.randn(R, K, device=dev) * 0.02).to(torch.bfloat16)
+            wq, s, b = rq.quantize(w, 64, 4)
+            for tr in transposes:
+                x = torch.randn(4096, K if tr else R, device=dev).to(torch.bfloat16)
+                runs.append(rq.BoundQmm(x, wq, s, b, tr, 64, 4).run)
+        torch.cuda.synchronize()
+        for run in runs:
+            for _ in range(PMC_RUNS):
+                run()
+            torch.cuda.synchronize()
+        return
     if which == "gemm":
         M, R, K = PMC_GEMM
         w = (torch.randn(R, K, device=dev) * 0.02).to(torch.bfloat16)
@@ -197,6 +217,53 @@ def kt_report(d):
             print(f"| `{name[:100]}` | {wg} | {len(v)} | {statistics.median(v):.2f} |")
 
 
+def pmc_counters(d):
+    """Per-kernel, per-grid averages of every counter in a rocprofv3 --pmc
+    output, for the library's kernels; plus each kernel's MFMA-busy fraction
+    where the pass holds SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE:
+    MFMA-busy cycles over the kernel's active cycles on every SIMD
+    (256 CUs x 4 SIMDs), rocprofv3's own MfmaUtil expression.  A
+    v_mfma_f32_16x16x32_bf16 counts 16 busy cycles, so the fraction is also
+    the kernel's MFMA rate over the dense peak at the clock it ran at."""
+    import csv
+    import glob
+    files = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    per = {}
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+                if not any(k in name for k in ("qmv_", "qmm_", "lora_", "quantize_kernel")):
+                    continue
+                grid = int(r.get("Grid_Size", r.get("Grid_Size_X", 0)) or 0)
+                key = (name, grid, int(r["Dispatch_Id"]))
+                c = per.setdefault(key, {})
+                cn, v = r["Counter_Name"], float(r["Counter_Value"])
+                # GRBM counters are whole-GPU cycle counts repeated per instance: max;
+                # the SQ counters are per-instance parts of one total: sum
+                c[cn] = max(c.get(cn, 0.0), v) if cn.startswith("GRBM_") else c.get(cn, 0.0) + v
+    agg = {}
+    for (name, grid, _), c in per.items():
+        a = agg.setdefault((name, grid), {"n": 0})
+        a["n"] += 1
+        for k, v in c.items():
+            a[k] = a.get(k, 0.0) + v
+    for (name, grid), a in sorted(agg.items()):
+        n = a.pop("n")
+        print(f"{name} grid={grid} dispatches={n}")
+        for k in sorted(a):
+            print(f"  {k}: {a[k] / n:.6g}")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in a and "GRBM_GUI_ACTIVE" in a:
+            # the csv's GRBM_GUI_ACTIVE is the sum over the 8 XCDs' instances (8 x the
+            # kernel's cycles); MfmaUtil takes one instance (reduce max)
+            cycles = a["GRBM_GUI_ACTIVE"] / n / XCDS
+            frac = a["SQ_VALU_MFMA_BUSY_CYCLES"] / n / (cycles * CUS * 4)
+            print(f"  kernel_cycles (GRBM_GUI_ACTIVE / {XCDS}): {cycles:.6g}")
+            print(f"  mfma_busy_frac: {frac:.4f}")
+
+
 def read_traffic():
     """traffic_bytes_per_launch from the committed counter summary, or None."""
     try:
@@ -209,11 +276,11 @@ def read_traffic():
     return None
 
 
-def make_sweep(rq, torch, dev, M, bits=4, gs=64):
+def make_sweep(rq, torch, dev, M, bits=4, gs=64, timed=True):
     """Quantize the config-2 weights on the GPU (seed per layer/projection).
     Also returns the quantize and dequantize kernels' GB/s on the head weight
     (R*K*2 bytes of bf16 weights + the packed bytes, read or written), each
-    timed as one region of repeated calls."""
+    timed as one region of repeated calls (timed=False: None, None)."""
     probs = []
     qgbs = dgbs = None
     for layer in range(LAYERS + 1):
@@ -223,7 +290,7 @@ def make_sweep(rq, torch, dev, M, bits=4, gs=64):
             g = torch.Generator(device=dev).manual_seed(seed)
             w = (torch.randn(R, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
             wq, s, b = rq.quantize(w, gs, bits)
-            if name == "head":
+            if name == "head" and timed:
                 nb = R * K * 2 + weight_bytes(R, K, bits, gs)
                 qgbs = nb / time_region(torch, lambda: rq.quantize(w, gs, bits), 20, 5) / 1e9
                 dgbs = nb / time_region(torch, lambda: rq.dequantize(wq, s, b, gs, bits), 20, 5) / 1e9
@@ -256,16 +323,18 @@ def config1(torch, rq, dev, args):
     return out
 
 
-def config5(torch, rq, dev, args):
-    """BASELINE config 5: RWKV-7 7.2B shapes (D=4096, FFN 16384, vocab 65536),
-    3-bit g64 r/k/v/o and FFN, 8-bit g64 head, bf16 scales/biases.  Decode:
-    all 32 layers' 3-bit projections in one planned launch plus the 8-bit
-    head in a second, M=1, GB/s of packed weights + scales/biases.  Prefill:
-    each shape at M=2048, TFLOP/s."""
-    D5, F5, V5, L5 = 4096, 16384, 65536, 32
+C5_SHAPE, C5_LAYERS = (4096, 16384, 65536), 32  # D, FFN, vocab of RWKV-7 7.2B
+
+
+def config5_sweep(torch, rq, dev):
+    """The config-5 decode inputs on the GPU: every layer's 3-bit g64
+    r/k/v/o [4096, 4096], ffn_key [16384, 4096], ffn_value [4096, 16384]
+    (one seed per layer and projection) with M = 1 activations, and the 8-bit
+    g64 head [65536, 4096].  Returns (ws, xs, head, xh, weight bytes)."""
+    D5, F5, V5 = C5_SHAPE
     shapes = [(D5, D5)] * 4 + [(F5, D5), (D5, F5)]
     ws, xs, nbytes = [], [], 0
-    for layer in range(L5):
+    for layer in range(C5_LAYERS):
         for i, (R, K) in enumerate(shapes):
             g = torch.Generator(device=dev).manual_seed(5_000_000 + 10 * layer + i)
             w = (torch.randn(R, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
@@ -279,6 +348,17 @@ def config5(torch, rq, dev, args):
     del w
     xh = torch.randn(1, D5, generator=g, device=dev).to(torch.bfloat16)
     nbytes += weight_bytes(V5, D5, 8)
+    return ws, xs, head, xh, nbytes
+
+
+def config5(torch, rq, dev, args):
+    """BASELINE config 5: RWKV-7 7.2B shapes (D=4096, FFN 16384, vocab 65536),
+    3-bit g64 r/k/v/o and FFN, 8-bit g64 head, bf16 scales/biases.  Decode:
+    all 32 layers' 3-bit projections in one planned launch plus the 8-bit
+    head in a second, M=1, GB/s of packed weights + scales/biases.  Prefill:
+    each shape at M=2048, TFLOP/s."""
+    D5, F5, V5 = C5_SHAPE
+    ws, xs, head, xh, nbytes = config5_sweep(torch, rq, dev)
     p3 = rq.GroupedQmv(xs, ws, 64, 3)
     p8 = rq.GroupedQmv([xh], [head], 64, 8)
 
@@ -392,35 +472,145 @@ def time_region(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / 1e3 / steps
 
 
+def dependency_levels(torch, rq, xs, ws, outs, total_wbytes, args):
+    """The config-2 sweep in a real decode step's order: per layer the
+    independent r/k/v projections (rwkv_metal/model/rwkv7_x070.py:142-144)
+    as one grouped call, then o (:204), ffn_key and ffn_value (:221, each
+    reads the previous one's output), then the head (:343) -- 97 dependent
+    launches.  Timed eagerly and replayed from one HIP graph."""
+    n = len(PROJ)
+    calls = []
+    for layer in range(LAYERS):
+        i0 = layer * n
+        for group in ((0, 1, 2), (3,), (4,), (5,)):
+            idx = [i0 + j for j in group]
+            calls.append(rq.GroupedQmv([xs[i] for i in idx], [ws[i] for i in idx], 64, 4,
+                                       out=[outs[i] for i in idx]).run)
+    calls.append(rq.GroupedQmv([xs[-1]], [ws[-1]], 64, 4, out=[outs[-1]]).run)
+
+    def step():
+        for f in calls:
+            f()
+    steady_state(torch, step, DECODE_STEADY_S / 2)
+    t_eager = time_region(torch, step, max(3, args.steps // 4), 1)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    t_graph = time_region(torch, graph.replay, max(3, args.steps // 4), 3)
+    del graph
+    return {"launches_per_step": len(calls),
+            "eager_gbs": round(total_wbytes / t_eager / 1e9, 2),
+            "hip_graph_gbs": round(total_wbytes / t_graph / 1e9, 2),
+            "hip_graph_us_per_step": round(t_graph * 1e6, 1)}
+
+
+def dense_bf16_gemms(torch, dev, args):
+    """torch.matmul (hipBLASLt) of dense bf16 operands at config 3's shapes,
+    M = 4096: the vendor library's dense GEMM on the same box and clocks."""
+    out, fl, tt = {}, 0.0, 0.0
+    for R, K in ((2560, 2560), (10240, 2560), (2560, 10240)):
+        a = torch.randn(4096, K, device=dev).to(torch.bfloat16)
+        w = (torch.randn(R, K, device=dev) * 0.02).to(torch.bfloat16)
+        wt = w.t()
+        t = time_region(torch, lambda: torch.matmul(a, wt), max(5, args.steps // 2), GEMM_WARMUP)
+        f = 2.0 * 4096 * R * K
+        out[f"{R}x{K}_M4096"] = round(f / t / 1e12, 1)
+        fl += f
+        tt += t
+        del a, w, wt
+    out["aggregate"] = round(fl / tt / 1e12, 1)
+    return out
+
+
+MFMA_FILE = os.path.join(ROOT, "profiles", "qmm_k64_m4096_counters.txt")
+
+
+def read_mfma_busy():
+    """mfma_busy_frac of qmm_t_k64 on config 3 [10240, 2560] at M = 4096 from
+    the committed rocprofv3 counter summary, or None."""
+    try:
+        with open(MFMA_FILE) as fh:
+            for line in fh:
+                if line.startswith("qmm_t_k64 mfma_busy_frac:"):
+                    return float(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def _cpu_model():
+    """The host CPU's model name (/proc/cpuinfo, as lscpu prints it)."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _host_threads():
+    """Threads the all-core leg uses: the cores this process may run on,
+    capped by OMP_NUM_THREADS where the environment sets it (one GPU's share
+    of a shared host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
 def cpu_baseline(torch, seconds):
-    """The oracle's GEMV (rqo_qmv_bf16) on host cores over a bounded sample:
-    one config-2 layer's six projections at M=1, repeated for ~`seconds`."""
+    """The oracle's GEMV (rqo_qmv_bf16, the reference algorithm restated in
+    C: per-group sums of x*code and x, scale and bias once per group) on the
+    host over a bounded sample of the headline workload: one config-2 layer's
+    six projections at M = 1 (28.3 MB of packed weights).  Each leg (1 thread,
+    then all the host threads this process may use) times 6 repetitions of
+    enough passes for ~`seconds`/12 each and reports the median of the last 5
+    (the first is the warm-up)."""
+    import statistics
     from oracle import oracle as O
     if not os.path.exists(O._LIB_PATH):
         O.build()
-    threads = max(1, min(16, os.cpu_count() or 1))
-    sample = []
+    sample, sample_bytes = [], 0
     for name, R, K in PROJ:
         g = torch.Generator().manual_seed(2_000_000 + PROJ_ID[name])
         w = (torch.randn(R, K, generator=g) * 0.02).to(torch.bfloat16)
         wq, s, b = O.quantize(w, 64, 4)
         x = torch.randn(1, K, generator=g).to(torch.bfloat16)
-        sample.append((x, wq, s, b, weight_bytes(R, K)))
-    done_bytes, t0 = 0, time.perf_counter()
-    passes = 0
-    while True:
-        for x, wq, s, b, nb in sample:
-            O.qmv_bf16(x, wq, s, b, 64, 4, nthreads=threads)
-            done_bytes += nb
-        passes += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": round(done_bytes / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+        sample.append((x, wq, s, b))
+        sample_bytes += weight_bytes(R, K)
+
+    def one_pass(nt):
+        for x, wq, s, b in sample:
+            O.qmv_bf16(x, wq, s, b, 64, 4, nthreads=nt)
+
+    legs = {}
+    for nt in (1, _host_threads()):
+        t0 = time.perf_counter()
+        one_pass(nt)
+        passes = max(1, int(seconds / 12 / max(time.perf_counter() - t0, 1e-6)))
+        rates = []
+        for _ in range(6):
+            t0 = time.perf_counter()
+            for _ in range(passes):
+                one_pass(nt)
+            rates.append(passes * sample_bytes / (time.perf_counter() - t0) / 1e9)
+        legs[nt] = (statistics.median(rates[1:]), passes)
+    threads = max(legs)
+    return {"value": round(legs[threads][0], 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
+            "value_1_thread": round(legs[1][0], 3),
+            "cpu_model": _cpu_model(), "nproc": os.cpu_count(),
             "sample": (f"oracle rqo_qmv_bf16 (reference-algorithm CPU restatement, not MLX), "
-                       f"one RWKV-7 1.5B layer r/k/v/o/ffn_key/ffn_value at M=1, 4-bit g64, "
-                       f"{passes} passes in {el:.1f} s on {threads} threads")}
+                       f"one RWKV-7 1.5B layer r/k/v/o/ffn_key/ffn_value at M=1, 4-bit g64 "
+                       f"({sample_bytes} B of weights); median of 5 timed repetitions after 1 "
+                       f"warm-up, {legs[threads][1]} passes each on {threads} threads, "
+                       f"{legs[1][1]} on 1 thread")}
 
 
 def main():
@@ -430,6 +620,9 @@ def main():
         return
     if args.kt_report:
         kt_report(args.kt_report)
+        return
+    if args.pmc_counters:
+        pmc_counters(args.pmc_counters)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -484,7 +677,10 @@ def main():
         "config": {
             "workload": ("config2: RWKV-7 1.5B decode GEMV sweep, 24 layers x {r,k,v,o "
                          "[2048,2048], ffn_key [8192,2048], ffn_value [2048,8192]} + head "
-                         "[65536,2048], M=1, 4-bit g64 bf16 scales/biases, grouped launch"),
+                         "[65536,2048], M=1, 4-bit g64 bf16 scales/biases, as ONE cross-layer "
+                         "batched launch of the 145 independent GEMVs (a real decode step "
+                         "cannot batch across layers: layer l+1 reads layer l's output; "
+                         "extra.decode_m1_dependency_levels is that order)"),
             "weight_bytes_per_step": total_wbytes,
             "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
             "launches_per_step": launches,
@@ -525,6 +721,8 @@ def main():
         tgr = time_region(torch, graph.replay, max(3, args.steps // 4), 3)
         extra["decode_m1_one_launch_per_projection_hip_graph_gbs"] = round(total_wbytes / tgr / 1e9, 2)
         del graph
+        extra["decode_m1_dependency_levels"] = dependency_levels(torch, rwkvq, xs, ws, outs,
+                                                                 total_wbytes, args)
         # prefill GEMM, config 3 (RWKV-7 2.9B shapes) at M = 4096 (aggregate) and
         # 2048 / 512; the transposed product (QLoRA dX) at M = 4096
         pre = {}
@@ -552,6 +750,17 @@ def main():
         extra["prefill_qmm_m4096"] = {"tflops": round(agg, 1),
                                       "frac_of_bf16_peak": round(agg / BF16_PEAK_TFLOPS, 4),
                                       "per_shape_tflops": pre}
+        dense = dense_bf16_gemms(torch, dev, args)
+        extra["dense_bf16_torch_matmul_m4096_tflops"] = dense
+        result["roofline_gemm"] = {
+            "bound": "mfma", "achieved": round(agg, 1), "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(agg / BF16_PEAK_TFLOPS, 4),
+            "kernel": "qmm_t_k64<BITS=4, scales bf16> (256 x 160 / 256 x 128 tiles)",
+            "workload": "config3 prefill at M=4096 over [2560,2560], [10240,2560], [2560,10240] "
+                        "(aggregate flops / summed time)",
+            "flops_per_step": tot_flops,
+            "mfma_busy_frac": read_mfma_busy(),
+            "dense_bf16_torch_matmul_same_shapes_tflops": dense["aggregate"]}
         # QLoRA backward, config 4 (D=2048, M = 8 x 512): dX = dY . W^ per projection
         bwd = {}
         for name, R, K in (("rkvo", D, D), ("ffn_key", FFN, D), ("ffn_value", D, FFN)):

@@ -43,6 +43,8 @@ def lib() -> ctypes.CDLL:
         L.rqo_qmm.argtypes = [vp, i32, vp, vp, vp, i32, i64, i64, i64, i32, i32, i32, vp, i32, i32,
                               i32]
         L.rqo_qmv_bf16.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, vp, i32]
+        L.rqo_count_ties.argtypes = [vp, i32, i64, i64, i32, i32]
+        L.rqo_count_ties.restype = i64
         L.rqo_round_bf16.argtypes = [ctypes.c_float]
         L.rqo_round_bf16.restype = ctypes.c_float
         L.rqo_max_threads.restype = i32
@@ -73,6 +75,17 @@ def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4):
     if rc != 0:
         raise ValueError(f"oracle quantize rejected arguments (rc={rc})")
     return wq, s, b
+
+
+def count_ties(w: torch.Tensor, group_size: int = 64, bits: int = 4) -> int:
+    """Exact half-integer quotients that quantize() rounds on w (each group's
+    q0 and every code before clipping): where rint and round-half-away differ."""
+    w = w.contiguous()
+    R, K = w.shape
+    n = lib().rqo_count_ties(_p(w), DT[w.dtype], R, K, group_size, bits)
+    if n < 0:
+        raise ValueError("oracle count_ties rejected arguments")
+    return int(n)
 
 
 def pack(codes: torch.Tensor, bits: int) -> torch.Tensor:

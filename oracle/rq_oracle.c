@@ -32,6 +32,12 @@
  *                      with no rounding (the form of MLX's qmv, which applies
  *                      scale and bias to per-group sums of x*code and x);
  *                      products are accumulated in double.
+ *   - rqo_qmv_bf16   : the same transpose=1 product organised like MLX's CPU
+ *                      qmv (per-group sums of x*code and x, scale and bias
+ *                      applied once per group), bf16 in and out; the timed CPU
+ *                      baseline.
+ *   - rqo_count_ties : how many exact half-integer quotients rqo_quantize
+ *                      rounds (where rint and round-half-away would differ).
  *   - rqo_sb6_*      : the rwkv-quant sb6 (K3) decode, dense dequantize and
  *                      the scale/min expansion of the native repack
  *                      (rwkv_metal/lora/rwkvq_kernel.py, rwkvq_linear.py,
@@ -187,8 +193,14 @@ void rqo_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bits, uint8_
 /* One group of gs values (fp32 copies of the inputs) -> codes, scale, bias.
  * The arithmetic and its order follow the affine quantizer of MLX's CPU
  * backend (all single precision, IEEE division, rint = round-half-even). */
+/* A quotient that lies exactly half-way between two integers: the one case
+ * where rint (half-to-even) and round (half-away-from-zero) differ. */
+static int is_half_tie(float v) { return v - floorf(v) == 0.5f; }
+
+/* ties (optional): incremented once per exact half-integer quotient seen by
+ * the rounding of q0 or of a code, before clipping. */
 static void quantize_group(const float* w, int gs, int bits, uint8_t* codes,
-                           float* scale_out, float* bias_out) {
+                           float* scale_out, float* bias_out, int64_t* ties) {
     const float n_bins = (float)((1 << bits) - 1);
     const float eps = 1e-7f;
     float w_min = INFINITY, w_max = -INFINITY;
@@ -200,14 +212,18 @@ static void quantize_group(const float* w, int gs, int bits, uint8_t* codes,
     float scale = fmaxf((w_max - w_min) / n_bins, eps);
     scale = side ? scale : -scale;
     float edge = side ? w_min : w_max;
-    float q0 = rintf(edge / scale);
+    const float e = edge / scale;
+    if (ties && is_half_tie(e)) ++*ties;
+    float q0 = rintf(e);
     float bias = 0.0f;
     if (q0 != 0.0f) {
         scale = edge / q0;
         bias = edge;
     }
     for (int j = 0; j < gs; ++j) {
-        float q = rintf((w[j] - bias) / scale);
+        const float v = (w[j] - bias) / scale;
+        if (ties && is_half_tie(v)) ++*ties;
+        float q = rintf(v);
         q = fminf(fmaxf(q, 0.0f), n_bins);
         codes[j] = (uint8_t)q;
     }
@@ -230,7 +246,7 @@ int rqo_quantize(const void* w, int w_dt, int64_t rows, int64_t cols, int gs, in
             for (int64_t g = 0; g < G; ++g) {
                 for (int j = 0; j < gs; ++j) buf[j] = load_el(w, w_dt, r * cols + g * gs + j);
                 float s, b;
-                quantize_group(buf, gs, bits, rowcodes + g * gs, &s, &b);
+                quantize_group(buf, gs, bits, rowcodes + g * gs, &s, &b, NULL);
                 store_el(scales, w_dt, r * G + g, s);
                 store_el(biases, w_dt, r * G + g, b);
             }
@@ -240,6 +256,33 @@ int rqo_quantize(const void* w, int w_dt, int64_t rows, int64_t cols, int gs, in
         free(rowcodes);
     }
     return 0;
+}
+
+/* Number of exact half-integer quotients rqo_quantize rounds on w (the q0
+ * of each group and every code before clipping).  These are the only values
+ * where MLX's CPU rint (half-to-even) and a half-away-from-zero round would
+ * give different codes, so a count of zero on a workload means its codes do
+ * not depend on that choice. */
+int64_t rqo_count_ties(const void* w, int w_dt, int64_t rows, int64_t cols, int gs, int bits) {
+    if (!valid_bits(bits) || !valid_gs(gs) || !valid_dt(w_dt)) return -1;
+    if (rows < 0 || cols <= 0 || cols % gs != 0) return -1;
+    const int64_t G = cols / gs;
+    int64_t total = 0;
+#pragma omp parallel reduction(+ : total)
+    {
+        float* buf = (float*)malloc(sizeof(float) * (size_t)gs);
+        uint8_t* codes = (uint8_t*)malloc((size_t)gs);
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < rows; ++r)
+            for (int64_t g = 0; g < G; ++g) {
+                for (int j = 0; j < gs; ++j) buf[j] = load_el(w, w_dt, r * cols + g * gs + j);
+                float s, b;
+                quantize_group(buf, gs, bits, codes, &s, &b, &total);
+            }
+        free(buf);
+        free(codes);
+    }
+    return total;
 }
 
 /* ------------------------------------------------------------ dequantize */

@@ -245,6 +245,12 @@ def merge_lora(model: nn.Module, requantize: bool = False) -> nn.Module:
             base.weight.copy_(child.merged_weight())
         return base
 
+    # refuse before mutating anything: a quantized base merges only by requantizing
+    if not requantize:
+        for m in model.modules():
+            if isinstance(m, LoRALinear) and isinstance(m.linear, QuantizedLinear):
+                m.merged_weight(requantize=False)  # raises ValueError
+
     def replace_in(parent: nn.Module) -> None:
         for cname, child in list(parent.named_children()):
             if isinstance(child, LoRALinear):

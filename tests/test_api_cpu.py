@@ -155,6 +155,22 @@ def test_merge_lora_dense_base_cpu(rq):
     assert torch.allclose(m.blocks[0].tmix.r_proj(x), y, atol=1e-4, rtol=1e-4)
 
 
+def test_merge_lora_refuses_quantized_bases_before_merging_anything(rq):
+    """Without requantize=True a model with any quantized base raises and no
+    layer is merged, including dense-base ones earlier in the module order."""
+    m = Tiny(device="cpu").float()
+    m, _ = rq.add_lora(m, rank=4, layers=[0, 2])
+    blk = m.blocks[2].tmix
+    q = rq.QuantizedLinear(128, 128, bias=False, group_size=64, bits=4)
+    blk.v_proj = rq.LoRALinear(rank=4, alpha=8.0, base_module=q)
+    before = m.blocks[0].tmix.r_proj.linear.weight.clone()
+    with pytest.raises(ValueError, match="requantize"):
+        rq.merge_lora(m)
+    assert all(isinstance(getattr(b.tmix, n), rq.LoRALinear)
+               for b in (m.blocks[0], m.blocks[2]) for n in ("r_proj", "k_proj", "v_proj", "o_proj"))
+    assert torch.equal(m.blocks[0].tmix.r_proj.linear.weight, before)
+
+
 def test_save_load_lora_roundtrip(rq, tmp_path):
     torch.manual_seed(1)
     m = Tiny(device="cpu").float()

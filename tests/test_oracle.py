@@ -309,3 +309,139 @@ def test_sb6_repack_equals_affine_dequantize(O):
     assert torch.equal(got[same].view(torch.int32), want[same].view(torch.int32))
     clamped = torch.from_numpy(codes).float() * np.float32(1e-8) + want  # want = min there
     assert torch.equal(got[~same], clamped[~same])
+
+
+# ------------------------------------------------- the CPU-baseline GEMV
+
+def _codes_exact(wq, bits, K):
+    """Codes by Python big-integer extraction (independent of the C unpack)."""
+    words = wq.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    out = []
+    for r in range(words.shape[0]):
+        row = sum(int(words[r, i]) << (32 * i) for i in range(words.shape[1]))
+        out.append([(row >> (k * bits)) & ((1 << bits) - 1) for k in range(K)])
+    return torch.tensor(out, dtype=torch.float64)
+
+
+def _qmv_bf16_bound(y, x, we):
+    """rqo_qmv_bf16 rounds once to bf16 at the end (2^-9 relative) after fp32
+    per-group sums (each within ~gs * 2^-24 of the sum of |terms|); the bound
+    is the sum of both, elementwise."""
+    ref = x.double() @ we.t()
+    mag = x.double().abs() @ we.abs().t()
+    err = (y.double() - ref).abs()
+    assert bool((err <= 2.0 ** -8 * ref.abs() + 1e-5 * mag).all()), float(
+        (err / (2.0 ** -8 * ref.abs() + 1e-5 * mag)).max())
+    return ref
+
+
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_qmv_bf16_matches_exact_weights_float64(O, bits, gs):
+    """rqo_qmv_bf16, the GEMV the CPU baseline times (per-group sums of
+    x*code and of x, then scale and bias once per group), against a float64
+    product of s*q + b from big-integer-extracted codes, and against
+    rqo_qmm's exact-weight mode: the same number up to the final bf16
+    rounding."""
+    g = torch.Generator().manual_seed(700 + 10 * bits + gs)
+    R, K = 24, 512
+    w = (torch.randn(R, K, generator=g) * 0.02).to(torch.bfloat16)
+    wq, s, b = O.quantize(w, gs, bits)
+    we = (_codes_exact(wq, bits, K) * s.double().repeat_interleave(gs, 1)
+          + b.double().repeat_interleave(gs, 1))
+    for M in (1, 3, 16):
+        x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+        y = O.qmv_bf16(x, wq, s, b, gs, bits)
+        assert y.dtype == torch.bfloat16 and y.shape == (M, R)
+        ref = _qmv_bf16_bound(y, x, we)
+        ye = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32,
+                                weights="exact").double()
+        assert torch.allclose(ye, ref, rtol=1e-6, atol=1e-7)
+        assert ((y.double() - ye).abs() <= 2.0 ** -8 * ye.abs() + 1e-5).all()
+
+
+@pytest.mark.parametrize("name,R,K", [("r", 2048, 2048), ("ffn_key", 8192, 2048),
+                                      ("ffn_value", 2048, 8192)])
+def test_qmv_bf16_config2_shapes(O, name, R, K):
+    """The baseline's sample is one RWKV-7 1.5B layer at M = 1: every output
+    of each projection within the bound above of the exact-weight product,
+    and a dropped bias term or a bias applied to the wrong group would miss it
+    (bias * sum(x) over a group is ~10x the per-group dot product here)."""
+    g = torch.Generator().manual_seed(2_000_000 + R + K)
+    w = (torch.randn(R, K, generator=g) * 0.02).to(torch.bfloat16)
+    wq, s, b = O.quantize(w, 64, 4)
+    x = torch.randn(1, K, generator=g).to(torch.bfloat16)
+    y = O.qmv_bf16(x, wq, s, b, 64, 4)
+    ye = O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32,
+                            weights="exact").double()
+    mag = (x.double().abs() @ O.dequantize(wq, s, b, 64, 4, out_dtype=torch.float32).double().abs().t())
+    assert ((y.double() - ye).abs() <= 2.0 ** -8 * ye.abs() + 1e-5 * mag).all()
+    # the bias contribution is what the per-group factorisation must not lose
+    no_bias = O.quantized_matmul(x, wq, s, torch.zeros_like(b), True, 64, 4,
+                                 out_dtype=torch.float32, weights="exact").double()
+    assert ((no_bias - ye).norm() / ye.norm()).item() > 0.5
+
+
+# ------------------------------------------------------- exact .5 ties
+
+def _numpy_quantize_ties(w, gs, bits):
+    """Group-affine quantize in numpy float32 (IEEE ops, independent of the C
+    oracle): codes and the number of exact half-integer quotients rounded."""
+    nb = np.float32((1 << bits) - 1)
+    a = w.float().numpy().reshape(w.shape[0], -1, gs)
+    wmin, wmax = a.min(-1), a.max(-1)
+    scale = np.maximum((wmax - wmin) / nb, np.float32(1e-7)).astype(np.float32)
+    side = np.abs(wmin) > np.abs(wmax)
+    scale = np.where(side, scale, -scale).astype(np.float32)
+    edge = np.where(side, wmin, wmax).astype(np.float32)
+    e = (edge / scale).astype(np.float32)
+    q0 = np.rint(e)
+    nz = q0 != 0
+    scale = np.where(nz, edge / np.where(nz, q0, np.float32(1)), scale).astype(np.float32)
+    bias = np.where(nz, edge, np.float32(0)).astype(np.float32)
+    v = ((a - bias[..., None]) / scale[..., None]).astype(np.float32)
+    ties = int(((e - np.floor(e)) == 0.5).sum() + ((v - np.floor(v)) == 0.5).sum())
+    codes = np.clip(np.rint(v), 0, nb).astype(np.uint8).reshape(w.shape)
+    return codes, ties
+
+
+def test_tie_count_pinned_by_numpy_config1(O):
+    """rqo_count_ties against an independent numpy float32 statement of the
+    quantizer on BASELINE config 1 (RWKV-7 0.1B FFN key [3072, 768], 4-bit
+    g64), whose codes must also equal the oracle's bit for bit."""
+    g = torch.Generator().manual_seed(1_000_004)
+    w = (torch.randn(3072, 768, generator=g) * 0.02).to(torch.bfloat16)
+    codes, ties = _numpy_quantize_ties(w, 64, 4)
+    wq, _, _ = O.quantize(w, 64, 4)
+    assert np.array_equal(O.unpack(wq, 4).numpy(), codes)
+    n = O.count_ties(w, 64, 4)
+    assert n == ties
+    print(f"\nconfig 1 [3072, 768] 4-bit g64: {n} exact .5 quotients of "
+          f"{w.numel() + w.numel() // 64} rounded ({100.0 * n / w.numel():.3f} %)")
+
+
+@pytest.mark.parametrize("bits", BITS)
+def test_tie_count_pinned_by_numpy_every_width(O, bits):
+    g = torch.Generator().manual_seed(77 + bits)
+    w = (torch.randn(256, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    codes, ties = _numpy_quantize_ties(w, 64, bits)
+    wq, _, _ = O.quantize(w, 64, bits)
+    assert np.array_equal(O.unpack(wq, bits).numpy(), codes)
+    assert O.count_ties(w, 64, bits) == ties
+
+
+def test_tie_count_config2_layer_and_head(O):
+    """How many codes of a config-2 layer (RWKV-7 1.5B: r/k/v/o, ffn_key,
+    ffn_value) and the head are exact .5 ties, i.e. depend on half-to-even
+    (MLX's CPU backend, which this oracle and the HIP quantizer follow) versus
+    half-away-from-zero rounding.  Reported; a tie count of zero would have
+    made the choice moot."""
+    total, elems = 0, 0
+    for i, (R, K) in enumerate([(2048, 2048)] * 4 + [(8192, 2048), (2048, 8192), (65536, 2048)]):
+        g = torch.Generator().manual_seed(2_000_000 + i)
+        w = (torch.randn(R, K, generator=g) * 0.02).to(torch.bfloat16)
+        total += O.count_ties(w, 64, 4)
+        elems += R * K
+    assert total > 0
+    print(f"\nconfig 2 layer + head, 4-bit g64: {total} exact .5 quotients over {elems} "
+          f"weights ({100.0 * total / elems:.3f} %)")
