@@ -24,6 +24,8 @@
  *                     and its dX (finetune.py:141): the low-rank term fused into rq_qmm's
  *                     output stage
  *   rq_lora_down   <- its x . A^T and the backward's dY . B (the same lines)
+ *   rq_lora_grads  <- the backward's adapter gradients u^T x and dY^T z (the same
+ *                     layer under nn.value_and_grad, rwkv_metal/lora/finetune.py:141)
  *   rq_sb6_dequantize / rq_sb6_to_affine
  *                  <- the .rwkvq (rwkv-quant sb6) base: RwkvqLinear's fused dequant
  *                     (rwkv_metal/lora/rwkvq_kernel.py) and RwkvqNativeLinear's repack into
@@ -165,6 +167,31 @@ int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* s
                 const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
                 int group_size, int bits, int transpose, const void* z, const void* lora,
                 int64_t rank, float scale, void* y, rq_dtype y_dt, void* stream);
+
+/* The QLoRA adapter gradients, the MLX autograd of LoRALinear.__call__
+ * (rwkv_metal/lora/lora.py:58-63) through nn.value_and_grad
+ * (rwkv_metal/lora/finetune.py:141), which the reference evaluates as two
+ * mx.matmul nodes of its backward graph:
+ *   da[rank, k] = scale * u^T . x     x [m, k], u = dY . B [m, rank]
+ *   db[n, rank] = scale * dy^T . z    dy [m, n], z = x . A^T [m, rank]
+ * in one launch: bf16 in and out, fp32 accumulation, one rounding of the
+ * scaled sum.  Either product may be skipped with da = NULL (x and u are
+ * then not read) or db = NULL.  rank 16, 32, 48 or 64; k and n multiples of
+ * 8; x, u, dy and z 16-byte aligned.  m == 0 writes zero gradients.
+ * Deterministic: the same inputs give the same bits.
+ * The launch splits the m rows into chunks and reduces fp32 partial tiles in
+ * `workspace`, rq_lora_grads_workspace_bytes(m, k, n, rank, da != NULL,
+ * db != NULL) bytes (0 when one chunk per tile fills the GPU; workspace may
+ * then be NULL), 16-byte aligned: 64 KiB of per-tile counters at fixed
+ * offsets, then the partial tiles.  The workspace must be zero-filled before
+ * its first use; every call leaves the counters at zero, so one workspace
+ * serves any later problem that fits it.  Calls that run at the same time
+ * need separate workspaces.  k/64 + n/64 is at most 16384. */
+int64_t rq_lora_grads_workspace_bytes(int64_t m, int64_t k, int64_t n, int64_t rank, int has_da,
+                                      int has_db);
+int rq_lora_grads(const void* x, const void* u, const void* dy, const void* z, int64_t m,
+                  int64_t k, int64_t n, int64_t rank, float scale, void* da, void* db,
+                  void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Pack codes uint8[rows, cols] (values < 2^bits) into the MLX bitstream
  * w_q uint32[rows, cols*bits/32].  cols must be a multiple of 32. */

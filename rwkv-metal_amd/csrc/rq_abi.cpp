@@ -281,6 +281,56 @@ int rq_lora_down(const void* x, int64_t m, int64_t k, const void* a, int64_t ran
                          "rq_lora_down");
 }
 
+static int check_lora_grads(const char* what, const void* x, const void* u, const void* dy,
+                            const void* z, int64_t m, int64_t k, int64_t n, int64_t rank,
+                            const void* da, const void* db) {
+    if (m < 0 || k < 0 || n < 0) return fail(RQ_EINVAL, "%s: negative size", what);
+    if (rank < 16 || rank > 64 || rank % 16)
+        return fail(RQ_EINVAL, "%s: rank must be 16, 32, 48 or 64 (got %lld)", what, (long long)rank);
+    if (da && k % 8) return fail(RQ_EINVAL, "%s: k must be a multiple of 8 (got %lld)", what, (long long)k);
+    if (db && n % 8) return fail(RQ_EINVAL, "%s: n must be a multiple of 8 (got %lld)", what, (long long)n);
+    if (m > 0 && ((da && k > 0 && (!x || !u)) || (db && n > 0 && (!dy || !z))))
+        return fail(RQ_EINVAL, "%s: NULL operand", what);
+    if ((da && (!aligned16(x) || !aligned16(u))) || (db && (!aligned16(dy) || !aligned16(z))))
+        return fail(RQ_EALIGN, "%s: x, u, dy and z must be 16-byte aligned", what);
+    return RQ_OK;
+}
+
+int64_t rq_lora_grads_workspace_bytes(int64_t m, int64_t k, int64_t n, int64_t rank, int has_da,
+                                      int has_db) {
+    if (m < 0 || k < 0 || n < 0 || rank < 16 || rank > 64 || rank % 16)
+        return fail(RQ_EINVAL, "rq_lora_grads_workspace_bytes: bad sizes");
+    const rq::LoraGradPlan p = rq::lora_grads_plan(m, k, n, (int)rank, has_da != 0, has_db != 0);
+    if (p.tiles_a + p.tiles_b > rq::kLoraGradMaxTiles)
+        return fail(RQ_EINVAL, "rq_lora_grads_workspace_bytes: k/64 + n/64 exceeds %d",
+                    rq::kLoraGradMaxTiles);
+    return (int64_t)p.work_bytes;
+}
+
+int rq_lora_grads(const void* x, const void* u, const void* dy, const void* z, int64_t m,
+                  int64_t k, int64_t n, int64_t rank, float scale, void* da, void* db,
+                  void* workspace, int64_t workspace_bytes, void* stream) {
+    if (int rc = check_lora_grads("rq_lora_grads", x, u, dy, z, m, k, n, rank, da, db)) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    // m == 0 runs too: every job then stores a zero tile (no memset, so the
+    // call may be captured in a HIP graph)
+    const rq::LoraGradPlan p =
+        rq::lora_grads_plan(m, k, n, (int)rank, da != nullptr, db != nullptr);
+    if (p.tiles_a + p.tiles_b > rq::kLoraGradMaxTiles)
+        return fail(RQ_EINVAL, "rq_lora_grads: k/64 + n/64 exceeds %d", rq::kLoraGradMaxTiles);
+    const int64_t need = (int64_t)p.work_bytes;
+    if (need > 0) {
+        if (!workspace || workspace_bytes < need)
+            return fail(RQ_EINVAL, "rq_lora_grads: workspace has %lld bytes, needs %lld",
+                        (long long)workspace_bytes, (long long)need);
+        if (!aligned16(workspace))
+            return fail(RQ_EALIGN, "rq_lora_grads: workspace must be 16-byte aligned");
+    }
+    return launch_status(rq::launch_lora_grads(x, u, dy, z, m, k, n, (int)rank, scale, da, db, p,
+                                               workspace, s),
+                         "rq_lora_grads");
+}
+
 int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
                 const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
                 int group_size, int bits, int transpose, const void* z, const void* lora,

@@ -73,6 +73,29 @@ struct LoraArgs {
 hipError_t launch_lora_down(const void* x, int64_t m, int64_t k, const void* a, int rank, void* z,
                             hipStream_t stream);
 
+// QLoRA adapter gradients dA[rank, k] = scale * u^T x and dB[n, rank] =
+// scale * dY^T z in one launch (bf16 in and out, fp32 accumulation).  The
+// plan splits the m rows into `splits` chunks per 64-column tile; with more
+// than one, the launch needs a work buffer of kLoraGradCounterBytes of
+// per-tile counters (at fixed offsets, so that a counter slot never holds
+// anything else: zero before the first use, left zero by every launch,
+// whatever problem used the buffer last) followed by `partial_bytes` of fp32
+// partial tiles.
+constexpr int kLoraGradTargetBlocks = 1024;          // ~4 jobs per CU
+constexpr int64_t kLoraGradPartialCap = 8ll << 20;   // fp32 partial bytes at most
+constexpr int kLoraGradMaxTiles = 16384;             // k/64 + n/64 at most
+constexpr size_t kLoraGradCounterBytes = (size_t)kLoraGradMaxTiles * 4;
+struct LoraGradPlan {
+    int tiles_a, tiles_b, splits;
+    int64_t mchunk;         // rows per chunk (a multiple of 64)
+    size_t partial_bytes;   // 0 when splits == 1
+    size_t work_bytes;      // counters + partials; 0 when splits == 1
+};
+LoraGradPlan lora_grads_plan(int64_t m, int64_t k, int64_t n, int rank, bool has_a, bool has_b);
+hipError_t launch_lora_grads(const void* x, const void* u, const void* dy, const void* z,
+                             int64_t m, int64_t k, int64_t n, int rank, float scale, void* da,
+                             void* db, const LoraGradPlan& p, void* work, hipStream_t stream);
+
 // MFMA GEMM, transpose=True: y[m, rows] = x[m, cols] . W^T.
 hipError_t launch_qmm_t(const void* x, int x_dt, const uint32_t* wq, const void* scales,
                         const void* biases, int sb_dt, int64_t m, int64_t rows, int64_t cols,

@@ -105,9 +105,221 @@ __global__ __launch_bounds__(64 * LoraShape<RT>::W) void lora_down_kernel(
     }
 }
 
+// ------------------------------------------------------------ lora_grads
+//
+// The QLoRA adapter gradients (MLX autograd of LoRALinear.__call__,
+// rwkv_metal/lora/lora.py:58-63, through nn.value_and_grad at
+// rwkv_metal/lora/finetune.py:141), both contractions over the M token rows:
+//   dA[j, k] = scale * sum_m u[m, j] * x[m, k]      (u = dY . B, [M, rank])
+//   dB[n, j] = scale * sum_m dY[m, n] * z[m, j]     (z = x . A^T, [M, rank])
+// One launch covers both.  A job is a 64-column tile of x (dA) or dY (dB)
+// times the rank over one chunk of the rows.  With S > 1 chunks per tile
+// each chunk's fp32 partial tile goes to scratch memory and the chunk that
+// finishes last (a per-tile counter) sums the S partials in chunk order,
+// scales, rounds once to bf16, stores the tile and resets the counter to
+// zero; with S = 1 the job stores its tile directly.  Deterministic: the
+// same inputs give the same bits whatever order the chunks finish in.
+//
+// v_mfma_f32_16x16x32_bf16 contracts over 32 rows: A = 16 columns of wave
+// w's 16-column slice (lane: column lr, rows 8 lg .. +7), B = 16 ranks (lane:
+// rank lr, the same rows).  Both operands want the rows contiguous per lane
+// while the tensors are row-major [M, *], so every 64-row step is written to
+// LDS transposed, [column][row], in 16-byte row chunks XOR-swizzled by
+// (c ^ c >> 3) & 7: the fragment reads (16 columns per 16 lanes) and the
+// transposing 2-byte writes (column c0 + 8 t + j from 8 lanes t) both spread
+// over all 32 banks.
+
+constexpr int kGradBlock = 256;
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
+
+RQ_DEV int tkey(int c) { return (c ^ (c >> 3)) & 7; }
+
+template <int RT>  // rank / 16
+__global__ __launch_bounds__(kGradBlock) void lora_grads_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ u,
+    const uint16_t* __restrict__ dy, const uint16_t* __restrict__ z, int64_t M, int64_t K,
+    int64_t N, float scale, uint16_t* __restrict__ da, uint16_t* __restrict__ db,
+    float* __restrict__ part, uint32_t* __restrict__ cnt, int tiles_a, int S, int64_t mchunk) {
+    constexpr int RANK = 16 * RT;
+    constexpr int QV = RANK * 64 / 8;            // 16-byte chunks of a 64-row step of Q
+    constexpr int QL = (QV + kGradBlock - 1) / kGradBlock;
+    __shared__ __attribute__((aligned(16))) uint16_t pt[2][64 * 64];    // [column][row]
+    __shared__ __attribute__((aligned(16))) uint16_t qt[2][RANK * 64];  // [rank][row]
+    __shared__ uint32_t last;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lg = lane >> 4, lr = lane & 15;
+    const int tile = (int)(blockIdx.x / S), s = (int)(blockIdx.x % S);
+    const bool is_a = tile < tiles_a;
+    const uint16_t* P = is_a ? x : dy;
+    const uint16_t* Q = is_a ? u : z;
+    const int64_t C = is_a ? K : N;
+    const int64_t c0 = (int64_t)(is_a ? tile : tile - tiles_a) * 64;
+    const int64_t mb = (int64_t)s * mchunk;
+    const int64_t me = M < mb + mchunk ? M : mb + mchunk;
+    const int nsteps = (int)((me - mb + 63) / 64);
+
+    // thread t loads rows t / 8 and t / 8 + 32 of the 64-column tile, columns
+    // 8 (t % 8) .. +7 (C % 8 == 0: a chunk is wholly inside or outside)
+    const int prow = tid >> 3, pch = tid & 7;
+    const bool pcol = c0 + pch * 8 < C;
+    u32x4_t pv[2], qv[QL];
+    auto load = [&](int st) {
+        const int64_t m = mb + (int64_t)st * 64;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t r = m + prow + 32 * h;
+            pv[h] = u32x4_t{0u, 0u, 0u, 0u};
+            if (r < me && pcol) pv[h] = *(const u32x4_t*)(P + r * C + c0 + pch * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < QL; ++i) {
+            const int q = tid + kGradBlock * i;
+            qv[i] = u32x4_t{0u, 0u, 0u, 0u};
+            if (QV % kGradBlock == 0 || q < QV) {
+                const int64_t r = m + q / (RANK / 8);
+                if (r < me) qv[i] = *(const u32x4_t*)(Q + r * RANK + (q % (RANK / 8)) * 8);
+            }
+        }
+    };
+    auto put = [&](int b) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int m = prow + 32 * h;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int c = pch * 8 + j;
+                pt[b][c * 64 + (((m >> 3) ^ tkey(c)) << 3) + (m & 7)] =
+                    (uint16_t)(pv[h][j >> 1] >> (16 * (j & 1)));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < QL; ++i) {
+            const int q = tid + kGradBlock * i;
+            if (QV % kGradBlock == 0 || q < QV) {
+                const int m = q / (RANK / 8), jc = q % (RANK / 8);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int r = jc * 8 + j;
+                    qt[b][r * 64 + (((m >> 3) ^ tkey(r)) << 3) + (m & 7)] =
+                        (uint16_t)(qv[i][j >> 1] >> (16 * (j & 1)));
+                }
+            }
+        }
+    };
+
+    f32x4_t acc[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int ca = 16 * wave + lr;  // this lane's column of the A fragments
+    if (nsteps > 0) load(0);
+    for (int st = 0; st < nsteps; ++st) {
+        const int b = st & 1;
+        put(b);
+        if (st + 1 < nsteps) load(st + 1);  // in flight across the barrier and the MFMAs
+        // own LDS writes (and the previous step's reads of the other buffer) done
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int q = 4 * ks + lg;
+            const bf16x8_t av = __builtin_bit_cast(
+                bf16x8_t, *(const u32x4_t*)(pt[b] + ca * 64 + ((q ^ tkey(ca)) << 3)));
+#pragma unroll
+            for (int t = 0; t < RT; ++t) {
+                const int r = 16 * t + lr;
+                const bf16x8_t bv = __builtin_bit_cast(
+                    bf16x8_t, *(const u32x4_t*)(qt[b] + r * 64 + ((q ^ tkey(r)) << 3)));
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[t], 0, 0, 0);
+            }
+        }
+    }
+
+    // lane (lg, lr) of wave w holds acc[t][i]: column 16 w + 4 lg + i, rank 16 t + lr
+    uint16_t* out = is_a ? da : db;
+    auto store = [&](int c, int j, float v) {
+        if (c0 + c >= C) return;
+        const int64_t o = is_a ? (int64_t)j * K + c0 + c : (c0 + c) * RANK + j;
+        out[o] = (uint16_t)f32_to_bf16_bits(scale * v);
+    };
+    if (S == 1) {
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) store(16 * wave + 4 * lg + i, 16 * t + lr, acc[t][i]);
+        return;
+    }
+    float* mine = part + ((int64_t)tile * S + s) * (64 * RANK);
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mine[(16 * wave + 4 * lg + i) * RANK + 16 * t + lr] = acc[t][i];
+    // every thread releases its partial stores at agent scope (visible to the
+    // other XCDs' L2s) before the block counts itself in
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+               (uint32_t)(S - 1);
+    __syncthreads();
+    if (!last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const float* tp = part + (int64_t)tile * S * (64 * RANK);
+    for (int e = tid * 4; e < 64 * RANK; e += kGradBlock * 4) {
+        f32x4v_t v = *(const f32x4v_t*)(tp + e);
+        for (int q = 1; q < S; ++q) v += *(const f32x4v_t*)(tp + (int64_t)q * (64 * RANK) + e);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) store((e + w) / RANK, (e + w) % RANK, v[w]);
+    }
+    if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace
 
 namespace rq {
+
+LoraGradPlan lora_grads_plan(int64_t m, int64_t k, int64_t n, int rank, bool has_a, bool has_b) {
+    LoraGradPlan p;
+    p.tiles_a = has_a ? (int)((k + 63) / 64) : 0;
+    p.tiles_b = has_b ? (int)((n + 63) / 64) : 0;
+    const int64_t tiles = p.tiles_a + p.tiles_b;
+    const int64_t steps = (m + 63) / 64;
+    int64_t S = tiles > 0 ? (kLoraGradTargetBlocks + tiles - 1) / tiles : 1;
+    S = S < steps ? S : steps;
+    const int64_t per_split = tiles * 64 * (int64_t)rank * 4;
+    if (per_split > 0 && S * per_split > kLoraGradPartialCap) S = kLoraGradPartialCap / per_split;
+    if (S < 1) S = 1;
+    const int64_t per = (steps + S - 1) / S;  // 64-row steps per chunk
+    p.mchunk = per * 64;
+    p.splits = steps > 0 ? (int)((steps + per - 1) / per) : 1;
+    p.partial_bytes = p.splits > 1 ? (size_t)(tiles * p.splits * 64 * (int64_t)rank * 4) : 0;
+    p.work_bytes = p.splits > 1 ? kLoraGradCounterBytes + p.partial_bytes : 0;
+    return p;
+}
+
+hipError_t launch_lora_grads(const void* x, const void* u, const void* dy, const void* z,
+                             int64_t m, int64_t k, int64_t n, int rank, float scale, void* da,
+                             void* db, const LoraGradPlan& p, void* work, hipStream_t stream) {
+    const int tiles = p.tiles_a + p.tiles_b;
+    if (tiles == 0) return hipSuccess;
+    uint32_t* cnt = (uint32_t*)work;
+    float* part = (float*)((uint8_t*)work + kLoraGradCounterBytes);
+    const dim3 grid((unsigned)(tiles * p.splits)), block(kGradBlock);
+    const uint16_t *xp = (const uint16_t*)x, *up = (const uint16_t*)u;
+    const uint16_t *dyp = (const uint16_t*)dy, *zp = (const uint16_t*)z;
+    uint16_t *dap = (uint16_t*)da, *dbp = (uint16_t*)db;
+#define RQ_GRADS(RT)                                                                           \
+    hipLaunchKernelGGL((lora_grads_kernel<RT>), grid, block, 0, stream, xp, up, dyp, zp, m, k, n,  \
+                       scale, dap, dbp, part, cnt, p.tiles_a, p.splits, p.mchunk)
+    switch (rank) {
+        case 16: RQ_GRADS(1); break;
+        case 32: RQ_GRADS(2); break;
+        case 48: RQ_GRADS(3); break;
+        case 64: RQ_GRADS(4); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef RQ_GRADS
+    return hipGetLastError();
+}
 
 hipError_t launch_lora_down(const void* x, int64_t m, int64_t k, const void* a, int rank, void* z,
                             hipStream_t stream) {

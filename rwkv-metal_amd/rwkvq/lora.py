@@ -47,8 +47,8 @@ class _QLoRAFunction(torch.autograd.Function):
     low-rank term fused into the packed-weight GEMMs (rq_qmm_lora):
     forward adds z B^T (z = x A^T) in the transpose=True GEMM's output stage;
     backward computes u = dY B, dX = dY . W^ + scale * u A in the transpose=False
-    GEMM's output stage, dA = scale * u^T x, dB = scale * dY^T z.  The frozen
-    base gets no gradient."""
+    GEMM's output stage, and dA = scale * u^T x, dB = scale * dY^T z in one
+    rq_lora_grads launch.  The frozen base gets no gradient."""
 
     @staticmethod
     def forward(ctx, x2, lora_a, lora_b, base, scale):
@@ -70,11 +70,14 @@ class _QLoRAFunction(torch.autograd.Function):
             dx = ops.quantized_matmul_lora(dy, base.weight, base.scales, base.biases, u,
                                            lora_a.t().contiguous(), scale, False, base.group_size,
                                            base.bits).to(x2.dtype)
-        # bf16 GEMMs accumulate in fp32; the scale goes on the small results
-        if ctx.needs_input_grad[1]:
-            da = (u.t() @ x2).mul_(scale).to(lora_a.dtype)
-        if ctx.needs_input_grad[2]:
-            db = (dy.t() @ z).mul_(scale).to(lora_b.dtype)
+        # both adapter gradients in one launch, fp32 accumulation, one rounding
+        want_a, want_b = ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+        da, db = ops.lora_grads(x2 if want_a else None, u if want_a else None,
+                                dy if want_b else None, z if want_b else None, scale)
+        if da is not None:
+            da = da.to(lora_a.dtype)
+        if db is not None:
+            db = db.to(lora_b.dtype)
         return dx, da, db, None, None
 
 

@@ -345,6 +345,65 @@ def lora_down(x: Tensor, a: Tensor) -> Tensor:
     return z.reshape(*x.shape[:-1], rank)
 
 
+_grad_workspaces: dict = {}
+
+
+def _lora_workspace(device: torch.device, stream: int, nbytes: int) -> Tensor:
+    """A zero-filled workspace for rq_lora_grads, one per (device, stream):
+    every call leaves it zeroed for the next, and calls on one stream run in
+    order, so they can share it."""
+    key = (device.index, stream)
+    ws = _grad_workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _grad_workspaces[key] = ws
+    return ws
+
+
+def lora_grads(x: Tensor | None, u: Tensor | None, dy: Tensor | None, z: Tensor | None,
+               scale: float) -> Tuple[Tensor | None, Tensor | None]:
+    """The QLoRA adapter gradients of rwkv_metal/lora/lora.py:58-63 under
+    nn.value_and_grad (finetune.py:141): dA = scale * u^T x [rank, K] and
+    dB = scale * dY^T z [N, rank], bf16, in one rq_lora_grads launch.  Pass
+    None for both operands of a gradient that is not needed."""
+    want_a, want_b = x is not None, dy is not None
+    ref = x if want_a else dy
+    if ref is None:
+        return None, None
+    q = u if want_a else z
+    rank = q.shape[-1]
+    if not (ref.is_cuda and rank in (16, 32, 48, 64)
+            and all(t is None or t.dtype == torch.bfloat16 for t in (x, u, dy, z))
+            and (not want_a or x.shape[-1] % 8 == 0) and (not want_b or dy.shape[-1] % 8 == 0)):
+        da = (scale * (u.float().t() @ x.float())).to(u.dtype) if want_a else None
+        db = (scale * (dy.float().t() @ z.float())).to(z.dtype) if want_b else None
+        return da, db
+    ops_ = [t for t in (x, u, dy, z) if t is not None]
+    _on_gpu(*ops_)
+    m = ref.numel() // ref.shape[-1]
+    x2 = _ready(x.reshape(m, x.shape[-1])) if want_a else None
+    u2 = _ready(u.reshape(m, rank)) if want_a else None
+    dy2 = _ready(dy.reshape(m, dy.shape[-1])) if want_b else None
+    z2 = _ready(z.reshape(m, rank)) if want_b else None
+    K = x2.shape[1] if want_a else 0
+    N = dy2.shape[1] if want_b else 0
+    da = torch.empty(rank, K, dtype=torch.bfloat16, device=ref.device) if want_a else None
+    db = torch.empty(N, rank, dtype=torch.bfloat16, device=ref.device) if want_b else None
+    L = lib()
+    with _DeviceGuard(ref.device):
+        stream = _stream_on(ref.device)
+        nbytes = L.rq_lora_grads_workspace_bytes(m, K, N, rank, int(want_a), int(want_b))
+        check(nbytes if nbytes < 0 else 0, "lora_grads")
+        ws = _lora_workspace(ref.device, stream, int(nbytes)) if nbytes > 0 else None
+        rc = L.rq_lora_grads(_ptr(x2) if want_a else 0, _ptr(u2) if want_a else 0,
+                             _ptr(dy2) if want_b else 0, _ptr(z2) if want_b else 0, m, K, N,
+                             rank, float(scale), _ptr(da) if want_a else 0,
+                             _ptr(db) if want_b else 0, ws.data_ptr() if ws is not None else 0,
+                             ws.numel() if ws is not None else 0, stream)
+    check(rc, "lora_grads")
+    return da, db
+
+
 def _qmm_lora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, z: Tensor,
                     lora: Tensor, scale: float, transpose: bool, group_size: int, bits: int):
     """rq_qmm_lora on 2-D operands; None where the fused kernels do not apply."""

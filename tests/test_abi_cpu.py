@@ -28,7 +28,8 @@ def test_header_declares_the_expected_surface():
         "rq_abi_version", "rq_last_error", "rq_quantize", "rq_dequantize", "rq_qmm",
         "rq_pack", "rq_unpack", "rq_qmm_grouped", "rq_grouped_plan_table_bytes",
         "rq_grouped_plan_init", "rq_grouped_plan_run", "rq_embedding", "rq_sb6_dequantize",
-        "rq_sb6_to_affine", "rq_qmm_lora", "rq_lora_down"])
+        "rq_sb6_to_affine", "rq_qmm_lora", "rq_lora_down", "rq_lora_grads_workspace_bytes",
+        "rq_lora_grads"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -145,3 +146,33 @@ def test_plan_rejections_before_any_device_work(L):
     # an empty set is a valid plan whose run is a no-op
     assert L.rq_grouped_plan_init(None, 0, 0, 0, 0, 1, 64, 4, None, 0, byref(plan), None) == 0
     assert L.rq_grouped_plan_run(byref(plan), None) == 0
+
+
+def test_lora_grads_workspace_and_rejections(L):
+    """The gradient launch's workspace: none when one chunk per tile already
+    fills the GPU, fp32 partial tiles plus one counter per tile otherwise;
+    bad ranks, unaligned operands and a short workspace are refused."""
+    p = 0x1000
+    # 4096 rows, K = N = 2048, rank 16: 64 tiles, 16 chunks of 256 rows
+    counters = 16384 * 4
+    nb = L.rq_lora_grads_workspace_bytes(4096, 2048, 2048, 16, 1, 1)
+    assert nb == counters + 64 * 16 * 64 * 16 * 4
+    # only dB: 32 tiles, 32 chunks of 128 rows (64 rows per step, 64 steps)
+    assert L.rq_lora_grads_workspace_bytes(4096, 2048, 2048, 16, 0, 1) == \
+        counters + 32 * 32 * 64 * 16 * 4
+    # few rows: one chunk, no workspace
+    assert L.rq_lora_grads_workspace_bytes(64, 2048, 2048, 16, 1, 1) == 0
+    # wide outputs at rank 64 stay within the 8 MiB partial cap
+    nb = L.rq_lora_grads_workspace_bytes(4096, 8192, 8192, 64, 1, 1)
+    assert 0 < nb <= (8 << 20) + counters
+    assert L.rq_lora_grads_workspace_bytes(4096, 1 << 20, 8, 16, 1, 1) == -1
+    assert L.rq_lora_grads_workspace_bytes(4096, 2048, 2048, 24, 1, 1) == -1
+    assert L.rq_lora_grads(p, p, p, p, 4096, 2048, 2048, 24, 1.0, p, p, p, 1 << 30, None) == -1
+    assert "rank" in _err(L)
+    assert L.rq_lora_grads(p, p, p, p, 4096, 2044, 2048, 16, 1.0, p, p, p, 1 << 30, None) == -1
+    assert L.rq_lora_grads(p + 8, p, p, p, 4096, 2048, 2048, 16, 1.0, p, p, p, 1 << 30, None) == -2
+    assert L.rq_lora_grads(p, p, p, p, 4096, 2048, 2048, 16, 1.0, p, p, p, 64, None) == -1
+    assert "workspace" in _err(L)
+    # dA only: dY and z are not read, so they may be NULL
+    assert L.rq_lora_grads(p, p, 0, 0, 4096, 2048, 2048, 16, 1.0, p, 0, 0, 0, None) == -1
+    assert "workspace" in _err(L)
