@@ -193,6 +193,22 @@ int rq_lora_grads(const void* x, const void* u, const void* dy, const void* z, i
                   int64_t k, int64_t n, int64_t rank, float scale, void* da, void* db,
                   void* workspace, int64_t workspace_bytes, void* stream);
 
+/* rq_lora_grads without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  It has no counterpart in the reference.
+ * Same arguments, results (bit for bit) and kernels; the counters and
+ * partial tiles live in a static device buffer of 8 MiB + 64 KiB per GPU,
+ * held until the process ends, whose address is looked up (and its counters
+ * cleared on `stream`) at the first call on each device, with the device of
+ * `stream` current.  The call allocates nothing.  Problems whose partial
+ * tiles would not fit are rejected with RQ_EINVAL (the row split is capped
+ * at 8 MiB, so that is k/64 + n/64 > 16384).  Every call on a GPU shares that
+ * GPU's buffer: calls that overlap in time on one GPU (other streams, other
+ * host threads) race and must be serialised by the caller. */
+int rq_lora_grads_noalloc(const void* x, const void* u, const void* dy, const void* z, int64_t m,
+                          int64_t k, int64_t n, int64_t rank, float scale, void* da, void* db,
+                          void* stream);
+
 /* Pack codes uint8[rows, cols] (values < 2^bits) into the MLX bitstream
  * w_q uint32[rows, cols*bits/32].  cols must be a multiple of 32. */
 int rq_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* w_q,

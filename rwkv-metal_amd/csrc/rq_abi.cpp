@@ -331,6 +331,32 @@ int rq_lora_grads(const void* x, const void* u, const void* dy, const void* z, i
                          "rq_lora_grads");
 }
 
+int rq_lora_grads_noalloc(const void* x, const void* u, const void* dy, const void* z, int64_t m,
+                          int64_t k, int64_t n, int64_t rank, float scale, void* da, void* db,
+                          void* stream) {
+    if (int rc = check_lora_grads("rq_lora_grads_noalloc", x, u, dy, z, m, k, n, rank, da, db))
+        return rc;
+    const rq::LoraGradPlan p =
+        rq::lora_grads_plan(m, k, n, (int)rank, da != nullptr, db != nullptr);
+    if (p.tiles_a + p.tiles_b > rq::kLoraGradMaxTiles)
+        return fail(RQ_EINVAL, "rq_lora_grads_noalloc: k/64 + n/64 exceeds %d",
+                    rq::kLoraGradMaxTiles);
+    if (p.work_bytes > rq::kLoraScratchBytes)
+        return fail(RQ_EINVAL, "rq_lora_grads_noalloc: needs %lld bytes of scratch, the static "
+                    "buffer holds %lld", (long long)p.work_bytes, (long long)rq::kLoraScratchBytes);
+    hipStream_t s = (hipStream_t)stream;
+    void* work = nullptr;
+    if (p.work_bytes > 0) {
+        const hipError_t e = rq::lora_scratch(&work, s);
+        if (e != hipSuccess)
+            return fail(RQ_ELAUNCH, "rq_lora_grads_noalloc: static scratch unavailable: %s",
+                        hipGetErrorString(e));
+    }
+    return launch_status(rq::launch_lora_grads(x, u, dy, z, m, k, n, (int)rank, scale, da, db, p,
+                                               work, s),
+                         "rq_lora_grads_noalloc");
+}
+
 int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
                 const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
                 int group_size, int bits, int transpose, const void* z, const void* lora,

@@ -92,6 +92,12 @@ struct LoraGradPlan {
     size_t work_bytes;      // counters + partials; 0 when splits == 1
 };
 LoraGradPlan lora_grads_plan(int64_t m, int64_t k, int64_t n, int rank, bool has_a, bool has_b);
+// The no-allocation form's work buffer: a static device array of
+// kLoraScratchBytes per GPU.  lora_scratch gives its address on the current
+// device (looked up, and its counters cleared on `stream`, at the first call
+// on that device).
+constexpr size_t kLoraScratchBytes = kLoraGradCounterBytes + (size_t)kLoraGradPartialCap;
+hipError_t lora_scratch(void** out, hipStream_t stream);
 hipError_t launch_lora_grads(const void* x, const void* u, const void* dy, const void* z,
                              int64_t m, int64_t k, int64_t n, int rank, float scale, void* da,
                              void* db, const LoraGradPlan& p, void* work, hipStream_t stream);

@@ -16,6 +16,8 @@
 //    the next U before the MFMAs of the current ones (two register sets).
 //  * The W waves' partial 16 x rank tiles are summed through LDS behind one
 //    barrier and stored as bf16.
+#include <mutex>
+
 #include "rq_common.h"
 #include "rq_launch.h"
 
@@ -273,9 +275,47 @@ __global__ __launch_bounds__(kGradBlock) void lora_grads_kernel(
     if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, int n) {
+    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n) p[i] = 0u;
+}
+
+// The no-allocation form's work buffer: counters and fp32 partial tiles of
+// the gradient launch, one copy per GPU, held until the process ends.  Host
+// code never uses this name as an address (it is a host-side stand-in): the
+// device address comes from hipGetSymbolAddress, per device.
+static __device__ __align__(256) uint8_t scratch[rq::kLoraScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
 }  // namespace
 
 namespace rq {
+
+hipError_t lora_scratch(void** out, hipStream_t stream) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        // the counters must start at zero (each launch leaves them so); a fill
+        // kernel rather than a memset node, so the stream may be capturing
+        const int words = (int)(kLoraGradCounterBytes / 4);
+        hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, stream,
+                           (uint32_t*)p, words);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
 
 LoraGradPlan lora_grads_plan(int64_t m, int64_t k, int64_t n, int rank, bool has_a, bool has_b) {
     LoraGradPlan p;

@@ -29,7 +29,7 @@ def test_header_declares_the_expected_surface():
         "rq_pack", "rq_unpack", "rq_qmm_grouped", "rq_grouped_plan_table_bytes",
         "rq_grouped_plan_init", "rq_grouped_plan_run", "rq_embedding", "rq_sb6_dequantize",
         "rq_sb6_to_affine", "rq_qmm_lora", "rq_lora_down", "rq_lora_grads_workspace_bytes",
-        "rq_lora_grads"])
+        "rq_lora_grads", "rq_lora_grads_noalloc"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -176,3 +176,11 @@ def test_lora_grads_workspace_and_rejections(L):
     # dA only: dY and z are not read, so they may be NULL
     assert L.rq_lora_grads(p, p, 0, 0, 4096, 2048, 2048, 16, 1.0, p, 0, 0, 0, None) == -1
     assert "workspace" in _err(L)
+
+
+def test_lora_grads_noalloc_rejections_before_any_device_work(L):
+    p = 0x1000
+    assert L.rq_lora_grads_noalloc(p, p, p, p, 4096, 1 << 20, 8, 16, 1.0, p, p, None) == -1
+    assert "exceeds" in _err(L)
+    assert L.rq_lora_grads_noalloc(p, p, p, p, 4096, 2048, 2048, 20, 1.0, p, p, None) == -1
+    assert L.rq_lora_grads_noalloc(p, p + 4, p, p, 4096, 2048, 2048, 16, 1.0, p, p, None) == -2
