@@ -1290,16 +1290,29 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
 //
 // Transposed product dX[M, K] = dY[M, R] . W^[R, K] (the QLoRA backward),
 // warp-specialised like qmm_t_k64: block tile 256 (dY rows) x 128 (output
-// columns k), 64 weight rows r per stage.  Waves 0-3 run MFMAs; waves 4-7
-// (producers) per stage
-//   - write the dY tile (256 rows x 128 B, whole-line loads) to a 2-slot ring,
-//   - dequantize the stage's 64 x 128 weight block from the packed code and
-//     (scale, bias) tiles they staged in LDS one stage earlier: thread
-//     (r-quad, k-octet) turns 4 rows x 8 columns into eight 8-byte writes of
-//     the bf16 tile Bt[k][r] (r contiguous, the MFMA B layout),
-//   - stage the next stage's code and (scale, bias) tiles (16-byte loads of
-//     the rows' packed words) and keep two stages of loads in flight.
+// columns k), 64 weight rows r per stage.  The contraction runs over r, the
+// rows of W, while the packed codes run along k, so the weight operand needs
+// a transpose somewhere.  It happens in the MFMA waves' fragment reads:
+//  * producers (waves 4-7) dequantize exactly like qmm_t_k64's: each thread
+//    takes one 32-code run of one weight row per stage (row pt % 64, run
+//    pt / 64 of the tile's four), its codes and (scale, bias) loaded straight
+//    into registers D stages ahead, and writes the 32 bf16 values as two
+//    16-byte stores of the natural [r][k] tile (k contiguous, 256-byte rows);
+//    they also write the dY tile (256 rows x 128 B) to a 2-slot ring;
+//  * MFMA waves (0-3) read each weight fragment (8 consecutive r of one k
+//    column per lane) with two gfx950 ds_read_b64_tr_b16: within 16 lanes,
+//    source lane 4s + a reads 4 columns 4a .. 4a+3 of row s and result lane
+//    4a + b receives column 4a + b of rows 0..3.
+// The [r][k] tile's 16-byte chunks are XOR-swizzled by nkey(r): a bijection
+// on r % 8, so the 8 rows of a producer store group hit 8 bank groups, whose
+// upper two bits are a bijection on each aligned quad of rows, so the 4 rows x
+// 2 chunks of a 16-lane transposed read hit 8.  No code tile is staged in
+// LDS and no (scale, bias) table: the producers' critical path has no LDS
+// read, and the tile is written with half as many stores as the earlier
+// r-contiguous layout needed.
 // Requires 16-bit scales, R % 64 == 0 and K % 128 == 0.
+RQ_DEV int nkey(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
 template <int BITS, int SDT>
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
@@ -1307,26 +1320,14 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
     void* __restrict__ y, int y_dt, int tiles_m, int tiles_n, rq::LoraArgs lora) {
     constexpr int BM = 256, BN = 128, WN = BN / 2;
     constexpr int TM = 8, TN = WN / 16;
-    constexpr int BLD = 72;                 // bf16 tile row stride (64 + 8 elements)
-    constexpr int CW = BN * BITS / 32;      // packed words per weight row per stage
-    constexpr int CCH = CW / 4;             // 16-byte chunks per row (BITS of them)
-    // LDS row stride of the code tile: odd, so that the 16 row quads a
-    // dequantization read spans (rows 4q + i) fall in 16 different banks (a
-    // stride of CW words put all 16 in one bank)
-    constexpr int CWP = CW + 1;
-    constexpr int NCL = (64 * CCH + 255) / 256;  // code chunks per producer thread
+    constexpr int D = RQ_K64_DEPTH;         // stages of loads in flight per producer thread
+    constexpr int ROWB = BN * 2;            // bytes per row of the bf16 weight tile
+    static_assert(D == 2, "the register ring index is the ring slot");
     static_assert(SDT != RQ_F32, "16-bit scales");
     __shared__ __attribute__((aligned(16))) uint8_t xs0[BM * 128];
     __shared__ __attribute__((aligned(16))) uint8_t xs1[BM * 128];
-    __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * BLD];
-    __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * BLD];
-    __shared__ __attribute__((aligned(16))) uint32_t cs0[64 * CWP];
-    __shared__ __attribute__((aligned(16))) uint32_t cs1[64 * CWP];
-    // fp32 (scale, bias) pairs [group][row % 4][row / 4][2]: one 8-byte read
-    // per row in the dequantization, the 16 row quads of a read in
-    // consecutive pairs
-    __shared__ __attribute__((aligned(16))) float ss0[64 * 4 * 2];
-    __shared__ __attribute__((aligned(16))) float ss1[64 * 4 * 2];
+    __shared__ __attribute__((aligned(16))) uint8_t bq0[64 * ROWB];
+    __shared__ __attribute__((aligned(16))) uint8_t bq1[64 * ROWB];
 
     const int ntiles = tiles_m * tiles_n;
     const int per_xcd = (ntiles + 7) / 8;
@@ -1337,14 +1338,14 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t wpr = (K >> 5) * BITS, G = K >> gs_shift;
     const int nst = (int)(R >> 6);
-    const int ng = BN >> gs_shift;          // groups per tile row: 4, 2, 1
-    const int64_t g_first = k0 >> gs_shift;
 
     if (wave >= 4) {
         // ---------------------------------------------------------- producers
         if (RQ_K64_PPRIO) __builtin_amdgcn_s_setprio(RQ_K64_PPRIO);
         const int pt = tid - 256, pw = wave - 4;
         typedef const __attribute__((address_space(1))) u32x4_t* gv_t;
+        typedef const __attribute__((address_space(1))) uint32_t* gw_t;
+        typedef const __attribute__((address_space(1))) uint16_t* gh_t;
         uint32_t xoff[8], xdst[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -1356,143 +1357,61 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
             xdst[i] = (uint32_t)(row * 128 + ((chunk ^ (row & 7)) * 16));
         }
         const uint8_t* xbase = (const uint8_t*)(x + m0 * R);
-        // code chunks: chunk c = pt + 256 j -> weight row c / CCH, 16-byte chunk c % CCH
-        const uint32_t* wtile = wq + (k0 >> 5) * BITS;
-        // (scale, bias): thread pt < 64 loads row pt's ng values of both arrays
-        const int srow = pt;
-        const uint16_t* ssrc = (const uint16_t*)scales + g_first;
-        const uint16_t* bsrc = (const uint16_t*)biases + g_first;
+        // the dequantization job: run jq of row jr of each stage
+        const int jr = pt & 63, jq = pt >> 6;
+        const uint32_t* wbase = wq + (k0 >> 5) * BITS + jq * BITS;
+        const int64_t gidx = (k0 + jq * 32) >> gs_shift;
+        const uint16_t* sbase = (const uint16_t*)scales + gidx;
+        const uint16_t* bbase = (const uint16_t*)biases + gidx;
+        uint32_t qdst[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) qdst[q] = (uint32_t)(jr * ROWB + (((4 * jq + q) ^ nkey(jr)) << 4));
 
-        u32x4_t xv[2][8];
-        u32x4_t cv[2][NCL];
-        uint32_t sv[2][4];  // raw: scales words 0-1, biases words 2-3
-        auto load_x = [&](int st, int r) {
+        u32x4_t xv[D][8];
+        uint32_t cv[D][BITS];
+        uint16_t sv[D][2];
+        auto issue = [&](int st, int r) {
             const int sc = st < nst ? st : nst - 1;
             const uint8_t* xb = xbase + (int64_t)sc * 128;
 #pragma unroll
             for (int i = 0; i < 8; ++i) xv[r][i] = *(gv_t)(xb + xoff[i]);
+            const int64_t row = (int64_t)sc * 64 + jr;
+            const uint32_t* ws = wbase + row * wpr;
+            if constexpr (BITS % 4 == 0) {
+#pragma unroll
+                for (int q = 0; q < BITS / 4; ++q) {
+                    const u32x4_t v = *((gv_t)ws + q);
+                    cv[r][4 * q] = v[0]; cv[r][4 * q + 1] = v[1];
+                    cv[r][4 * q + 2] = v[2]; cv[r][4 * q + 3] = v[3];
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < BITS; ++q) cv[r][q] = *((gw_t)ws + q);
+            }
+            sv[r][0] = *(gh_t)(sbase + row * G);
+            sv[r][1] = *(gh_t)(bbase + row * G);
         };
-        auto load_c = [&](int st, int r) {
-            const int sc = st < nst ? st : nst - 1;
 #pragma unroll
-            for (int j = 0; j < NCL; ++j) {
-                const int c = pt + 256 * j;
-                if (c < 64 * CCH) {
-                    const int64_t row = (int64_t)sc * 64 + c / CCH;
-                    cv[r][j] = *(gv_t)(wtile + row * wpr + (c % CCH) * 4);
-                }
-            }
-            if (pt < 64) {
-                const int64_t row = (int64_t)sc * 64 + srow;
-#pragma unroll
-                for (int a = 0; a < 2; ++a) {
-                    const uint16_t* src = (a ? bsrc : ssrc) + row * G;
-                    if (ng == 4) {
-                        const uint2 v = *(const uint2*)src;
-                        sv[r][2 * a] = v.x; sv[r][2 * a + 1] = v.y;
-                    } else if (ng == 2) {
-                        sv[r][2 * a] = *(const uint32_t*)src; sv[r][2 * a + 1] = 0u;
-                    } else {
-                        sv[r][2 * a] = *src; sv[r][2 * a + 1] = 0u;
-                    }
-                }
-            }
-        };
-        auto put_c = [&](int r, uint32_t* cs, float* ss) {
-#pragma unroll
-            for (int j = 0; j < NCL; ++j) {
-                const int c = pt + 256 * j;
-                if (c < 64 * CCH) {
-                    uint32_t* d = cs + (c / CCH) * CWP + (c % CCH) * 4;
-                    d[0] = cv[r][j][0]; d[1] = cv[r][j][1]; d[2] = cv[r][j][2]; d[3] = cv[r][j][3];
-                }
-            }
-            if (pt < 64) {
-                typedef float f32x2_t __attribute__((ext_vector_type(2)));
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const uint32_t sw = sv[r][g >> 1], bw = sv[r][2 + (g >> 1)];
-                    const int sh = 16 * (g & 1);
-                    *(f32x2_t*)(ss + ((g * 4 + (srow & 3)) * 16 + (srow >> 2)) * 2) =
-                        f32x2_t{dt_traits<SDT>::to_f32((uint16_t)(sw >> sh)),
-                                dt_traits<SDT>::to_f32((uint16_t)(bw >> sh))};
-                }
-            }
-        };
-        // dequantization unit: rows 4*rq .. 4*rq+3, columns 8*kc .. 8*kc+7
-        const int rq = pt & 15, kc = pt >> 4;
-        auto dequant = [&](const uint32_t* cs, const float* ss, uint16_t* bq) {
-            const int gl = (kc * 8) >> gs_shift;  // group of these columns within the tile
-            float v[4][8];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = rq * 4 + i;
-                const int bit = kc * 8 * BITS;
-                const uint32_t* wr = cs + row * CWP + (bit >> 5);
-                const uint64_t win = (uint64_t)wr[0] | ((bit & 31) + 8 * BITS > 32 ? (uint64_t)wr[1] << 32 : 0ull);
-                const int off = bit & 31;
-                typedef float f32x2_t __attribute__((ext_vector_type(2)));
-                const f32x2_t sbv = *(const f32x2_t*)(ss + ((gl * 4 + i) * 16 + rq) * 2);
-                const float sf = sbv[0], bf = sbv[1];
-                float cf[8];
-                if constexpr (BITS == 4) {
-                    // one word = the 8 codes; byte converts on the nibble halves
-                    // (masks hidden from the optimiser, see dequant_run_fast)
-                    uint32_t lo = wr[0] & 0x0F0F0F0Fu, hi = (wr[0] >> 4) & 0x0F0F0F0Fu;
-                    asm("" : "+v"(lo));
-                    asm("" : "+v"(hi));
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        cf[2 * q] = (float)(uint8_t)(lo >> (8 * q));
-                        cf[2 * q + 1] = (float)(uint8_t)(hi >> (8 * q));
-                    }
-                } else if constexpr (BITS == 8) {
-                    uint32_t w0 = wr[0], w1 = wr[1];
-                    asm("" : "+v"(w0));
-                    asm("" : "+v"(w1));
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        cf[q] = (float)(uint8_t)(w0 >> (8 * q));
-                        cf[4 + q] = (float)(uint8_t)(w1 >> (8 * q));
-                    }
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 8; ++c)
-                        cf[c] = (float)(uint32_t)((win >> (off + c * BITS)) & ((1u << BITS) - 1u));
-                }
-#pragma unroll
-                for (int c = 0; c < 8; ++c) v[i][c] = fmaf(sf, cf[c], bf);
-            }
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-                *(u32x2_t*)(bq + (kc * 8 + c) * BLD + rq * 4) =
-                    u32x2_t{pack_bf16x2(v[0][c], v[1][c]), pack_bf16x2(v[2][c], v[3][c])};
-            }
-        };
-
-        load_x(0, 0);
-        load_x(1, 1);
-        load_c(0, 0);
-        load_c(1, 1);
-        put_c(0, cs0, ss0);
-        load_c(2, 0);
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        for (int r = 0; r < D; ++r) issue(r, r);
         asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();        // stage 0's code tile is staged
+        __builtin_amdgcn_s_barrier();  // pairs with the MFMA waves' first barrier
         asm volatile("" ::: "memory");
         for (int s0 = 0; s0 < nst; s0 += 2) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int st = s0 + u;
                 uint8_t* xs = u ? xs1 : xs0;
+                uint8_t* bq = u ? bq1 : bq0;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u][i];
-                dequant(u ? cs1 : cs0, u ? ss1 : ss0, u ? bq1 : bq0);
-                put_c(u ^ 1, u ? cs0 : cs1, u ? ss0 : ss1);  // stage st+1's tiles
-                load_x(st + 2, u);
-                load_c(st + 3, u ^ 1);
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                uint32_t d[16];
+                dequant_run_fast<BITS>(cv[u], dt_traits<SDT>::to_f32(sv[u][0]),
+                                       dt_traits<SDT>::to_f32(sv[u][1]), d);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *(u32x4_t*)(bq + qdst[q]) = u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
+                issue(st + D, u);
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this stage's LDS writes are done
                 asm volatile("" ::: "memory");
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
@@ -1518,7 +1437,20 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
             const int row = wm * 128 + a * 16 + lr;
             aoff[h][a] = (uint32_t)(row * 128 + (((h * 4 + lg) ^ (row & 7)) * 16));
         }
-    const uint32_t boff = (uint32_t)((wn * WN + lr) * BLD + lg * 8);
+    // weight fragment (k-step h, column subtile b), half v: rows 32 h + 8 lg +
+    // 4 v + lr / 4, columns wn * 64 + 16 b + 4 (lr % 4) .. +3 (the source side
+    // of the transposed read); row % 8 does not depend on h or lg
+    uint32_t boff[2][TN];
+#pragma unroll
+    for (int v = 0; v < 2; ++v)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int row = 8 * lg + 4 * v + (lr >> 2);
+            const int col = wn * WN + 16 * b + 4 * (lr & 3);
+            boff[v][b] = (uint32_t)(row * ROWB + (((col >> 3) ^ nkey(row)) << 4) + (col & 7) * 2);
+        }
+    typedef short s16x4_t __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_p;
 
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();  // the producers' initial barrier
@@ -1533,15 +1465,20 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
             asm volatile("" ::: "memory");
             if (st < nst) {
                 const uint8_t* xs = u ? xs1 : xs0;
-                const uint16_t* bq = u ? bq1 : bq0;
+                uint8_t* bq = u ? bq1 : bq0;
                 // fragments software-pipelined as in qmm_t_k64
                 bf16x8_t bf[2][TN], af[3];
                 auto rdA = [&](int h, int a) {
                     return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
                 };
                 auto rdB = [&](int h, int b) {
-                    return __builtin_bit_cast(bf16x8_t,
-                                              *(const u32x4_t*)(bq + boff + b * 16 * BLD + h * 32));
+                    const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4_p)(bq + boff[0][b] + h * 32 * ROWB));
+                    const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4_p)(bq + boff[1][b] + h * 32 * ROWB));
+                    typedef short s16x8_t __attribute__((ext_vector_type(8)));
+                    const s16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    return __builtin_bit_cast(bf16x8_t, v);
                 };
 #pragma unroll
                 for (int b = 0; b < TN; ++b) bf[0][b] = rdB(0, b);
