@@ -72,6 +72,9 @@ def parse():
                          "GEMM at M=4096 (gemm) 3x, then 3 calibration copies; gemm_pair: "
                          "qmm_t_k64 and qmm_n_k64 on [2048, 2048] at M=4096 and qmm_t_k64 on "
                          "[10240, 2560] at M=4096, 3x each; print nothing")
+    ap.add_argument("--qlora-step-workload", action="store_true",
+                    help="run 5 + 20 config-4 QLoRA layer steps (LoRALinear autograd, the "
+                         "bench's fused path) for a kernel trace; print the per-step time")
     ap.add_argument("--pmc-counters", metavar="DIR",
                     help="per-kernel averages of every counter in a rocprofv3 --pmc csv output")
     ap.add_argument("--pmc-report", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -384,17 +387,12 @@ def config5(torch, rq, dev, args):
     return out
 
 
-def qlora_step(torch, rq, dev, ws, args):
-    """BASELINE config 4: one QLoRA training step of one RWKV-7 1.5B layer
-    (D=2048) on a frozen 4-bit g64 base -- for each of r, k, v, o, ffn_key,
-    ffn_value: y = qmm(x, Wq) + (alpha/r) (x A^T) B^T, r = alpha = 16,
-    A ~ N(0, 1/D), B ~ N(0, 0.01) (std), x [8, 512, K] bf16, then dX, dA, dB
-    for a given dY.  `fused`: LoRALinear's path (low-rank term in the GEMMs'
-    output stage, rq_qmm_lora); `composed`: the same layer as separate ops
-    (quantized_matmul + two torch GEMMs + scale + add, autograd).  Reported:
-    ms per layer step and the step's TFLOP/s (base forward + dX GEMMs, 4*M*R*K,
-    plus the adapter GEMMs)."""
-    from torch import nn
+def qlora_layers(torch, rq, dev, ws):
+    """Config 4's QLoRA layer: for each projection a LoRALinear (r = alpha =
+    16, A ~ N(0, 1/D), B ~ N(0, 0.01) std) over the frozen 4-bit g64 base
+    `ws[i]`, with x [8, 512, K] and dY [8, 512, R] bf16.  Returns the
+    (layer, x, dY) triples and the step's flops (base forward + dX GEMMs and
+    the adapter GEMMs)."""
     r, alpha, M = 16, 16.0, 8 * 512
     layers, flops = [], 0.0
     for name, R, K in PROJ:
@@ -410,6 +408,44 @@ def qlora_step(torch, rq, dev, ws, args):
         dy = torch.randn(8, 512, R, device=dev).to(torch.bfloat16)
         layers.append((lay, x, dy))
         flops += 4.0 * M * R * K + 6.0 * M * r * (R + K)
+    return layers, flops
+
+
+def qlora_step_workload(torch, rq, dev):
+    """What a kernel trace of the config-4 QLoRA layer step profiles: 5
+    untimed and 20 timed fused layer steps."""
+    ws = []
+    for name, R, K in PROJ:
+        g = torch.Generator(device=dev).manual_seed(2_000_000 + PROJ_ID[name])
+        ws.append(rq.quantize((torch.randn(R, K, generator=g, device=dev) * 0.02).to(torch.bfloat16), 64, 4))
+    layers, _ = qlora_layers(torch, rq, dev, ws)
+
+    def fused():
+        for lay, x, dy in layers:
+            torch.autograd.grad(lay(x), (x, lay.lora_a, lay.lora_b), dy)
+    for _ in range(5):
+        fused()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        fused()
+    torch.cuda.synchronize()
+    print(f"config-4 QLoRA layer step: {1e3 * (time.perf_counter() - t0) / 20:.3f} ms", flush=True)
+
+
+def qlora_step(torch, rq, dev, ws, args):
+    """BASELINE config 4: one QLoRA training step of one RWKV-7 1.5B layer
+    (D=2048) on a frozen 4-bit g64 base -- for each of r, k, v, o, ffn_key,
+    ffn_value: y = qmm(x, Wq) + (alpha/r) (x A^T) B^T, r = alpha = 16,
+    A ~ N(0, 1/D), B ~ N(0, 0.01) (std), x [8, 512, K] bf16, then dX, dA, dB
+    for a given dY.  `fused`: LoRALinear's path (rank 16, 4-bit: the forward
+    and dX are one rq_qlora launch each, with x A^T / dY B computed inside the
+    GEMM and the term added in its output stage, and dA, dB one rq_lora_grads
+    launch); `composed`: the same layer as separate ops
+    (quantized_matmul + two torch GEMMs + scale + add, autograd).  Reported:
+    ms per layer step and the step's TFLOP/s (base forward + dX GEMMs, 4*M*R*K,
+    plus the adapter GEMMs)."""
+    layers, flops = qlora_layers(torch, rq, dev, ws)
 
     def fused():
         for lay, x, dy in layers:
@@ -636,6 +672,9 @@ def main():
     bits, gs = 4, 64
     if args.pmc_workload:
         pmc_workload(torch, rwkvq, dev, args.pmc_workload)
+        return
+    if args.qlora_step_workload:
+        qlora_step_workload(torch, rwkvq, dev)
         return
 
     # ---------------- headline: config-2 decode sweep, M=1, grouped launches

@@ -23,6 +23,8 @@
  *   rq_qmm_lora    <- LoRALinear.__call__ over a quantized base (rwkv_metal/lora/lora.py:58-63)
  *                     and its dX (finetune.py:141): the low-rank term fused into rq_qmm's
  *                     output stage
+ *   rq_qlora       <- the same layer with x . A^T (or dY . B) computed inside the GEMM:
+ *                     forward and dX each one launch
  *   rq_lora_down   <- its x . A^T and the backward's dY . B (the same lines)
  *   rq_lora_grads  <- the backward's adapter gradients u^T x and dY^T z (the same
  *                     layer under nn.value_and_grad, rwkv_metal/lora/finetune.py:141)
@@ -208,6 +210,26 @@ int rq_lora_grads(const void* x, const void* u, const void* dy, const void* z, i
 int rq_lora_grads_noalloc(const void* x, const void* u, const void* dy, const void* z, int64_t m,
                           int64_t k, int64_t n, int64_t rank, float scale, void* da, void* db,
                           void* stream);
+
+/* The whole QLoRA layer product over a quantized base in ONE launch
+ * (LoRALinear.__call__, rwkv_metal/lora/lora.py:58-63, and its dX under
+ * nn.value_and_grad, rwkv_metal/lora/finetune.py:141): the down-projection
+ * z = x . a^T is accumulated by the GEMM itself from the activation tiles it
+ * already holds, then
+ *   y = rq_qmm(x, ...) + scale * z . lora^T
+ * and z is also stored to z_out [m, rank] bf16 (if not NULL) for the
+ * backward.  Forward (transpose=1): a = lora_a [rank, cols], lora = lora_b
+ * [rows, rank], z_out = x . lora_a^T.  dX (transpose=0): a = lora_b^T
+ * [rank, rows], lora = lora_a^T [cols, rank], z_out = u = dY . lora_b.
+ * z is rounded once to bf16 before the term, as rq_lora_down + rq_qmm_lora
+ * do.  Covers rank 16 with 4- or 8-bit codes on the 64-wide-stage GEMMs
+ * (the conditions of rq_qmm_lora); other problems return RQ_EUNSUPPORTED and
+ * the caller runs rq_lora_down and rq_qmm_lora.  a, lora and z_out 16-byte
+ * aligned. */
+int rq_qlora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
+             const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
+             int group_size, int bits, int transpose, const void* a, const void* lora,
+             int64_t rank, float scale, void* z_out, void* y, rq_dtype y_dt, void* stream);
 
 /* Pack codes uint8[rows, cols] (values < 2^bits) into the MLX bitstream
  * w_q uint32[rows, cols*bits/32].  cols must be a multiple of 32. */

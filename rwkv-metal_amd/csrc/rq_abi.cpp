@@ -386,6 +386,37 @@ int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* s
     return launch_status(e, "rq_qmm_lora");
 }
 
+int rq_qlora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
+             const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
+             int group_size, int bits, int transpose, const void* a, const void* lora,
+             int64_t rank, float scale, void* z_out, void* y, rq_dtype y_dt, void* stream) {
+    if (int rc = check_common(rows, cols, group_size, bits)) return rc;
+    if (!valid_dt(x_dt) || !valid_dt(sb_dt) || !valid_dt(y_dt)) return fail(RQ_EINVAL, "unsupported dtype");
+    if (m < 0) return fail(RQ_EINVAL, "negative m");
+    if (rank < 16 || rank > 64 || rank % 16)
+        return fail(RQ_EINVAL, "rq_qlora: rank must be 16, 32, 48 or 64 (got %lld)", (long long)rank);
+    const int64_t n_out = transpose ? rows : cols, n_in = transpose ? cols : rows;
+    if (m == 0 || n_out == 0) return ok();
+    if (n_in == 0) return fail(RQ_EINVAL, "rq_qlora: empty contraction is not supported");
+    if (!x || !w_q || !scales || !biases || !y || !a || !lora)
+        return fail(RQ_EINVAL, "rq_qlora: NULL pointer");
+    if (!aligned16(x) || !aligned16(w_q) || !aligned16(a) || !aligned16(lora) || !aligned16(z_out))
+        return fail(RQ_EALIGN, "rq_qlora: x, w_q, a, lora and z_out must be 16-byte aligned");
+    rq::LoraArgs lo{nullptr, lora, (int)rank, scale};
+    lo.a = a;
+    lo.z_out = z_out;
+    lo.a_ld = n_in;
+    const hipError_t e = rq::launch_qmm(transpose, x, x_dt, w_q, scales, biases, sb_dt, m, rows,
+                                        cols, group_size, bits, y, y_dt, (hipStream_t)stream, &lo);
+    if (e == hipErrorNotSupported)
+        return fail(RQ_EUNSUPPORTED,
+                    "rq_qlora: the in-kernel down-projection covers rank 16 with 4- or 8-bit codes "
+                    "on the 64-wide-stage GEMMs (bf16 x, m >= 256, 16-bit 16-byte aligned scales; "
+                    "transpose=1: cols a multiple of 8 groups; transpose=0: rows %% 64 == 0, "
+                    "cols %% 128 == 0); use rq_lora_down and rq_qmm_lora");
+    return launch_status(e, "rq_qlora");
+}
+
 static int check_grouped(const char* what, const rq_problem* problems, int n, rq_dtype x_dt,
                          rq_dtype sb_dt, rq_dtype y_dt, int64_t m, int group_size, int bits) {
     if (n < 0 || (n > 0 && !problems)) return fail(RQ_EINVAL, "%s: bad problem list", what);

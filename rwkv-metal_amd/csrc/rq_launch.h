@@ -66,6 +66,13 @@ struct LoraArgs {
     const void* l;
     int rank;
     float scale;
+    // In-kernel down-projection (rank 16): z = act . a^T is accumulated by the
+    // GEMM's MFMA waves from the activation fragments they already hold (a:
+    // [16, a_ld] bf16, a_ld the contraction length) instead of being read
+    // from `z`, and written to z_out [m, 16] (if not NULL).
+    const void* a = nullptr;
+    void* z_out = nullptr;
+    int64_t a_ld = 0;
 };
 
 // Low-rank down-projection z[m, rank] = x[m, k] . a[rank, k]^T, bf16 (rank

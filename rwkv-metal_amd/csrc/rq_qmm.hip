@@ -996,6 +996,66 @@ RQ_DEV void lora_epilogue(f32x4_t (&acc)[TM][TN], const rq::LoraArgs& lo, int64_
     }
 }
 
+// The fused QLoRA layer's down-projection, computed in the GEMM (rank 16).
+// Each MFMA wave of a (wm) pair accumulated z over the k-steps h == wn of
+// every stage (accz: lane (lg, lr) holds row lr of 16-row tile a, ranks
+// 4 lg .. +3) from the activation fragments of its main MFMAs.  Once the
+// ring slots are free (a barrier every wave of the block joins), the pair's
+// fp32 partials are exchanged through one slot (zx: [4 waves][rows][16]),
+// summed in the same order by both waves, rounded once to bf16, stored to
+// z_out by the column-tile-0 blocks (one wave of the pair), and the term
+// scale * z . L^T is added to acc (L [ncols, 16] bf16 from global memory).
+template <int TM, int TN>
+RQ_DEV void fused_lora_tail(f32x4_t (&acc)[TM][TN], const f32x4_t (&accz)[TM], float* zx, int wm,
+                            int wn, int lane, const rq::LoraArgs& lo, bool write_z, int64_t nrows,
+                            int64_t ncols, int64_t r0, int64_t c0) {
+    const int lg = lane >> 4, lr = lane & 15;
+    constexpr int ROWS = TM * 16;
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+        *(f32x4_t*)(zx + ((wm * 2 + wn) * ROWS + a * 16 + lr) * 16 + 4 * lg) = accz[a];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partials are in LDS
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();        // the pair's partials are visible (every wave joins)
+    asm volatile("" ::: "memory");
+    bf16x8_t zf[TM];
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+        u32x4_t v = {0u, 0u, 0u, 0u};
+        if (lg < 2) {
+            const float* p0 = zx + ((wm * 2) * ROWS + a * 16 + lr) * 16 + 8 * lg;
+            const float* p1 = p0 + ROWS * 16;
+            const f32x4_t a0 = *(const f32x4_t*)p0, a1 = *(const f32x4_t*)(p0 + 4);
+            const f32x4_t b0 = *(const f32x4_t*)p1, b1 = *(const f32x4_t*)(p1 + 4);
+            v = u32x4_t{pack_bf16x2(a0[0] + b0[0], a0[1] + b0[1]),
+                        pack_bf16x2(a0[2] + b0[2], a0[3] + b0[3]),
+                        pack_bf16x2(a1[0] + b1[0], a1[1] + b1[1]),
+                        pack_bf16x2(a1[2] + b1[2], a1[3] + b1[3])};
+            const int64_t m = r0 + a * 16 + lr;
+            if (write_z && m < nrows) *(u32x4_t*)((uint16_t*)lo.z_out + m * 16 + 8 * lg) = v;
+        }
+        zf[a] = __builtin_bit_cast(bf16x8_t, v);
+    }
+    const uint16_t* l = (const uint16_t*)lo.l;
+    bf16x8_t lf[TN];
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+        const int64_t n = c0 + b * 16 + lr;
+        u32x4_t v = {0u, 0u, 0u, 0u};
+        if (lg < 2 && n < ncols) v = *(const u32x4_t*)(l + n * 16 + 8 * lg);
+        lf[b] = __builtin_bit_cast(bf16x8_t, v);
+    }
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const f32x4_t t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                lf[b], zf[a], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(lo.scale, t[r], acc[a][b][r]);
+        }
+}
+
 // ------------------------------------------------------------- qmm_t_k64
 //
 // The warp-specialised GEMM with 64-element contraction stages (bf16
@@ -1022,7 +1082,7 @@ RQ_DEV void lora_epilogue(f32x4_t (&acc)[TM][TN], const rq::LoraArgs& lo, int64_
 //    software-pipelined by hand (B fragments of the next k-step and A
 //    fragments two MFMA groups ahead), with scheduling barriers keeping the
 //    order: the compiler's own order waited on every fragment read.
-template <int BITS, int SDT, int BN, int GSH, int BM>
+template <int BITS, int SDT, int BN, int GSH, int BM, bool FZ = false>
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, void* __restrict__ y,
@@ -1198,6 +1258,12 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                 asm volatile("" ::: "memory");
             }
         }
+        if constexpr (FZ) {
+            // the MFMA waves' two barriers of the down-projection exchange
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+        }
         return;
     }
 
@@ -1224,6 +1290,20 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
 #pragma unroll
     for (int h = 0; h < 2; ++h)
         boff[h] = (uint32_t)((wn * WN + lr) * BLD + (((h * 4 + lg) ^ (lr & 7)) * 8));
+    // fused down-projection: this wave's 16 x 32 fragment of a (rank lr,
+    // columns 8 lg .. +7 of k-step h == wn) for the current and next stage
+    f32x4_t accz[TM];
+    u32x4_t zfa_cur = {0u, 0u, 0u, 0u}, zfa_nxt = zfa_cur;
+    const uint16_t* zarow = nullptr;
+    // wn as a wave-uniform (scalar) value: the k-step this wave projects is
+    // chosen by a scalar branch, since an EXEC-masked MFMA still runs
+    const int wn_s = __builtin_amdgcn_readfirstlane(wn);
+    if constexpr (FZ) {
+#pragma unroll
+        for (int a = 0; a < TM; ++a) accz[a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        zarow = (const uint16_t*)lora.a + (int64_t)lr * lora.a_ld + 32 * wn + 8 * lg;
+        zfa_nxt = *(const u32x4_t*)zarow;
+    }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();  // the producers' prologue barrier
     asm volatile("" ::: "memory");
@@ -1239,6 +1319,10 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
             if (st < nst) {
                 const uint8_t* xs = (u & 1) ? xs1 : xs0;
                 const uint16_t* bq = (u & 1) ? bq1 : bq0;
+                if constexpr (FZ) {
+                    zfa_cur = zfa_nxt;
+                    if (st + 1 < nst) zfa_nxt = *(const u32x4_t*)(zarow + (int64_t)(st + 1) * 64);
+                }
                 // software pipeline over (h, a): B fragments of k-step h+1 are read
                 // while k-step h runs; A fragments rotate through 3 registers, read
                 // 2 MFMA groups (10 MFMAs) ahead of their use.
@@ -1268,6 +1352,12 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                         for (int b = 0; b < TN; ++b)
                             acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[h][b], af[(h * TM + a) % 3],
                                                                                 acc[a][b], 0, 0, 0);
+                        if constexpr (FZ) {
+                            if (h == wn_s)  // a scalar branch: MFMAs ignore the EXEC mask
+                                accz[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                    __builtin_bit_cast(bf16x8_t, zfa_cur), af[(h * TM + a) % 3],
+                                    accz[a], 0, 0, 0);
+                        }
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
@@ -1277,7 +1367,17 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
 
     // after the last barrier the ring slot of stage nst - 2 (nst & 1) is read
     // by nobody and written by nobody: 8 KB of it per wave stage the output
-    if (lora.z) lora_epilogue<TM, TN>(acc, lora, M, R, m0 + wm * (BM / 2), n0 + wn * WN, lane);
+    if constexpr (FZ) {
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // every wave is done with both ring slots
+        asm volatile("" ::: "memory");
+        fused_lora_tail<TM, TN>(acc, accz, (float*)((nst & 1) ? xs0 : xs1), wm, wn, lane, lora,
+                                lora.z_out != nullptr && nt == 0 && wn == 0, M, R,
+                                m0 + wm * (BM / 2), n0 + wn * WN);
+    } else if (lora.z) {
+        lora_epilogue<TM, TN>(acc, lora, M, R, m0 + wm * (BM / 2), n0 + wn * WN, lane);
+    }
     // strips of 32 rows (BM 256: 8 KB of the free slot per wave) or 16 (BM 128: 4 KB)
     constexpr int SA = BM == 256 ? 2 : 1;
     static_assert(16 * SA * (BN + 16) <= BM * 32, "a wave's staging strip fits its share of a slot");
@@ -1313,7 +1413,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
 // Requires 16-bit scales, R % 64 == 0 and K % 128 == 0.
 RQ_DEV int nkey(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
-template <int BITS, int SDT>
+template <int BITS, int SDT, bool FZ = false>
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
@@ -1417,6 +1517,12 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                 asm volatile("" ::: "memory");
             }
         }
+        if constexpr (FZ) {
+            // the MFMA waves' two barriers of the down-projection exchange
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+        }
         return;
     }
 
@@ -1451,6 +1557,19 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
         }
     typedef short s16x4_t __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_p;
+    // fused down-projection (u = dY . B with a = B^T [16, R]): as in qmm_t_k64
+    f32x4_t accz[TM];
+    u32x4_t zfa_cur = {0u, 0u, 0u, 0u}, zfa_nxt = zfa_cur;
+    const uint16_t* zarow = nullptr;
+    // wn as a wave-uniform (scalar) value: the k-step this wave projects is
+    // chosen by a scalar branch, since an EXEC-masked MFMA still runs
+    const int wn_s = __builtin_amdgcn_readfirstlane(wn);
+    if constexpr (FZ) {
+#pragma unroll
+        for (int a = 0; a < TM; ++a) accz[a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        zarow = (const uint16_t*)lora.a + (int64_t)lr * lora.a_ld + 32 * wn + 8 * lg;
+        zfa_nxt = *(const u32x4_t*)zarow;
+    }
 
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();  // the producers' initial barrier
@@ -1466,6 +1585,10 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
             if (st < nst) {
                 const uint8_t* xs = u ? xs1 : xs0;
                 uint8_t* bq = u ? bq1 : bq0;
+                if constexpr (FZ) {
+                    zfa_cur = zfa_nxt;
+                    if (st + 1 < nst) zfa_nxt = *(const u32x4_t*)(zarow + (int64_t)(st + 1) * 64);
+                }
                 // fragments software-pipelined as in qmm_t_k64
                 bf16x8_t bf[2][TN], af[3];
                 auto rdA = [&](int h, int a) {
@@ -1499,6 +1622,12 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                         for (int b = 0; b < TN; ++b)
                             acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                                 bf[h][b], af[(h * TM + a) % 3], acc[a][b], 0, 0, 0);
+                        if constexpr (FZ) {
+                            if (h == wn_s)  // a scalar branch: MFMAs ignore the EXEC mask
+                                accz[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                    __builtin_bit_cast(bf16x8_t, zfa_cur), af[(h * TM + a) % 3],
+                                    accz[a], 0, 0, 0);
+                        }
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
@@ -1507,7 +1636,17 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
     }
 
     // after the last barrier the ring slot of stage nst - 2 (nst & 1) is free
-    if (lora.z) lora_epilogue<TM, TN>(acc, lora, M, K, m0 + wm * 128, k0 + wn * WN, lane);
+    if constexpr (FZ) {
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // every wave is done with both ring slots
+        asm volatile("" ::: "memory");
+        fused_lora_tail<TM, TN>(acc, accz, (float*)((nst & 1) ? xs0 : xs1), wm, wn, lane, lora,
+                                lora.z_out != nullptr && k0 == 0 && wn == 0, M, K, m0 + wm * 128,
+                                k0 + wn * WN);
+    } else if (lora.z) {
+        lora_epilogue<TM, TN>(acc, lora, M, K, m0 + wm * 128, k0 + wn * WN, lane);
+    }
     store_wave_tile<TM, TN>(acc, ((nst & 1) ? xs1 : xs0) + wave * 8192, y, y_dt, M, K,
                             m0 + wm * 128, k0 + wn * WN, lane);
 }
@@ -1525,9 +1664,42 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
                                       int y_dt, hipStream_t stream, const LoraArgs* lora) {
     const int gs_shift = __builtin_ctz(gs);
     const LoraArgs lo = lora ? *lora : LoraArgs{nullptr, nullptr, 0, 0.f};
+    const bool k64 = m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 &&
+                     cols % 64 == 0 && (cols / gs) % 8 == 0 &&
+                     (((uintptr_t)scales | (uintptr_t)biases) & 15) == 0;
+    if (lora && lora->a) {
+        // the fused QLoRA layer with its down-projection in the kernel: rank 16,
+        // 4- or 8-bit codes, 128-column tiles (the 160-column ones have no
+        // registers left for the extra accumulators)
+#if RQ_BITS == 4 || RQ_BITS == 8
+        if (!k64 || lora->rank != 16) return hipErrorNotSupported;
+        const int tn = (int)((rows + 127) / 128);
+        const int bm = ((m + 255) / 256) * tn < RQ_K64_BM128_BELOW ? 128 : 256;
+        const int tm = (int)((m + bm - 1) / bm);
+        const int blocks = ((tm * tn + 7) / 8) * 8;
+#define RQ_FZ_BM(SD, GSHV, BMV)                                                                   \
+    hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, 128, GSHV, BMV, true>), dim3(blocks),              \
+                       dim3(kWsBlock), 0, stream, (const uint16_t*)x, wq, scales, biases, m, rows, \
+                       cols, y, y_dt, tm, tn, lo)
+#define RQ_FZ(SD, GSHV) \
+    if (bm == 256) { RQ_FZ_BM(SD, GSHV, 256); } else { RQ_FZ_BM(SD, GSHV, 128); }
+#define RQ_FZ_GS(SD)                          \
+    switch (gs_shift) {                       \
+        case 5: RQ_FZ(SD, 5); break;          \
+        case 6: RQ_FZ(SD, 6); break;          \
+        default: RQ_FZ(SD, 7); break;         \
+    }
+        if (sb_dt == RQ_BF16) { RQ_FZ_GS(RQ_BF16) } else { RQ_FZ_GS(RQ_F16) }
+#undef RQ_FZ_GS
+#undef RQ_FZ
+#undef RQ_FZ_BM
+        return hipGetLastError();
+#else
+        return hipErrorNotSupported;
+#endif
+    }
     // 64-wide stages: 16-bit 16-byte aligned scales, whole 8-group chunks
-    if (m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 && cols % 64 == 0 &&
-        (cols / gs) % 8 == 0 && (((uintptr_t)scales | (uintptr_t)biases) & 15) == 0) {
+    if (k64) {
         // 160-row tiles (whole rounds over 256 CUs for the 2560-wide RWKV-7 shapes) split
         // evenly into 8-code dequant jobs only at 4 bits
         int bn = (RQ_BITS == 4 && rows % 160 == 0) ? 160 : 128;
@@ -1632,9 +1804,31 @@ hipError_t RQ_CAT(launch_qmm_n_b, RQ_BITS)(const void* x, int x_dt, const uint32
     const LoraArgs lo = lora ? *lora : LoraArgs{nullptr, nullptr, 0, 0.f};
     // warp-specialised transposed GEMM: bf16 dY, 16-bit aligned scales,
     // whole stages of 64 weight rows and 128 output columns
-    if (m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 && rows % 64 == 0 &&
-        cols % 128 == 0 && ((uintptr_t)x & 15) == 0 &&
-        (((uintptr_t)scales | (uintptr_t)biases) & 7) == 0) {
+    const bool k64 = m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 &&
+                     rows % 64 == 0 && cols % 128 == 0 && ((uintptr_t)x & 15) == 0 &&
+                     (((uintptr_t)scales | (uintptr_t)biases) & 7) == 0;
+    if (lora && lora->a) {
+        // the fused QLoRA layer's dX with u = dY . B in the kernel (rank 16,
+        // 4- or 8-bit codes)
+#if RQ_BITS == 4 || RQ_BITS == 8
+        if (!k64 || lora->rank != 16) return hipErrorNotSupported;
+        const int tm = (int)((m + 255) / 256);
+        const int tn = (int)(cols / 128);
+        const int blocks = ((tm * tn + 7) / 8) * 8;
+        if (sb_dt == RQ_BF16)
+            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_BF16, true>), dim3(blocks), dim3(kWsBlock), 0,
+                               stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
+                               __builtin_ctz(gs), y, y_dt, tm, tn, lo);
+        else
+            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_F16, true>), dim3(blocks), dim3(kWsBlock), 0,
+                               stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
+                               __builtin_ctz(gs), y, y_dt, tm, tn, lo);
+        return hipGetLastError();
+#else
+        return hipErrorNotSupported;
+#endif
+    }
+    if (k64) {
         const int tm = (int)((m + 255) / 256);
         const int tn = (int)(cols / 128);
         const int blocks = ((tm * tn + 7) / 8) * 8;

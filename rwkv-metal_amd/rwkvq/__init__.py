@@ -11,7 +11,7 @@ add_lora_rwkvq, load_sidecar.
 All compute runs in librwkvq_hip.so; tensors must be on the GPU.
 """
 from .ops import (VALID_BITS, VALID_GROUP_SIZES, BoundQmm, GroupedQmv, dequantize, grouped_qmv,
-                  lora_down, lora_grads, pack_codes, quantize, quantized_embedding, quantized_matmul,
+                  lora_down, lora_grads, pack_codes, qlora_fused, quantize, quantized_embedding, quantized_matmul,
                   quantized_matmul_lora, unpack_codes)
 from .nn import QuantizedEmbedding, QuantizedLinear, is_quantizable
 from .nn import quantize as quantize_model
@@ -22,7 +22,7 @@ from .lora import (BIG_QUANT_TARGETS, CMIX_TARGETS, TMIX_TARGETS, LoRALinear, ad
 
 __all__ = [
     "VALID_BITS", "VALID_GROUP_SIZES", "quantize", "dequantize", "quantized_matmul",
-    "quantized_embedding", "quantized_matmul_lora", "lora_down", "lora_grads",
+    "quantized_embedding", "quantized_matmul_lora", "lora_down", "lora_grads", "qlora_fused",
     "pack_codes", "unpack_codes", "grouped_qmv", "GroupedQmv", "BoundQmm", "QuantizedLinear", "QuantizedEmbedding",
     "is_quantizable", "quantize_model", "BIG_QUANT_TARGETS", "TMIX_TARGETS", "CMIX_TARGETS",
     "LoRALinear", "add_lora", "quantize_base_model", "lora_state", "save_lora", "load_lora",

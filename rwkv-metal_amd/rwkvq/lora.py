@@ -44,17 +44,25 @@ def _promote(a: torch.dtype, b: torch.dtype) -> torch.dtype:
 
 class _QLoRAFunction(torch.autograd.Function):
     """y = base(x) + scale * (x A^T) B^T over a QuantizedLinear base with the
-    low-rank term fused into the packed-weight GEMMs (rq_qmm_lora):
-    forward adds z B^T (z = x A^T) in the transpose=True GEMM's output stage;
-    backward computes u = dY B, dX = dY . W^ + scale * u A in the transpose=False
-    GEMM's output stage, and dA = scale * u^T x, dB = scale * dY^T z in one
-    rq_lora_grads launch.  The frozen base gets no gradient."""
+    low-rank term fused into the packed-weight GEMMs.  Rank 16 at 4 or 8 bits
+    (rq_qlora): the forward is one launch that also computes z = x A^T
+    inside the transpose=True GEMM and adds z B^T in its output stage; dX is
+    one launch that computes u = dY B inside the transpose=False GEMM and adds
+    scale * u A; dA = scale * u^T x and dB = scale * dY^T z are one
+    rq_lora_grads launch.  Other ranks run z and u as rq_lora_down launches
+    and the term with rq_qmm_lora.  The frozen base gets no gradient."""
 
     @staticmethod
     def forward(ctx, x2, lora_a, lora_b, base, scale):
-        z = ops.lora_down(x2, lora_a)
-        y = ops.quantized_matmul_lora(x2, base.weight, base.scales, base.biases, z, lora_b, scale,
-                                      True, base.group_size, base.bits)
+        gs, bits = base.group_size, base.bits
+        yz = ops.qlora_fused(x2, base.weight, base.scales, base.biases, lora_a, lora_b, scale,
+                             True, gs, bits)
+        if yz is not None:
+            y, z = yz      # one launch: z = x A^T inside the GEMM
+        else:
+            z = ops.lora_down(x2, lora_a)
+            y = ops.quantized_matmul_lora(x2, base.weight, base.scales, base.biases, z, lora_b,
+                                          scale, True, gs, bits)
         ctx.save_for_backward(x2, z, lora_a, lora_b)
         ctx.base, ctx.scale = base, scale
         return y
@@ -63,13 +71,24 @@ class _QLoRAFunction(torch.autograd.Function):
     def backward(ctx, dy):
         x2, z, lora_a, lora_b = ctx.saved_tensors
         base, scale = ctx.base, ctx.scale
+        gs, bits = base.group_size, base.bits
         dy = dy.contiguous().to(x2.dtype)
-        u = ops.lora_down(dy, lora_b.t().contiguous())
+        bt = lora_b.t().contiguous()
         dx = da = db = None
+        dxu = None
         if ctx.needs_input_grad[0]:
-            dx = ops.quantized_matmul_lora(dy, base.weight, base.scales, base.biases, u,
-                                           lora_a.t().contiguous(), scale, False, base.group_size,
-                                           base.bits).to(x2.dtype)
+            at = lora_a.t().contiguous()
+            dxu = ops.qlora_fused(dy, base.weight, base.scales, base.biases, bt, at, scale, False,
+                                  gs, bits)
+            if dxu is not None:
+                dx, u = dxu  # one launch: u = dY B inside the GEMM
+            else:
+                u = ops.lora_down(dy, bt)
+                dx = ops.quantized_matmul_lora(dy, base.weight, base.scales, base.biases, u, at,
+                                               scale, False, gs, bits)
+            dx = dx.to(x2.dtype)
+        else:
+            u = ops.lora_down(dy, bt)
         # both adapter gradients in one launch, fp32 accumulation, one rounding
         want_a, want_b = ctx.needs_input_grad[1], ctx.needs_input_grad[2]
         da, db = ops.lora_grads(x2 if want_a else None, u if want_a else None,

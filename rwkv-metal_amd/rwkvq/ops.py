@@ -426,6 +426,44 @@ def _qmm_lora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, z: T
     return y
 
 
+def qlora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, a: Tensor,
+                lora: Tensor, scale: float, transpose: bool = True, group_size: int = 64,
+                bits: int = 4):
+    """The QLoRA layer product in one rq_qlora launch, its down-projection
+    inside the GEMM: (y, z) with z = x @ a^T [m, rank] (bf16) and
+    y = quantized_matmul(x, ...) + scale * z @ lora^T.  Forward: a = lora_a,
+    lora = lora_b; dX: a = lora_b^T, lora = lora_a^T (transpose=False), z is
+    then u = dY @ lora_b.  x is 2-D.  None where the fused kernels do not
+    apply (see rq_qlora); no autograd (rwkvq.lora differentiates the layer)."""
+    _check_args(group_size, bits)
+    w_q = _words(w_q)
+    K = _check_packed(w_q, scales, biases, group_size, bits)
+    n_in, n_out = (K, w_q.shape[0]) if transpose else (w_q.shape[0], K)
+    rank = a.shape[0]
+    if (x.dim() != 2 or x.shape[1] != n_in or tuple(a.shape) != (rank, n_in)
+            or tuple(lora.shape) != (n_out, rank)):
+        raise ValueError("qlora_fused: x, a and lora shapes do not agree")
+    if not (x.dtype == a.dtype == lora.dtype == torch.bfloat16) or rank != 16:
+        return None
+    _on_gpu(x, w_q, scales, biases, a, lora)
+    x, w_q, scales, a, lora = _ready(x), _ready(w_q), _ready(scales), _ready(a), _ready(lora)
+    biases = _ready(biases.to(scales.dtype))
+    m = x.shape[0]
+    y = torch.empty(m, n_out, dtype=_promote(x.dtype, scales.dtype), device=x.device)
+    z = torch.empty(m, rank, dtype=torch.bfloat16, device=x.device)
+    if m == 0:
+        return y, z
+    with _DeviceGuard(x.device):
+        rc = lib().rq_qlora(_ptr(x), DTYPE_CODE[x.dtype], _ptr(w_q), _ptr(scales), _ptr(biases),
+                            DTYPE_CODE[scales.dtype], m, w_q.shape[0], K, group_size, bits,
+                            1 if transpose else 0, _ptr(a), _ptr(lora), rank, float(scale),
+                            _ptr(z), _ptr(y), DTYPE_CODE[y.dtype], _stream(x))
+    if rc == RQ_EUNSUPPORTED:
+        return None
+    check(rc, "qlora_fused")
+    return y, z
+
+
 def quantized_matmul_lora(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, z: Tensor,
                           lora: Tensor, scale: float, transpose: bool = True,
                           group_size: int = 64, bits: int = 4) -> Tensor:

@@ -29,7 +29,7 @@ def test_header_declares_the_expected_surface():
         "rq_pack", "rq_unpack", "rq_qmm_grouped", "rq_grouped_plan_table_bytes",
         "rq_grouped_plan_init", "rq_grouped_plan_run", "rq_embedding", "rq_sb6_dequantize",
         "rq_sb6_to_affine", "rq_qmm_lora", "rq_lora_down", "rq_lora_grads_workspace_bytes",
-        "rq_lora_grads", "rq_lora_grads_noalloc"])
+        "rq_lora_grads", "rq_lora_grads_noalloc", "rq_qlora"])
 
 
 def test_library_exports_every_declared_symbol(L):

@@ -68,3 +68,111 @@ def test_lora_grads_empty_contraction_is_zero(rq, dev):
     da, db = ops.lora_grads(x, u, dy, z, 1.0)
     assert da.shape == (16, 256) and db.shape == (128, 16)
     assert not da.float().abs().any() and not db.float().abs().any()
+
+
+# ------------------------------------------------ one-launch QLoRA products
+
+def _wdense(rq, wq, s, b, gs, bits):
+    """fp32 s*q + b from the (bit-exact) unpacked codes: [R, K]."""
+    q = rq.unpack_codes(wq, bits).float()
+    return q * s.float().repeat_interleave(gs, 1) + b.float().repeat_interleave(gs, 1)
+
+
+def _dense(rq, x, wq, s, b, gs, bits, transpose):
+    wd = _wdense(rq, wq, s, b, gs, bits)
+    return x.float() @ (wd.t() if transpose else wd)
+
+
+# (transpose, M, R, K, bits, gs, scales dtype): 256- and 128-row tiles,
+# partial row and column tiles, 4 and 8 bits, every group size, f16 scales
+QLORA_CASES = [
+    (True, 4096, 2048, 2048, 4, 64, torch.bfloat16),
+    (True, 4096, 8192, 2048, 4, 64, torch.bfloat16),
+    (True, 4096, 2048, 8192, 4, 64, torch.bfloat16),
+    (True, 1000, 520, 1024, 4, 128, torch.bfloat16),
+    (True, 300, 2048, 512, 8, 32, torch.float16),
+    (False, 4096, 2048, 2048, 4, 64, torch.bfloat16),
+    (False, 4096, 8192, 2048, 4, 64, torch.bfloat16),
+    (False, 4096, 2048, 8192, 4, 64, torch.bfloat16),
+    (False, 700, 320, 1024, 8, 128, torch.float16),
+    (False, 300, 256, 512, 4, 32, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("transpose,M,R,K,bits,gs,sdt", QLORA_CASES)
+def test_qlora_one_launch(rq, dev, transpose, M, R, K, bits, gs, sdt):
+    """rq_qlora: z = x a^T computed inside the GEMM (rounded once to bf16,
+    stored for the backward) and y = qmm(x) + scale * z lora^T, against fp32
+    products of the same bf16 operands."""
+    from rwkvq import ops
+    say(f"qlora one launch t={transpose} M={M} R={R} K={K} b={bits} gs={gs} s={sdt}")
+    wq, s, b = rq.quantize(weights(R, K, 70_000 + R + K, sdt).to(dev), gs, bits)
+    n_in, n_out = (K, R) if transpose else (R, K)
+    g = torch.Generator().manual_seed(M + R + K)
+    x = acts(M, n_in, M + K).to(dev)
+    a = (torch.randn(16, n_in, generator=g) / n_in ** 0.5).to(torch.bfloat16).to(dev)
+    L = (torch.randn(n_out, 16, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    yz = ops.qlora_fused(x, wq, s, b, a, L, 0.75, transpose, gs, bits)
+    assert yz is not None, "this problem must run the one-launch kernels"
+    y, z = yz
+    zref = x.float() @ a.float().t()
+    rel_check(z, zref, what="z")
+    # the term uses z rounded to bf16, as the two-launch path does
+    ref = _dense(rq, x, wq, s, b, gs, bits, transpose) + 0.75 * (z.float() @ L.float().t())
+    rel_check(y, ref, what="y")
+    # and the two-launch path gives the same product within the bar
+    y2 = ops.quantized_matmul_lora(x, wq, s, b, ops.lora_down(x, a), L, 0.75, transpose, gs, bits)
+    rel_check(y, y2.float(), what="y vs lora_down + rq_qmm_lora")
+
+
+def test_qlora_one_launch_declines_other_ranks_and_bits(rq, dev):
+    from rwkvq import ops
+    wq, s, b = rq.quantize(weights(256, 512, 3).to(dev), 64, 3)
+    x = acts(512, 512, 3).to(dev)
+    a = torch.zeros(16, 512, dtype=torch.bfloat16, device=dev)
+    L = torch.zeros(256, 16, dtype=torch.bfloat16, device=dev)
+    assert ops.qlora_fused(x, wq, s, b, a, L, 1.0, True, 64, 3) is None        # 3-bit codes
+    wq, s, b = rq.quantize(weights(256, 512, 4).to(dev), 64, 4)
+    a32 = torch.zeros(32, 512, dtype=torch.bfloat16, device=dev)
+    L32 = torch.zeros(256, 32, dtype=torch.bfloat16, device=dev)
+    assert ops.qlora_fused(x, wq, s, b, a32, L32, 1.0, True, 64, 4) is None    # rank 32
+    assert ops.qlora_fused(x[:100], wq, s, b, a, L, 1.0, True, 64, 4) is None  # m < 256
+
+
+def test_config4_qlora_layer_step_full_size(rq, dev):
+    """BASELINE config 4 at full size: one RWKV-7 1.5B layer (D = 2048) on a
+    frozen 4-bit g64 base, 8 x 512 tokens, r = alpha = 16, A ~ N(0, 1/D),
+    B ~ N(0, 0.01) (std); for each of r, k, v, o, ffn_key and ffn_value the
+    forward y = qmm(x, Wq) + (alpha / r) (x A^T) B^T and the gradients dX, dA,
+    dB against an fp32 dense reference on the dequantized base.  Every
+    projection runs the one-launch forward and dX kernels and one
+    adapter-gradient launch."""
+    D, F, r, alpha = 2048, 8192, 16, 16.0
+    for i, (name, R, K) in enumerate([("r", D, D), ("k", D, D), ("v", D, D), ("o", D, D),
+                                      ("ffn_key", F, D), ("ffn_value", D, F)]):
+        say(f"config4 layer step {name} [{R},{K}]")
+        base = rq.QuantizedLinear(K, R, bias=False, group_size=64, bits=4, device=dev)
+        wq, s, b = rq.quantize(weights(R, K, 4_000_000 + 1000 + i).to(dev), 64, 4)
+        base.weight, base.scales, base.biases = wq, s, b
+        lay = rq.LoRALinear(rank=r, alpha=alpha, base_module=base)
+        g = torch.Generator().manual_seed(4_000_600 + i)
+        with torch.no_grad():
+            lay.lora_a.copy_((torch.randn(r, K, generator=g) / K ** 0.5).to(torch.bfloat16))
+            lay.lora_b.copy_((torch.randn(R, r, generator=g) * 0.01).to(torch.bfloat16))
+        x = acts(8 * 512, K, 4_000_000 + i).to(dev).reshape(8, 512, K).requires_grad_(True)
+        dy = acts(8 * 512, R, 4_000_800 + i).to(dev).reshape(8, 512, R)
+        from rwkvq import ops
+        assert ops.qlora_fused(x.detach().reshape(-1, K), wq, s, b, lay.lora_a.detach(),
+                               lay.lora_b.detach(), 1.0, True, 64, 4) is not None
+        y = lay(x)
+        dx, da, db = torch.autograd.grad(y, (x, lay.lora_a, lay.lora_b), dy)
+        wd = _wdense(rq, wq, s, b, 64, 4)
+        xr = x.detach().float().reshape(-1, K).requires_grad_(True)
+        A = lay.lora_a.detach().float().requires_grad_(True)
+        B = lay.lora_b.detach().float().requires_grad_(True)
+        yr = xr @ wd.t() + (alpha / r) * ((xr @ A.t()) @ B.t())
+        yr.backward(dy.float().reshape(-1, R))
+        rel_check(y.reshape(-1, R), yr, what=f"{name} y")
+        rel_check(dx.reshape(-1, K), xr.grad, what=f"{name} dX")
+        rel_check(da, A.grad, what=f"{name} dA")
+        rel_check(db, B.grad, what=f"{name} dB")
