@@ -47,12 +47,16 @@
 //  * The activation rows x[0..M) of the block's problem are staged once in
 //    LDS as bf16; A operands are read from there for every span, so only
 //    packed codes (and their scales) live in registers: a wave issues the
-//    loads of NS spans at once and consumes them in order.  Packed codes use
-//    non-temporal loads (they are read once).
+//    loads of NS spans at once and consumes them in order.
 //    When M*K*2 bytes exceed the LDS budget, A comes from global memory.
 //  * One launch can cover many independent problems (rq_qmm_grouped): a
 //    block finds its problem by binary search in a prefix table of block
 //    counts held in the kernel arguments.
+//
+// The kernels: qmv_kernel (above: any layout), and for 16-bit scales the
+// streamed qmv_stream_* (m <= 4) and qmv_wide_* (4 < m <= 16) for launches
+// that fill the GPU with rows, and qmv_split for small launches (one memory
+// round trip per launch); each is described where it is defined.
 
 #include "rq_common.h"
 #include "rq_launch.h"
@@ -88,6 +92,9 @@ constexpr int kBlock = 64 * kWaves;
 #endif
 #ifndef RQ_QMV_STREAM
 #define RQ_QMV_STREAM 1  // 0: never use the streamed-scale GEMV
+#endif
+#ifndef RQ_QMV_SPLIT
+#define RQ_QMV_SPLIT 1  // 0: never use the split GEMV (small launches)
 #endif
 #ifndef RQ_QMV_BIG_MIN
 #define RQ_QMV_BIG_MIN 16384  // 16-row blocks in a launch from which RQ_QMV_BIG_RB applies
@@ -1046,6 +1053,286 @@ __global__ __launch_bounds__(kBlock) RQ_STREAM_OCC void qmv_stream_table(const r
     qmv_stream_body<BITS, SDT, NMC, MI, GSH>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
 }
 
+// ------------------------------------------------------------ split GEMV
+//
+// qmv_split: the decode GEMV of launches too small to fill the GPU with rows
+// (one projection, or the few independent projections of one step of a
+// layer), where a launch costs its memory round trips rather than its bytes.
+//
+//  * A block is one 16-row tile; its KS waves split K into contiguous slices
+//    of NSW stages (a stage is 256 codes of the 16 rows, laid out as in the
+//    streamed GEMV: lane L holds the 64 codes 64(L/16).. of row L%16).
+//  * Every global load of a wave is issued before any is waited for: its
+//    slice of x (first, so that it can be staged while codes still arrive),
+//    the (scale, bias) values of its slice (lane groups 0/2 scales, 1/3
+//    biases, half a row each) and the codes of all its stages.  A wave
+//    stages x (pair-permuted bf16, plus activation sums) and its (scale,
+//    bias) values in a wave-private LDS region, so no barrier precedes the
+//    MFMAs; the arithmetic per stage is the streamed GEMV's.
+//  * The slices' per-row sums meet behind the block's only barrier; wave 0
+//    adds them in wave order (deterministic) and stores y.
+#ifndef RQ_SPLIT_WAVES
+#define RQ_SPLIT_WAVES 16  // most waves (K slices) per block
+#endif
+constexpr int kSplitMaxWaves = RQ_SPLIT_WAVES;
+constexpr int kSplitBlock = 64 * kSplitMaxWaves;
+
+template <int GSH>
+struct SplitSB {
+    static constexpr int SB1 = (256 >> GSH) * 2;  // bytes of one array per row and stage
+};
+
+// stages per wave: the fewest (a power of two) that need at most
+// kSplitMaxWaves waves; 0 if that exceeds 4 (not covered: at 16 waves per
+// block a wave may hold 128 VGPRs, and 8 stages of codes need more)
+__host__ __device__ inline int split_nsw(int64_t cols) {
+    const int64_t nst = cols >> 8;
+    for (int nsw = 1; nsw <= 4; nsw *= 2)
+        if (nst <= (int64_t)nsw * kSplitMaxWaves) return nsw;
+    return 0;
+}
+__host__ __device__ inline int split_wave_bytes(int m, int nsw, int gsh, int bits) {
+    const int xsh = gsh < 6 ? gsh : 6;
+    const int sbb = nsw * ((256 >> gsh) * 2);
+    return 128 + m * nsw * 512 + (bits == 3 ? 2 : 1) * m * ((nsw * 256) >> xsh) * 4 +
+           16 * (2 * sbb + 16);
+}
+
+template <int BITS, int SDT, int MI, int GSH, int NSW>
+__global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
+    static_assert(SDT != RQ_F32, "split GEMV scales are 16-bit");
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+    constexpr int XSH = GSH < 6 ? GSH : 6;
+    constexpr int NSUM = BITS == 3 ? 2 : 1;
+    constexpr int KW = NSW * 256;                 // codes per row in a wave's slice
+    constexpr int SBB = NSW * SplitSB<GSH>::SB1;  // bytes per row and array in a slice
+    constexpr int SBH = SBB / 2;                  // bytes of it one lane loads
+    // load width: at most 16 B and never across a stage, so that a short last
+    // slice loads exactly its own stages
+    constexpr int SBW = SBH < SplitSB<GSH>::SB1 ? SBH : (SplitSB<GSH>::SB1 < 16 ? SplitSB<GSH>::SB1 : 16);
+    constexpr int SBN = SBH / SBW;                // loads per lane
+    constexpr int ROWB = 2 * SBB + 16;
+    constexpr int XP = (MI * KW / 8 + 63) / 64;   // 8-element x pieces per lane (upper bound)
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lg = lane >> 4, lr = lane & 15;
+    const int bid = blockIdx.x;
+    int lo = 0, hi = args.n - 1;  // last problem whose first block <= bid
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (args.block_start[mid] <= bid) lo = mid; else hi = mid - 1;
+    }
+    const rq_problem& P = args.p[lo];
+    const int M = args.m, x_dt = args.x_dt;
+    const int64_t R = P.rows, K = P.cols;
+    const int nst = (int)(K >> 8);
+    const int st0 = wave * NSW;                                // first stage of this wave
+    const int nv = nst - st0 < NSW ? nst - st0 : NSW;          // its stages (>= 1)
+    const int64_t row0 = (int64_t)(bid - args.block_start[lo]) * 16;
+    const int64_t rowc = (row0 + lr) < R ? (row0 + lr) : R - 1;
+    const int64_t wpr = (K >> 5) * BITS;
+
+    // wave-private LDS: zero line | x slice [M][KW] | sums | (scale, bias) rows
+    const int wbytes = split_wave_bytes(M, NSW, GSH, BITS);
+    uint8_t* wl = lds8 + wave * wbytes;
+    uint16_t* xs = (uint16_t*)(wl + 128);
+    float* xsum = (float*)(wl + 128 + M * KW * 2);
+    const int gxw = KW >> XSH;  // sums per activation row in the slice
+    uint8_t* sbl = (uint8_t*)(xsum + NSUM * M * gxw);
+
+    // ---- issue every load: x slice, (scale, bias) values, codes
+    const int n8 = M * nv * 32;  // 8-element x pieces of the slice
+    XRaw xr[XP];
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        const int e = lane + 64 * i;
+        if (e < n8) {
+            const int m = e / (nv * 32), kk = (e - m * nv * 32) * 8;
+            xr[i] = load_x8(P.x, x_dt, ((int64_t)m * K + (int64_t)st0 * 256 + kk) >> 3);
+        }
+    }
+    const RQ_GLOBAL uint8_t* sbsrc =
+        (const RQ_GLOBAL uint8_t*)((lg & 1) ? P.biases : P.scales) +
+        (rowc * (K >> GSH)) * 2 + (int64_t)st0 * SplitSB<GSH>::SB1;
+    uint32_t sbv[(SBH + 3) / 4];
+#pragma unroll
+    for (int q = 0; q < SBN; ++q) {
+        // bytes past a short last slice are never read: load the slice start instead
+        const int off = (lg >> 1) * SBH + q * SBW;
+        const int so = off < nv * SplitSB<GSH>::SB1 ? off : 0;
+        if constexpr (SBW == 16) {
+            const u32x4_t v = *(const RQ_GLOBAL u32x4_t*)(sbsrc + so);
+            sbv[4 * q] = v[0]; sbv[4 * q + 1] = v[1]; sbv[4 * q + 2] = v[2]; sbv[4 * q + 3] = v[3];
+        } else if constexpr (SBW == 8) {
+            const u32x2_t v = *(const RQ_GLOBAL u32x2_t*)(sbsrc + so);
+            sbv[2 * q] = v[0]; sbv[2 * q + 1] = v[1];
+        } else if constexpr (SBW == 4) {
+            sbv[q] = *(const RQ_GLOBAL uint32_t*)(sbsrc + so);
+        } else {
+            sbv[0] = *(const RQ_GLOBAL uint16_t*)(sbsrc + so);
+        }
+    }
+    const gptr_u32 wqr = (gptr_u32)P.w_q + rowc * wpr + lg * 2 * BITS;
+    uint32_t cw[NSW][2 * BITS];
+#pragma unroll
+    for (int t = 0; t < NSW; ++t) {
+        const int sc = st0 + (t < nv ? t : 0);
+        load_two_runs<BITS>(wqr + sc * (8 * BITS), cw[t]);
+    }
+
+    // ---- stage x and its sums (waits for x only: it was requested first)
+    if (lane < 8) *(u32x4_t*)(wl + lane * 16) = u32x4_t{0u, 0u, 0u, 0u};
+    float* xlo = xsum + M * gxw;  // 3-bit: sums over the low-half positions
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        const int e = lane + 64 * i;
+        if (e < n8) {
+            const int m = e / (nv * 32), kk = (e - m * nv * 32) * 8;
+            uint32_t d[4];
+            x8_to_bf16(xr[i], x_dt, d);
+            uint32_t pr[4];
+            reorder_pairs(d, pr);
+            *(u32x4_t*)&xs[m * KW + kk] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
+            float sum = 0.f, lo4 = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float v = __uint_as_float(d[q] << 16) + __uint_as_float(d[q] & 0xffff0000u);
+                sum += v;
+                if (q < 2) lo4 += v;
+            }
+            // a sum covers 2^(XSH-3) consecutive pieces = consecutive lanes
+#pragma unroll
+            for (int w = 1; w < (1 << (XSH - 3)); w <<= 1) {
+                sum += __shfl_xor(sum, w, 64);
+                if constexpr (BITS == 3) lo4 += __shfl_xor(lo4, w, 64);
+            }
+            if ((e & ((1 << (XSH - 3)) - 1)) == 0) {
+                const int si = m * gxw + (kk >> XSH);
+                xsum[si] = sum;
+                if constexpr (BITS == 3) xlo[si] = lo4;
+            }
+        }
+    }
+    {   // (scale, bias) values of the slice: row lr, array lg&1, half lg>>1
+        uint8_t* dst = sbl + lr * ROWB + (lg & 1) * SBB + (lg >> 1) * SBH;
+#pragma unroll
+        for (int q = 0; q < SBN; ++q) {
+            if constexpr (SBW == 16)
+                *(u32x4_t*)(dst + 16 * q) = u32x4_t{sbv[4 * q], sbv[4 * q + 1], sbv[4 * q + 2], sbv[4 * q + 3]};
+            else if constexpr (SBW == 8)
+                *(u32x2_t*)(dst + 8 * q) = u32x2_t{sbv[2 * q], sbv[2 * q + 1]};
+            else if constexpr (SBW == 4)
+                *(uint32_t*)(dst + 4 * q) = sbv[q];
+            else
+                *(uint16_t*)dst = (uint16_t)sbv[0];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();  // LDS writes above are read by other lanes of this wave
+
+    // ---- per-lane constants (as in the streamed GEMV, on the slice)
+    const PairConsts kc = BITS == 3 ? pair3_consts() : pair_consts();
+    const int m_a = lr & 3;
+    const bool a_act = (lr >> 2) == lg && m_a < M;
+    const uint32_t a_base = a_act ? (uint32_t)(64 + m_a * KW + lg * 64) : 0u;  // in 16-bit units
+    const uint32_t a_step = a_act ? 256u : 0u;
+    constexpr int GL = GSH == 5 ? 2 : 1;
+    const int glane = GSH == 5 ? 2 * lg : (GSH == 6 ? lg : (lg >> 1));
+    const int xlane = GSH == 5 ? 2 * lg : lg;
+    const uint32_t xsum_f = (uint32_t)((128 + M * KW * 2) >> 2);  // float index of xsum in wl
+    uint32_t g_idx[MI], g_step[MI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+        const bool act = i < M;
+        g_idx[i] = act ? xsum_f + (uint32_t)(i * gxw + xlane) : 0u;
+        g_step[i] = act ? (uint32_t)(256 >> XSH) : 0u;
+    }
+    const uint8_t* sb_r = sbl + lr * ROWB + glane * 2;
+
+    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const uint16_t* wl16 = (const uint16_t*)wl;
+    const float* wlf = (const float*)wl;
+#pragma unroll
+    for (int t = 0; t < NSW; ++t) {
+        if (t < nv) {
+            float sc[GL], cb[GL], cl[GL];
+#pragma unroll
+            for (int q = 0; q < GL; ++q) {
+                const int gw = t * (256 >> GSH) + q;
+                sc[q] = raw_to_f32<SDT>(*(const uint16_t*)(sb_r + gw * 2));
+                const float bi = raw_to_f32<SDT>(*(const uint16_t*)(sb_r + SBB + gw * 2));
+                cb[q] = (BITS == 8) ? bi : fmaf(sc[q], -128.f, bi);
+                cl[q] = 120.f * sc[q];
+            }
+            f32x4_t d[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                bf16x8_t bop[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t pr[4];
+                    if constexpr (BITS == 3) codes3_to_bf16_pairs(cw[t], h, j, pr, kc);
+                    else codes_to_bf16_pairs<BITS>(cw[t] + h * BITS, j, pr, kc);
+                    bop[j] = as_bf16x8(pr[0], pr[1], pr[2], pr[3]);
+                }
+                const u32x4_t* src = (const u32x4_t*)&wl16[a_base + (uint32_t)t * a_step + h * 32];
+                d[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const u32x4_t v = src[j];
+                    d[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(v[0], v[1], v[2], v[3]),
+                                                                  bop[j], d[h], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const float* xg = wlf + g_idx[i] + (uint32_t)t * g_step[i];
+                if constexpr (BITS == 3) {
+                    const float* xl = xg + M * gxw;
+#pragma unroll
+                    for (int q = 0; q < GL; ++q) acc[i] = fmaf(cl[q], xl[q], acc[i]);
+                }
+                if constexpr (GL == 2) {
+                    acc[i] = fmaf(sc[0], d[0][i], fmaf(cb[0], xg[0], acc[i]));
+                    acc[i] = fmaf(sc[1], d[1][i], fmaf(cb[1], xg[1], acc[i]));
+                } else {
+                    acc[i] = fmaf(sc[0], d[0][i] + d[1][i], fmaf(cb[0], xg[0], acc[i]));
+                }
+            }
+        }
+    }
+
+    // ---- slots (lane groups) of a row meet by shuffles, slices in LDS
+    float v[MI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+        v[i] = acc[i];
+        v[i] += __shfl_xor(v[i], 16, 64);
+        v[i] += __shfl_xor(v[i], 32, 64);
+    }
+    const int ks = blockDim.x >> 6;
+    float* red = (float*)(wl + 128);  // this wave's x slice is no longer read
+    if (ks > 1) {
+        __builtin_amdgcn_wave_barrier();
+        if (lg == 0) {
+#pragma unroll
+            for (int i = 0; i < MI; ++i) red[i * 16 + lr] = v[i];
+        }
+        __syncthreads();
+        if (wave != 0) return;
+        if (lg < MI) {
+            float s = 0.f;
+            for (int w = 0; w < ks; ++w) s += ((const float*)(lds8 + w * wbytes + 128))[lg * 16 + lr];
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+                if (i == lg) v[i] = s;
+        }
+    }
+    const int64_t row = row0 + lr;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+        if (lg == i && i < M && row < R) store_dt(P.y, args.y_dt, (int64_t)i * R + row, v[i]);
+}
+
 // ------------------------------------------------------------ wide GEMV
 //
 // qmv_wide_*: the decode GEMV for 4 < m <= 16 on the streamed layout (same
@@ -1486,6 +1773,72 @@ hipError_t launch_stream_inline(const QmvArgs& a, int blocks, int sb_dt, int gs,
     });
 }
 
+// The split GEMV's instantiations: m <= 4 activation rows (MI 1, 2, 4) with
+// slices of up to 4, 4 and 2 stages.
+constexpr int split_max_nsw(int mi) { return mi <= 2 ? 4 : 2; }
+
+bool split_covers(const rq_problem& p, int sb_dt, int64_t m, int gs) {
+    if (sb_dt == RQ_F32 || m < 1 || m > 4 || p.cols % 256 != 0 || p.rows < 1) return false;
+    const int nsw = split_nsw(p.cols);
+    const int mi = m >= 3 ? 4 : (int)m;
+    if (nsw == 0 || nsw > split_max_nsw(mi)) return false;
+    const int gsh = __builtin_ctz(gs);
+    const int sb1 = (256 >> gsh) * 2;  // bytes of one array per row and stage
+    const int sbh = nsw * sb1 / 2;     // (scale, bias) bytes one lane loads
+    const int sbw = sbh < sb1 ? sbh : (sb1 < 16 ? sb1 : 16);
+    const int64_t row_bytes = (p.cols >> gsh) * 2;
+    const int ks = (int)(((p.cols >> 8) + nsw - 1) / nsw);
+    const uintptr_t code_align = (RQ_BITS & 1) ? 7 : 15;
+    return row_bytes % sbw == 0 && (((uintptr_t)p.scales | (uintptr_t)p.biases) % sbw) == 0 &&
+           ((uintptr_t)p.w_q & code_align) == 0 && ((uintptr_t)p.x & 15) == 0 &&
+           (int64_t)ks * split_wave_bytes(mi, nsw, gsh, RQ_BITS) <= kLdsBudget;
+}
+
+hipError_t launch_split(const QmvArgs& a, int blocks, int64_t cols, int sb_dt, int gs,
+                        hipStream_t stream) {
+    const int nsw = split_nsw(cols);
+    const int ks = (int)(((cols >> 8) + nsw - 1) / nsw);
+    const int gsh = __builtin_ctz(gs);
+    const int mi = a.m >= 3 ? 4 : a.m;
+    const size_t lds = (size_t)ks * split_wave_bytes(mi, nsw, gsh, RQ_BITS);
+    auto go = [&](auto sd, auto mic, auto gshc, auto nswc) {
+        constexpr int MI = decltype(mic)::value, NSW = decltype(nswc)::value;
+        if constexpr (NSW <= split_max_nsw(MI)) {
+            hipLaunchKernelGGL((qmv_split<RQ_BITS, decltype(sd)::value, MI, decltype(gshc)::value, NSW>),
+                               dim3(blocks), dim3(64 * ks), lds, stream, a);
+            return hipGetLastError();
+        }
+        return hipErrorInvalidValue;
+    };
+    typedef std::integral_constant<int, RQ_BF16> BF;
+    typedef std::integral_constant<int, RQ_F16> FH;
+    auto by_nsw = [&](auto sd, auto mic, auto gshc) {
+        switch (nsw) {
+            case 1: return go(sd, mic, gshc, std::integral_constant<int, 1>());
+            case 2: return go(sd, mic, gshc, std::integral_constant<int, 2>());
+            case 4: return go(sd, mic, gshc, std::integral_constant<int, 4>());
+            default: return hipErrorInvalidValue;
+        }
+    };
+    auto by_gs = [&](auto sd, auto mic) {
+        switch (gsh) {
+            case 5: return by_nsw(sd, mic, std::integral_constant<int, 5>());
+            case 6: return by_nsw(sd, mic, std::integral_constant<int, 6>());
+            case 7: return by_nsw(sd, mic, std::integral_constant<int, 7>());
+            default: return hipErrorInvalidValue;
+        }
+    };
+    auto by_m = [&](auto sd) {
+        switch (mi) {
+            case 1: return by_gs(sd, std::integral_constant<int, 1>());
+            case 2: return by_gs(sd, std::integral_constant<int, 2>());
+            case 4: return by_gs(sd, std::integral_constant<int, 4>());
+            default: return hipErrorInvalidValue;
+        }
+    };
+    return sb_dt == RQ_BF16 ? by_m(BF()) : by_m(FH());
+}
+
 hipError_t launch_stream_table(const rq::QmvTable& a, int blocks, int sb_dt, int gs, size_t lds,
                                hipStream_t stream) {
     if (a.m > kStreamSlotsMax) {
@@ -1530,6 +1883,31 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
     int64_t rowblocks = 0;
     for (int i = 0; i < n; ++i) rowblocks += (probs[i]->rows + 15) / 16;
     const int cfg = rowblocks >= RQ_QMV_BIG_MIN ? 2 : (rowblocks >= 2048 ? 1 : 0);
+    // Small launches: the split GEMV (one memory round trip per launch).
+    bool split = cfg == 0 && RQ_QMV_SPLIT;
+    for (int i = 0; i < n && split; ++i) split = split_covers(*probs[i], sb_dt, m, gs);
+    if (split) {
+        for (int base = 0; base < n; base += RQ_MAX_GROUPED) {
+            const int cnt = (n - base) < RQ_MAX_GROUPED ? (n - base) : RQ_MAX_GROUPED;
+            QmvArgs a;
+            std::memset(&a, 0, sizeof(a));
+            int64_t blocks = 0;
+            for (int i = 0; i < cnt; ++i) {
+                a.p[i] = *probs[base + i];
+                a.block_start[i] = (int)blocks;
+                blocks += (probs[base + i]->rows + 15) / 16;
+            }
+            a.block_start[cnt] = (int)blocks;
+            a.n = cnt;
+            a.m = (int)m;
+            a.gs_shift = gs_shift;
+            a.x_dt = x_dt;
+            a.y_dt = y_dt;
+            hipError_t e = launch_split(a, (int)blocks, K, sb_dt, gs, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     bool streamed = cfg >= 1 && RQ_QMV_STREAM;
     for (int i = 0; i < n && streamed; ++i) streamed = qmv_stream_covers(*probs[i], sb_dt, m, gs, RQ_BITS);
     if (streamed) {

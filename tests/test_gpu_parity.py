@@ -185,6 +185,42 @@ def test_qmv_parity_dtypes(O, rq, dev, bits, gs, xdt, sdt):
     rel_check(y, ref, what="qmv dtypes")
 
 
+def _rel(y, ref):
+    y, ref = y.detach().double().cpu(), ref.double()
+    return ((y - ref).norm() / ref.norm()).item(), ((y - ref).abs().max() / ref.abs().max()).item()
+
+
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("R,K,gs,bits", [(2048, 2048, 64, 4), (512, 4096, 32, 5), (4096, 2048, 64, 8)])
+def test_fp32_activation_precision(O, rq, dev, R, K, gs, bits, sdt):
+    """The MFMA operands are bf16: fp32 activations are rounded to bf16 once
+    when they are staged (MLX's qmv multiplies in fp32, so this is the one
+    place the products differ in kind).  Pins how much that costs on fp32
+    residual-stream inputs, tighter than the general 1e-2 bar: the GEMV
+    (M = 1, 8) is the oracle's product of bf16(x) to fp32 accumulation order
+    (nothing else is rounded), and both the GEMV and the GEMM (M = 300, which
+    also rounds each dequantized weight s*q + b to bf16) stay within 3e-3
+    Frobenius / 4e-3 elementwise of the fp32 product."""
+    w = weights(R, K, R + K + bits, sdt)
+    wq, s, b = O.quantize(w, gs, bits)
+    g = torch.Generator().manual_seed(R + K + bits)
+    for M in (1, 8, 300):
+        say(f"fp32 activations [{R},{K}] b{bits} g{gs} s={sdt} M={M}")
+        x = torch.randn(M, K, generator=g)
+        y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
+        assert y.dtype == torch.float32
+        ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
+        refb = O.quantized_matmul(x.to(torch.bfloat16).float(), wq, s, b, True, gs, bits,
+                                  out_dtype=torch.float32, weights="exact")
+        fro, elem = _rel(y, ref)
+        assert fro <= 3e-3 and elem <= 4e-3, f"M={M} vs fp32 x: {fro:.2e} {elem:.2e}"
+        frob, elemb = _rel(y, refb)
+        if M <= 8:
+            assert frob <= 1e-5 and elemb <= 2e-5, f"M={M} vs bf16(x): {frob:.2e} {elemb:.2e}"
+        else:
+            assert frob <= 2.5e-3, f"M={M} vs bf16(x): {frob:.2e}"
+
+
 # Small single launches (the K-split kernel) over contraction lengths from
 # one 256-code stage to 16384, rows ending mid-tile.
 SMALL_SHAPES = [(200, 256), (37, 768), (130, 2048), (64, 2304), (100, 8192), (17, 16384)]
@@ -202,6 +238,47 @@ def test_qmv_small_launch_shapes(O, rq, dev, bits, gs, M):
         y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
         ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
         rel_check(y, ref, what=f"small b{bits} g{gs} M{M} {R}x{K}")
+
+
+# The split GEMV (small launches: a block is one 16-row tile whose waves take
+# contiguous K slices of 1, 2 or 4 256-code stages).  Stage counts that do not
+# divide into the slices leave the last wave a short slice: 9 stages on 9
+# waves of one, 17 / 21 on 2-stage slices, 33 / 63 on 4-stage slices.
+SPLIT_SHAPES = [(37, 2304), (130, 4352), (16, 5376), (61, 8448), (200, 16128)]
+
+
+@pytest.mark.parametrize("xdt,sdt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                     (torch.float32, torch.bfloat16)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_split_gemv_short_slices(O, rq, dev, bits, gs, M, xdt, sdt):
+    for R, K in SPLIT_SHAPES:
+        w = weights(R, K, 11 * bits + gs + K, sdt)
+        wq, s, b = O.quantize(w, gs, bits)
+        x = acts(M, K, 3 * M + K, xdt)
+        say(f"split gemv bits={bits} gs={gs} M={M} x={xdt} R={R} K={K}")
+        y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
+        ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
+        rel_check(y, ref, what=f"split b{bits} g{gs} M{M} {R}x{K}")
+
+
+def test_split_gemv_dependency_level(O, rq, dev):
+    """One decode dependency level as one grouped launch (the r, k, v
+    projections of a layer: three problems, three activations) and the
+    same problems again as single calls: bit-identical, since each row's
+    slices are summed in the same order."""
+    probs = []
+    for i in range(3):
+        wq, s, b = O.quantize(weights(2048, 2048, 60_000 + i), 64, 4)
+        probs.append((acts(1, 2048, 60_100 + i).to(dev), (wq.to(dev), s.to(dev), b.to(dev))))
+    ys = rq.grouped_qmv([x for x, _ in probs], [w for _, w in probs], 64, 4)
+    for (x, (wq, s, b)), y in zip(probs, ys):
+        ref = O.quantized_matmul(x.cpu(), wq.cpu(), s.cpu(), b.cpu(), True, 64, 4,
+                                 out_dtype=torch.float32, weights="exact")
+        rel_check(y, ref, what="dependency level")
+        y1 = rq.quantized_matmul(x, wq, s, b, True, 64, 4)
+        assert bits_equal(y, y1)
 
 
 def test_qmv_edge_shapes(O, rq, dev):
