@@ -168,7 +168,8 @@ int rq_lora_down(const void* x, int64_t m, int64_t k, const void* a, int64_t ran
  * accumulated in fp32 with the GEMM and rounded once into y_dt.  Runs on the
  * 64-wide-stage GEMMs only (bf16 x, m >= 256, 16-bit scales 16-byte aligned;
  * transpose=1: cols a multiple of 8 groups; transpose=0: rows % 64 == 0,
- * cols % 128 == 0); other problems return RQ_EUNSUPPORTED and the caller
+ * cols % 128 == 0, or cols % 160 == 0 with 4- or 8-bit codes); other
+ * problems return RQ_EUNSUPPORTED and the caller
  * runs rq_qmm plus the term separately. */
 int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
                 const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,

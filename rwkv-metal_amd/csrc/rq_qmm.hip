@@ -581,6 +581,10 @@ __device__ __forceinline__ void k64_tile(int t, int tiles_m, int tiles_n, int& m
 #ifndef RQ_GEMM_K64
 #define RQ_GEMM_K64 1  // 1: 64-wide stages with whole-line loads (qmm_t_k64) where they apply
 #endif
+#ifndef RQ_GEMM_N160
+#define RQ_GEMM_N160 1  // 1: 160-column tiles for the transposed GEMM where they fill the GPU better
+#endif
+constexpr int kK64Cus = 256;  // CUs of one MI355X: one k64 block per CU
 #ifndef RQ_WS_SLOTS
 #define RQ_WS_SLOTS 6  // DMA ring slots of qmm_t_ws (4 or 6): RQ_WS_SLOTS-1 stages in flight
 #endif
@@ -1410,20 +1414,29 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
 // LDS and no (scale, bias) table: the producers' critical path has no LDS
 // read, and the tile is written with half as many stores as the earlier
 // r-contiguous layout needed.
-// Requires 16-bit scales, R % 64 == 0 and K % 128 == 0.
+// BN = 160 (4- and 8-bit codes, K % 160 == 0): the 2560-wide outputs of
+// the 2.9B shapes are 16 x 16 = 256 tiles (one round on 256 CUs) instead of
+// 16 x 20 = 320 at BN = 128.  A stage row is 20 chunks of 8 codes; producer
+// thread (row, q) dequantizes chunks 5q .. 5q+4 (40 codes, at most three
+// groups: their (scale, bias) values are loaded per stage), and tile rows are
+// padded to 24 chunks so that the swizzle stays inside aligned 8-chunk
+// groups.
+// Requires 16-bit scales, R % 64 == 0 and K % BN == 0.
 RQ_DEV int nkey(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// physical 16-byte chunk of chunk c in tile row r
+RQ_DEV int nchunk(int c, int r) { return (c & ~7) | ((c ^ nkey(r)) & 7); }
 
-template <int BITS, int SDT, bool FZ = false>
+template <int BITS, int SDT, int BN = 128, bool FZ = false>
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
     void* __restrict__ y, int y_dt, int tiles_m, int tiles_n, rq::LoraArgs lora) {
-    constexpr int BM = 256, BN = 128, WN = BN / 2;
+    constexpr int BM = 256, WN = BN / 2;
     constexpr int TM = 8, TN = WN / 16;
-    constexpr int D = RQ_K64_DEPTH;         // stages of loads in flight per producer thread
-    constexpr int ROWB = BN * 2;            // bytes per row of the bf16 weight tile
-    static_assert(D == 2, "the register ring index is the ring slot");
+    constexpr int D = 2;  // stages of loads in flight per producer thread: the ring slot index
+    constexpr int ROWB = BN == 160 ? 384 : BN * 2;  // bytes per row of the bf16 weight tile
     static_assert(SDT != RQ_F32, "16-bit scales");
+    static_assert(BN == 128 || (BN == 160 && (BITS == 4 || BITS == 8) && !FZ), "tile width");
     __shared__ __attribute__((aligned(16))) uint8_t xs0[BM * 128];
     __shared__ __attribute__((aligned(16))) uint8_t xs1[BM * 128];
     __shared__ __attribute__((aligned(16))) uint8_t bq0[64 * ROWB];
@@ -1457,6 +1470,110 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
             xdst[i] = (uint32_t)(row * 128 + ((chunk ^ (row & 7)) * 16));
         }
         const uint8_t* xbase = (const uint8_t*)(x + m0 * R);
+        if constexpr (BN == 160) {
+            // chunks 5 jq .. 5 jq + 4 (8 codes each) of row jr of each stage
+            constexpr int NC = 5, WPC = BITS / 4, NG = 3;
+            typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+            const int jr = pt & 63, jq = pt >> 6;
+            const uint32_t* wbase = wq + ((k0 >> 3) + NC * jq) * WPC;
+            const int64_t kc0 = k0 + 8 * NC * jq;
+            const int64_t glo = kc0 >> gs_shift;
+            int gsel[NC];
+            uint32_t qdst[NC];
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                gsel[i] = (int)(((kc0 + 8 * i) >> gs_shift) - glo);
+                qdst[i] = (uint32_t)(jr * ROWB + (nchunk(NC * jq + i, jr) << 4));
+            }
+            int gcl[NG];  // group offsets, clamped inside the row (past-the-row ones are unused)
+#pragma unroll
+            for (int j = 0; j < NG; ++j) gcl[j] = glo + j < G ? j : (int)(G - 1 - glo);
+            const uint16_t* sbase = (const uint16_t*)scales + glo;
+            const uint16_t* bbase = (const uint16_t*)biases + glo;
+            u32x4_t xv[D][8];
+            uint32_t cv[D][NC * WPC];
+            uint16_t sv[D][NG][2];
+            auto issue = [&](int st, int r) {
+                const int sc = st < nst ? st : nst - 1;
+                const uint8_t* xb = xbase + (int64_t)sc * 128;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xv[r][i] = *(gv_t)(xb + xoff[i]);
+                const int64_t row = (int64_t)sc * 64 + jr;
+                const uint32_t* ws = wbase + row * wpr;
+                if constexpr (WPC == 1) {
+#pragma unroll
+                    for (int q = 0; q < NC; ++q) cv[r][q] = *((gw_t)ws + q);
+                } else {
+                    typedef const __attribute__((address_space(1))) u32x2_t* g2_t;
+#pragma unroll
+                    for (int q = 0; q < NC; ++q) {
+                        const u32x2_t v = *((g2_t)ws + q);
+                        cv[r][2 * q] = v[0];
+                        cv[r][2 * q + 1] = v[1];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < NG; ++j) {
+                    sv[r][j][0] = *(gh_t)(sbase + row * G + gcl[j]);
+                    sv[r][j][1] = *(gh_t)(bbase + row * G + gcl[j]);
+                }
+            };
+#pragma unroll
+            for (int r = 0; r < D; ++r) issue(r, r);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();  // pairs with the MFMA waves' first barrier
+            asm volatile("" ::: "memory");
+            for (int s0 = 0; s0 < nst; s0 += 2) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int st = s0 + u;
+                    uint8_t* xs = u ? xs1 : xs0;
+                    uint8_t* bq = u ? bq1 : bq0;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u][i];
+                    float sf[NG], bf[NG];
+#pragma unroll
+                    for (int j = 0; j < NG; ++j) {
+                        sf[j] = dt_traits<SDT>::to_f32(sv[u][j][0]);
+                        bf[j] = dt_traits<SDT>::to_f32(sv[u][j][1]);
+                    }
+#pragma unroll
+                    for (int i = 0; i < NC; ++i) {
+                        const float sc = gsel[i] == 0 ? sf[0] : (gsel[i] == 1 ? sf[1] : sf[2]);
+                        const float bc = gsel[i] == 0 ? bf[0] : (gsel[i] == 1 ? bf[1] : bf[2]);
+                        uint32_t d[4];
+                        if constexpr (WPC == 1) {
+                            uint32_t lo = cv[u][i] & 0x0F0F0F0Fu;         // codes 0, 2, 4, 6
+                            uint32_t hi = (cv[u][i] >> 4) & 0x0F0F0F0Fu;  // codes 1, 3, 5, 7
+                            asm("" : "+v"(lo));
+                            asm("" : "+v"(hi));
+#pragma unroll
+                            for (int k = 0; k < 4; ++k)
+                                d[k] = pack_bf16x2(fmaf(sc, (float)(uint8_t)(lo >> (8 * k)), bc),
+                                                   fmaf(sc, (float)(uint8_t)(hi >> (8 * k)), bc));
+                        } else {
+#pragma unroll
+                            for (int w = 0; w < 2; ++w) {
+                                uint32_t v = cv[u][2 * i + w];
+                                asm("" : "+v"(v));
+#pragma unroll
+                                for (int k = 0; k < 2; ++k)
+                                    d[2 * w + k] =
+                                        pack_bf16x2(fmaf(sc, (float)(uint8_t)(v >> (16 * k)), bc),
+                                                    fmaf(sc, (float)(uint8_t)(v >> (16 * k + 8)), bc));
+                            }
+                        }
+                        *(u32x4_t*)(bq + qdst[i]) = u32x4_t{d[0], d[1], d[2], d[3]};
+                    }
+                    issue(st + D, u);
+                    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this stage's LDS writes are done
+                    asm volatile("" ::: "memory");
+                    __builtin_amdgcn_s_barrier();
+                    asm volatile("" ::: "memory");
+                }
+            }
+            return;
+        }
         // the dequantization job: run jq of row jr of each stage
         const int jr = pt & 63, jq = pt >> 6;
         const uint32_t* wbase = wq + (k0 >> 5) * BITS + jq * BITS;
@@ -1553,7 +1670,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
         for (int b = 0; b < TN; ++b) {
             const int row = 8 * lg + 4 * v + (lr >> 2);
             const int col = wn * WN + 16 * b + 4 * (lr & 3);
-            boff[v][b] = (uint32_t)(row * ROWB + (((col >> 3) ^ nkey(row)) << 4) + (col & 7) * 2);
+            boff[v][b] = (uint32_t)(row * ROWB + (nchunk(col >> 3, row) << 4) + (col & 7) * 2);
         }
     typedef short s16x4_t __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_p;
@@ -1803,24 +1920,27 @@ hipError_t RQ_CAT(launch_qmm_n_b, RQ_BITS)(const void* x, int x_dt, const uint32
                                       int y_dt, hipStream_t stream, const LoraArgs* lora) {
     const LoraArgs lo = lora ? *lora : LoraArgs{nullptr, nullptr, 0, 0.f};
     // warp-specialised transposed GEMM: bf16 dY, 16-bit aligned scales,
-    // whole stages of 64 weight rows and 128 output columns
+    // whole stages of 64 weight rows and whole tiles of 128 or 160 output
+    // columns (160: 4- and 8-bit codes)
+    const bool can128 = cols % 128 == 0;
+    const bool can160 = (RQ_BITS == 4 || RQ_BITS == 8) && RQ_GEMM_N160 && cols % 160 == 0;
     const bool k64 = m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 &&
-                     rows % 64 == 0 && cols % 128 == 0 && ((uintptr_t)x & 15) == 0 &&
+                     rows % 64 == 0 && (can128 || can160) && ((uintptr_t)x & 15) == 0 &&
                      (((uintptr_t)scales | (uintptr_t)biases) & 7) == 0;
     if (lora && lora->a) {
         // the fused QLoRA layer's dX with u = dY . B in the kernel (rank 16,
         // 4- or 8-bit codes)
 #if RQ_BITS == 4 || RQ_BITS == 8
-        if (!k64 || lora->rank != 16) return hipErrorNotSupported;
+        if (!k64 || !can128 || lora->rank != 16) return hipErrorNotSupported;
         const int tm = (int)((m + 255) / 256);
         const int tn = (int)(cols / 128);
         const int blocks = ((tm * tn + 7) / 8) * 8;
         if (sb_dt == RQ_BF16)
-            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_BF16, true>), dim3(blocks), dim3(kWsBlock), 0,
+            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_BF16, 128, true>), dim3(blocks), dim3(kWsBlock), 0,
                                stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
                                __builtin_ctz(gs), y, y_dt, tm, tn, lo);
         else
-            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_F16, true>), dim3(blocks), dim3(kWsBlock), 0,
+            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_F16, 128, true>), dim3(blocks), dim3(kWsBlock), 0,
                                stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
                                __builtin_ctz(gs), y, y_dt, tm, tn, lo);
         return hipGetLastError();
@@ -1830,8 +1950,30 @@ hipError_t RQ_CAT(launch_qmm_n_b, RQ_BITS)(const void* x, int x_dt, const uint32
     }
     if (k64) {
         const int tm = (int)((m + 255) / 256);
-        const int tn = (int)(cols / 128);
+        // 160-column tiles where 128-column ones do not divide the output or
+        // take more rounds of 256 CUs than it costs to run fewer, wider tiles:
+        // a 160-column tile runs ~1.5x as long as a 128-column one (measured
+        // at M = 4096, R = 2560), so 2560-wide outputs (one round of 256
+        // instead of two of 320) take them and 10240-wide ones (4 rounds of
+        // 1024 against 5 of 1280) do not
+        auto rounds = [&](int64_t nt) { return (double)((nt + kK64Cus - 1) / kK64Cus); };
+        const bool wide = can160 && (!can128 || 1.5 * rounds((int64_t)tm * (cols / 160)) <
+                                                    rounds((int64_t)tm * (cols / 128)));
+        const int tn = (int)(cols / (wide ? 160 : 128));
         const int blocks = ((tm * tn + 7) / 8) * 8;
+#if RQ_BITS == 4 || RQ_BITS == 8
+        if (wide) {
+            if (sb_dt == RQ_BF16)
+                hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_BF16, 160>), dim3(blocks), dim3(kWsBlock), 0,
+                                   stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
+                                   __builtin_ctz(gs), y, y_dt, tm, tn, lo);
+            else
+                hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_F16, 160>), dim3(blocks), dim3(kWsBlock), 0,
+                                   stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
+                                   __builtin_ctz(gs), y, y_dt, tm, tn, lo);
+            return hipGetLastError();
+        }
+#endif
         if (sb_dt == RQ_BF16)
             hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_BF16>), dim3(blocks), dim3(kWsBlock), 0,
                                stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,

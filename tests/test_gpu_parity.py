@@ -493,6 +493,35 @@ def test_config3_oracle_small_m(O, rq, dev):
     rel_check(y, O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32, weights="exact"))
 
 
+# The transposed GEMM's 160-column tiles: output widths that 128 does not
+# divide (480, 800, 960) against the oracle, with partial row tiles and
+# 40-code producer chunks spanning two or three groups (gs 32 / 64), and the
+# 2.9B shapes at full size: 2560-wide outputs take 160 (256 tiles, one round,
+# instead of 320), the 10240-wide one stays on 128.
+N160_ORACLE = [(300, 128, 480, 4, 32, torch.bfloat16), (257, 192, 960, 8, 64, torch.float16),
+               (512, 64, 800, 4, 32, torch.bfloat16), (700, 320, 960, 4, 64, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("M,R,K,bits,gs,sdt", N160_ORACLE)
+def test_qmm_n_160_tiles_oracle(O, rq, dev, M, R, K, bits, gs, sdt):
+    say(f"qmm_n 160 tiles M={M} R={R} K={K} bits={bits} gs={gs}")
+    wq, s, b = O.quantize(weights(R, K, 80_000 + K + bits, sdt), gs, bits)
+    dy = acts(M, R, 80_000 + M)
+    y = rq.quantized_matmul(dy.to(dev), wq.to(dev), s.to(dev), b.to(dev), False, gs, bits)
+    ref = O.quantized_matmul(dy, wq, s, b, False, gs, bits, out_dtype=torch.float32, weights="exact")
+    rel_check(y, ref, what=f"qmm_n 160 {M}x{R}x{K}")
+
+
+@pytest.mark.parametrize("M,R,K,bits,gs", [(4096, 2560, 2560, 4, 64), (4096, 10240, 2560, 4, 128),
+                                           (4000, 2560, 2560, 8, 64), (2048, 2560, 10240, 4, 64)])
+def test_config3_transposed_full_size(rq, dev, M, R, K, bits, gs):
+    say(f"config3 transposed M={M} [{R},{K}] bits={bits} gs={gs}")
+    wq, s, b = rq.quantize(weights(R, K, 3_100_000 + R + K).to(dev), gs, bits)
+    dy = acts(M, R, 3_100_000 + M).to(dev)
+    y = rq.quantized_matmul(dy, wq, s, b, False, gs, bits)
+    rel_check(y, _gpu_dense_ref(rq, dy, wq, s, b, gs, bits, False), what=f"config3 dX {R}x{K} M{M}")
+
+
 @pytest.mark.parametrize("shape", [(2048, 2048), (8192, 2048), (2048, 8192)])
 def test_config4_transposed_full_size(rq, dev, shape):
     """QLoRA backward dX = dY . W at D=2048, M = 8 x 512."""

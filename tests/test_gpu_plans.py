@@ -87,6 +87,8 @@ LORA_TILES = [
     (False, 4096, 2048, 8192, 4, 64),   # config 4 dX, ffn_value
     (False, 1000, 512, 1024, 8, 128),   # 8-bit transposed, gs 128, partial row tile
     (False, 600, 256, 2048, 4, 32),     # gs 32
+    (False, 4096, 2560, 2560, 4, 64),   # transposed, 160-column tiles (2.9B dX)
+    (False, 300, 128, 480, 8, 32),      # transposed, 160-column tiles, 8-bit, partial row tile
 ]
 
 
