@@ -540,6 +540,61 @@ def dependency_levels(torch, rq, xs, ws, outs, total_wbytes, args):
             "hip_graph_us_per_step": round(t_graph * 1e6, 1)}
 
 
+def decode_per_shape(torch, rq, dev, args, gs=64, bits=4):
+    """Config 2's GEMV per shape (r/k/v/o, ffn_key, ffn_value, head) at M = 1
+    and 8, each over a rotation of distinct weight buffers of >= 512 MB (2x
+    the 256 MB MALL, so neither L2 nor MALL serves a launch its weights): one
+    launch per buffer, captured in one HIP graph, replayed; 5 timed regions
+    of >= 20 launches after 3 warm-up replays, median per-launch time.  Each
+    launch is one rq_qmm call (the split GEMV below 32768 rows, the streamed
+    one for the head)."""
+    import statistics
+    out = {}
+    for name, R, K in [("rkvo", D, D), ("ffn_key", FFN, D), ("ffn_value", D, FFN), ("head", VOCAB, D)]:
+        wb = weight_bytes(R, K, bits, gs)
+        nbuf = max(2, -(-(512 << 20) // wb))
+        bufs = []
+        for i in range(nbuf):
+            g = torch.Generator(device=dev).manual_seed(2_100_000 + 7919 * i + R + K)
+            w = (torch.randn(R, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            bufs.append(rq.quantize(w, gs, bits))
+            del w
+        res = {"weight_bytes": wb, "buffers": nbuf}
+        for M in (1, 8):
+            x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+            bound = [rq.BoundQmm(x, wq, s, b, True, gs, bits) for wq, s, b in bufs]
+            reps_per_region = max(1, -(-20 // nbuf))
+
+            def rotation():
+                for _ in range(reps_per_region):
+                    for bq in bound:
+                        bq.run()
+            rotation()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                rotation()
+            for _ in range(3):
+                graph.replay()
+            torch.cuda.synchronize()
+            launches = reps_per_region * nbuf
+            per = []
+            for _ in range(5):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                graph.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                per.append(e0.elapsed_time(e1) / 1e3 / launches)
+            t = statistics.median(per)
+            res[f"m{M}_us"] = round(t * 1e6, 2)
+            res[f"m{M}_gbs"] = round(wb / t / 1e9, 1)
+            del graph, bound
+        out[name] = res
+        del bufs
+    return out
+
+
 def dense_bf16_gemms(torch, dev, args):
     """torch.matmul (hipBLASLt) of dense bf16 operands at config 3's shapes,
     M = 4096: the vendor library's dense GEMM on the same box and clocks."""
@@ -762,6 +817,7 @@ def main():
         del graph
         extra["decode_m1_dependency_levels"] = dependency_levels(torch, rwkvq, xs, ws, outs,
                                                                  total_wbytes, args)
+        extra["decode_per_shape_rotating_512mb"] = decode_per_shape(torch, rwkvq, dev, args)
         # prefill GEMM, config 3 (RWKV-7 2.9B shapes) at M = 4096 (aggregate) and
         # 2048 / 512; the transposed product (QLoRA dX) at M = 4096
         pre = {}

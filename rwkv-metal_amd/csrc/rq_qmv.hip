@@ -55,8 +55,8 @@
 //
 // The kernels: qmv_kernel (above: any layout), and for 16-bit scales the
 // streamed qmv_stream_* (m <= 4) and qmv_wide_* (4 < m <= 16) for launches
-// that fill the GPU with rows, and qmv_split for small launches (one memory
-// round trip per launch); each is described where it is defined.
+// that fill the GPU with rows, and qmv_split for small launches (m <= 8; one
+// memory round trip per launch); each is described where it is defined.
 
 #include "rq_common.h"
 #include "rq_launch.h"
@@ -1058,6 +1058,8 @@ __global__ __launch_bounds__(kBlock) RQ_STREAM_OCC void qmv_stream_table(const r
 // qmv_split: the decode GEMV of launches too small to fill the GPU with rows
 // (one projection, or the few independent projections of one step of a
 // layer), where a launch costs its memory round trips rather than its bytes.
+// m <= 4 activation rows run in one pass of the slotted MFMA rows, 4 < m <= 8
+// in two passes (NMC) that share each stage's code conversion.
 //
 //  * A block is one 16-row tile; its KS waves split K into contiguous slices
 //    of NSW stages (a stage is 256 codes of the 16 rows, laid out as in the
@@ -1098,7 +1100,7 @@ __host__ __device__ inline int split_wave_bytes(int m, int nsw, int gsh, int bit
            16 * (2 * sbb + 16);
 }
 
-template <int BITS, int SDT, int MI, int GSH, int NSW>
+template <int BITS, int SDT, int NMC, int MI, int GSH, int NSW>
 __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
     static_assert(SDT != RQ_F32, "split GEMV scales are 16-bit");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
@@ -1112,7 +1114,8 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
     constexpr int SBW = SBH < SplitSB<GSH>::SB1 ? SBH : (SplitSB<GSH>::SB1 < 16 ? SplitSB<GSH>::SB1 : 16);
     constexpr int SBN = SBH / SBW;                // loads per lane
     constexpr int ROWB = 2 * SBB + 16;
-    constexpr int XP = (MI * KW / 8 + 63) / 64;   // 8-element x pieces per lane (upper bound)
+    constexpr int MR = NMC == 1 ? MI : 4 * NMC;   // activation rows at most
+    constexpr int XP = (MR * KW / 8 + 63) / 64;   // 8-element x pieces per lane (upper bound)
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lg = lane >> 4, lr = lane & 15;
@@ -1229,26 +1232,35 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
     }
     __builtin_amdgcn_wave_barrier();  // LDS writes above are read by other lanes of this wave
 
-    // ---- per-lane constants (as in the streamed GEMV, on the slice)
+    // ---- per-lane constants (as in the streamed GEMV, on the slice); pass c
+    // carries activation rows 4c .. 4c+3
     const PairConsts kc = BITS == 3 ? pair3_consts() : pair_consts();
-    const int m_a = lr & 3;
-    const bool a_act = (lr >> 2) == lg && m_a < M;
-    const uint32_t a_base = a_act ? (uint32_t)(64 + m_a * KW + lg * 64) : 0u;  // in 16-bit units
-    const uint32_t a_step = a_act ? 256u : 0u;
+    uint32_t a_base[NMC], a_step[NMC];
+#pragma unroll
+    for (int c = 0; c < NMC; ++c) {
+        const int m_a = 4 * c + (lr & 3);
+        const bool a_act = (lr >> 2) == lg && m_a < M;
+        a_base[c] = a_act ? (uint32_t)(64 + m_a * KW + lg * 64) : 0u;  // in 16-bit units
+        a_step[c] = a_act ? 256u : 0u;
+    }
     constexpr int GL = GSH == 5 ? 2 : 1;
     const int glane = GSH == 5 ? 2 * lg : (GSH == 6 ? lg : (lg >> 1));
     const int xlane = GSH == 5 ? 2 * lg : lg;
     const uint32_t xsum_f = (uint32_t)((128 + M * KW * 2) >> 2);  // float index of xsum in wl
-    uint32_t g_idx[MI], g_step[MI];
+    uint32_t g_idx[NMC][MI], g_step[NMC][MI];
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
-        const bool act = i < M;
-        g_idx[i] = act ? xsum_f + (uint32_t)(i * gxw + xlane) : 0u;
-        g_step[i] = act ? (uint32_t)(256 >> XSH) : 0u;
-    }
+    for (int c = 0; c < NMC; ++c)
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            const bool act = 4 * c + i < M;
+            g_idx[c][i] = act ? xsum_f + (uint32_t)((4 * c + i) * gxw + xlane) : 0u;
+            g_step[c][i] = act ? (uint32_t)(256 >> XSH) : 0u;
+        }
     const uint8_t* sb_r = sbl + lr * ROWB + glane * 2;
 
-    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc[NMC];
+#pragma unroll
+    for (int c = 0; c < NMC; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const uint16_t* wl16 = (const uint16_t*)wl;
     const float* wlf = (const float*)wl;
 #pragma unroll
@@ -1263,7 +1275,7 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
                 cb[q] = (BITS == 8) ? bi : fmaf(sc[q], -128.f, bi);
                 cl[q] = 120.f * sc[q];
             }
-            f32x4_t d[2];
+            f32x4_t d[NMC][2];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 bf16x8_t bop[4];
@@ -1274,63 +1286,81 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
                     else codes_to_bf16_pairs<BITS>(cw[t] + h * BITS, j, pr, kc);
                     bop[j] = as_bf16x8(pr[0], pr[1], pr[2], pr[3]);
                 }
-                const u32x4_t* src = (const u32x4_t*)&wl16[a_base + (uint32_t)t * a_step + h * 32];
-                d[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const u32x4_t v = src[j];
-                    d[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(v[0], v[1], v[2], v[3]),
-                                                                  bop[j], d[h], 0, 0, 0);
+                for (int c = 0; c < NMC; ++c) {
+                    const u32x4_t* src =
+                        (const u32x4_t*)&wl16[a_base[c] + (uint32_t)t * a_step[c] + h * 32];
+                    d[c][h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const u32x4_t v = src[j];
+                        d[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            as_bf16x8(v[0], v[1], v[2], v[3]), bop[j], d[c][h], 0, 0, 0);
+                    }
                 }
             }
 #pragma unroll
-            for (int i = 0; i < MI; ++i) {
-                const float* xg = wlf + g_idx[i] + (uint32_t)t * g_step[i];
-                if constexpr (BITS == 3) {
-                    const float* xl = xg + M * gxw;
+            for (int c = 0; c < NMC; ++c)
 #pragma unroll
-                    for (int q = 0; q < GL; ++q) acc[i] = fmaf(cl[q], xl[q], acc[i]);
+                for (int i = 0; i < MI; ++i) {
+                    const float* xg = wlf + g_idx[c][i] + (uint32_t)t * g_step[c][i];
+                    if constexpr (BITS == 3) {
+                        const float* xl = xg + M * gxw;
+#pragma unroll
+                        for (int q = 0; q < GL; ++q) acc[c][i] = fmaf(cl[q], xl[q], acc[c][i]);
+                    }
+                    if constexpr (GL == 2) {
+                        acc[c][i] = fmaf(sc[0], d[c][0][i], fmaf(cb[0], xg[0], acc[c][i]));
+                        acc[c][i] = fmaf(sc[1], d[c][1][i], fmaf(cb[1], xg[1], acc[c][i]));
+                    } else {
+                        acc[c][i] = fmaf(sc[0], d[c][0][i] + d[c][1][i], fmaf(cb[0], xg[0], acc[c][i]));
+                    }
                 }
-                if constexpr (GL == 2) {
-                    acc[i] = fmaf(sc[0], d[0][i], fmaf(cb[0], xg[0], acc[i]));
-                    acc[i] = fmaf(sc[1], d[1][i], fmaf(cb[1], xg[1], acc[i]));
-                } else {
-                    acc[i] = fmaf(sc[0], d[0][i] + d[1][i], fmaf(cb[0], xg[0], acc[i]));
-                }
-            }
         }
     }
 
     // ---- slots (lane groups) of a row meet by shuffles, slices in LDS
-    float v[MI];
+    float v[NMC][MI];
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
-        v[i] = acc[i];
-        v[i] += __shfl_xor(v[i], 16, 64);
-        v[i] += __shfl_xor(v[i], 32, 64);
-    }
+    for (int c = 0; c < NMC; ++c)
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            v[c][i] = acc[c][i];
+            v[c][i] += __shfl_xor(v[c][i], 16, 64);
+            v[c][i] += __shfl_xor(v[c][i], 32, 64);
+        }
     const int ks = blockDim.x >> 6;
     float* red = (float*)(wl + 128);  // this wave's x slice is no longer read
     if (ks > 1) {
         __builtin_amdgcn_wave_barrier();
         if (lg == 0) {
 #pragma unroll
-            for (int i = 0; i < MI; ++i) red[i * 16 + lr] = v[i];
+            for (int c = 0; c < NMC; ++c)
+#pragma unroll
+                for (int i = 0; i < MI; ++i) red[(4 * c + i) * 16 + lr] = v[c][i];
         }
         __syncthreads();
         if (wave != 0) return;
-        if (lg < MI) {
-            float s = 0.f;
-            for (int w = 0; w < ks; ++w) s += ((const float*)(lds8 + w * wbytes + 128))[lg * 16 + lr];
+        // lane group lg sums rows m = 4c + lg over the slices, in wave order
 #pragma unroll
-            for (int i = 0; i < MI; ++i)
-                if (i == lg) v[i] = s;
+        for (int c = 0; c < NMC; ++c) {
+            if (lg < MI) {
+                float s = 0.f;
+                for (int w = 0; w < ks; ++w)
+                    s += ((const float*)(lds8 + w * wbytes + 128))[(4 * c + lg) * 16 + lr];
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+                    if (i == lg) v[c][i] = s;
+            }
         }
     }
     const int64_t row = row0 + lr;
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
-        if (lg == i && i < M && row < R) store_dt(P.y, args.y_dt, (int64_t)i * R + row, v[i]);
+    for (int c = 0; c < NMC; ++c)
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+            if (lg == i && 4 * c + i < M && row < R)
+                store_dt(P.y, args.y_dt, (int64_t)(4 * c + i) * R + row, v[c][i]);
 }
 
 // ------------------------------------------------------------ wide GEMV
@@ -1773,15 +1803,19 @@ hipError_t launch_stream_inline(const QmvArgs& a, int blocks, int sb_dt, int gs,
     });
 }
 
-// The split GEMV's instantiations: m <= 4 activation rows (MI 1, 2, 4) with
-// slices of up to 4, 4 and 2 stages.
-constexpr int split_max_nsw(int mi) { return mi <= 2 ? 4 : 2; }
+// The split GEMV's instantiations: m <= 4 activation rows in one pass (MI
+// 1, 2, 4: slices of up to 4, 4 and 2 stages) and 4 < m <= 8 in two (MI 4,
+// up to 2 stages); 8-bit codes (twice the registers per stage) one step
+// less where more would spill.  "Pass code" pc = 8 * NMC + MI.
+constexpr int split_max_nsw(int pc) {
+    return RQ_BITS == 8 ? (pc == 9 ? 4 : (pc == 20 ? 1 : 2)) : (pc == 9 || pc == 10 ? 4 : 2);
+}
+inline int split_pass_code(int64_t m) { return m > 4 ? 20 : (m >= 3 ? 12 : 8 + (int)m); }
 
 bool split_covers(const rq_problem& p, int sb_dt, int64_t m, int gs) {
-    if (sb_dt == RQ_F32 || m < 1 || m > 4 || p.cols % 256 != 0 || p.rows < 1) return false;
+    if (sb_dt == RQ_F32 || m < 1 || m > 8 || p.cols % 256 != 0 || p.rows < 1) return false;
     const int nsw = split_nsw(p.cols);
-    const int mi = m >= 3 ? 4 : (int)m;
-    if (nsw == 0 || nsw > split_max_nsw(mi)) return false;
+    if (nsw == 0 || nsw > split_max_nsw(split_pass_code(m))) return false;
     const int gsh = __builtin_ctz(gs);
     const int sb1 = (256 >> gsh) * 2;  // bytes of one array per row and stage
     const int sbh = nsw * sb1 / 2;     // (scale, bias) bytes one lane loads
@@ -1791,7 +1825,7 @@ bool split_covers(const rq_problem& p, int sb_dt, int64_t m, int gs) {
     const uintptr_t code_align = (RQ_BITS & 1) ? 7 : 15;
     return row_bytes % sbw == 0 && (((uintptr_t)p.scales | (uintptr_t)p.biases) % sbw) == 0 &&
            ((uintptr_t)p.w_q & code_align) == 0 && ((uintptr_t)p.x & 15) == 0 &&
-           (int64_t)ks * split_wave_bytes(mi, nsw, gsh, RQ_BITS) <= kLdsBudget;
+           (int64_t)ks * split_wave_bytes((int)m, nsw, gsh, RQ_BITS) <= kLdsBudget;
 }
 
 hipError_t launch_split(const QmvArgs& a, int blocks, int64_t cols, int sb_dt, int gs,
@@ -1799,12 +1833,14 @@ hipError_t launch_split(const QmvArgs& a, int blocks, int64_t cols, int sb_dt, i
     const int nsw = split_nsw(cols);
     const int ks = (int)(((cols >> 8) + nsw - 1) / nsw);
     const int gsh = __builtin_ctz(gs);
-    const int mi = a.m >= 3 ? 4 : a.m;
-    const size_t lds = (size_t)ks * split_wave_bytes(mi, nsw, gsh, RQ_BITS);
-    auto go = [&](auto sd, auto mic, auto gshc, auto nswc) {
-        constexpr int MI = decltype(mic)::value, NSW = decltype(nswc)::value;
-        if constexpr (NSW <= split_max_nsw(MI)) {
-            hipLaunchKernelGGL((qmv_split<RQ_BITS, decltype(sd)::value, MI, decltype(gshc)::value, NSW>),
+    // the kernel lays out its wave regions for exactly a.m activation rows
+    const size_t lds = (size_t)ks * split_wave_bytes(a.m, nsw, gsh, RQ_BITS);
+    auto go = [&](auto sd, auto nmcc, auto mic, auto gshc, auto nswc) {
+        constexpr int NMC = decltype(nmcc)::value, MI = decltype(mic)::value;
+        constexpr int NSW = decltype(nswc)::value;
+        if constexpr (NSW <= split_max_nsw(8 * NMC + MI)) {
+            hipLaunchKernelGGL((qmv_split<RQ_BITS, decltype(sd)::value, NMC, MI, decltype(gshc)::value,
+                                          NSW>),
                                dim3(blocks), dim3(64 * ks), lds, stream, a);
             return hipGetLastError();
         }
@@ -1812,27 +1848,30 @@ hipError_t launch_split(const QmvArgs& a, int blocks, int64_t cols, int sb_dt, i
     };
     typedef std::integral_constant<int, RQ_BF16> BF;
     typedef std::integral_constant<int, RQ_F16> FH;
-    auto by_nsw = [&](auto sd, auto mic, auto gshc) {
+    auto by_nsw = [&](auto sd, auto nmcc, auto mic, auto gshc) {
         switch (nsw) {
-            case 1: return go(sd, mic, gshc, std::integral_constant<int, 1>());
-            case 2: return go(sd, mic, gshc, std::integral_constant<int, 2>());
-            case 4: return go(sd, mic, gshc, std::integral_constant<int, 4>());
+            case 1: return go(sd, nmcc, mic, gshc, std::integral_constant<int, 1>());
+            case 2: return go(sd, nmcc, mic, gshc, std::integral_constant<int, 2>());
+            case 4: return go(sd, nmcc, mic, gshc, std::integral_constant<int, 4>());
             default: return hipErrorInvalidValue;
         }
     };
-    auto by_gs = [&](auto sd, auto mic) {
+    auto by_gs = [&](auto sd, auto nmcc, auto mic) {
         switch (gsh) {
-            case 5: return by_nsw(sd, mic, std::integral_constant<int, 5>());
-            case 6: return by_nsw(sd, mic, std::integral_constant<int, 6>());
-            case 7: return by_nsw(sd, mic, std::integral_constant<int, 7>());
+            case 5: return by_nsw(sd, nmcc, mic, std::integral_constant<int, 5>());
+            case 6: return by_nsw(sd, nmcc, mic, std::integral_constant<int, 6>());
+            case 7: return by_nsw(sd, nmcc, mic, std::integral_constant<int, 7>());
             default: return hipErrorInvalidValue;
         }
     };
+    typedef std::integral_constant<int, 1> C1;
+    typedef std::integral_constant<int, 2> C2;
     auto by_m = [&](auto sd) {
-        switch (mi) {
-            case 1: return by_gs(sd, std::integral_constant<int, 1>());
-            case 2: return by_gs(sd, std::integral_constant<int, 2>());
-            case 4: return by_gs(sd, std::integral_constant<int, 4>());
+        switch (split_pass_code(a.m)) {
+            case 9: return by_gs(sd, C1(), std::integral_constant<int, 1>());
+            case 10: return by_gs(sd, C1(), std::integral_constant<int, 2>());
+            case 12: return by_gs(sd, C1(), std::integral_constant<int, 4>());
+            case 20: return by_gs(sd, C2(), std::integral_constant<int, 4>());
             default: return hipErrorInvalidValue;
         }
     };

@@ -241,15 +241,16 @@ def test_qmv_small_launch_shapes(O, rq, dev, bits, gs, M):
 
 
 # The split GEMV (small launches: a block is one 16-row tile whose waves take
-# contiguous K slices of 1, 2 or 4 256-code stages).  Stage counts that do not
-# divide into the slices leave the last wave a short slice: 9 stages on 9
-# waves of one, 17 / 21 on 2-stage slices, 33 / 63 on 4-stage slices.
+# contiguous K slices of 1, 2 or 4 256-code stages; m <= 4 in one pass of
+# activation rows, 4 < m <= 8 in two).  Stage counts that do not divide into
+# the slices leave the last wave a short slice: 9 stages on 9 waves of one,
+# 17 / 21 on 2-stage slices, 33 / 63 on 4-stage slices.
 SPLIT_SHAPES = [(37, 2304), (130, 4352), (16, 5376), (61, 8448), (200, 16128)]
 
 
 @pytest.mark.parametrize("xdt,sdt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
                                      (torch.float32, torch.bfloat16)])
-@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6, 8])
 @pytest.mark.parametrize("gs", GROUPS)
 @pytest.mark.parametrize("bits", BITS)
 def test_split_gemv_short_slices(O, rq, dev, bits, gs, M, xdt, sdt):
