@@ -99,11 +99,14 @@ int rq_dequantize(const uint32_t* w_q, const void* scales, const void* biases, r
  * transpose=0: y[m, cols] = x[m, rows] . Ŵ.  x_dt and sb_dt may differ
  * (MLX promotes both to a common type); accumulation is fp32; y in y_dt.
  * m <= 16 with transpose=1 runs the decode GEMV; larger m runs the MFMA GEMM.
- * Both multiply on bf16 MFMA operands: fp32 or f16 x is rounded to bf16 once
- * (the GEMV keeps every other step exact: codes enter the MFMA as small
- * integers and s, b are applied in fp32; the GEMM also rounds each s*q + b to
- * bf16).  On N(0,1) fp32 x this puts y about 1.6e-3 (GEMV) and 2.3e-3 (GEMM)
- * Frobenius-relative from the fp32 product; bf16 x loses nothing to it. */
+ * Both multiply on bf16 MFMA operands.  The GEMV keeps every other step exact
+ * (codes enter the MFMA as small integers, s and b are applied in fp32), and
+ * at m <= 2 it multiplies fp32 or f16 x as two bf16 rows, bf16(x) and
+ * bf16(x - bf16(x)), added at the end: y is then within ~1e-5 of the fp32
+ * product.  At 2 < m <= 16 fp32 / f16 x is rounded to bf16 once, and the GEMM
+ * also rounds each s*q + b to bf16: on N(0,1) fp32 x about 1.6e-3 (GEMV) and
+ * 2.3e-3 (GEMM) Frobenius-relative from the fp32 product.  bf16 x loses
+ * nothing to either. */
 int rq_qmm(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
            const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
            int group_size, int bits, int transpose, void* y, rq_dtype y_dt, void* stream);

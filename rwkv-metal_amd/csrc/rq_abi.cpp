@@ -473,10 +473,11 @@ int rq_grouped_plan_init(const rq_problem* problems, int n, rq_dtype x_dt, rq_dt
     if (int rc = check_grouped("rq_grouped_plan_init", problems, n, x_dt, sb_dt, y_dt, m,
                                group_size, bits))
         return rc;
+    const int64_t mk = rq::qmv_rows(x_dt, m);  // MFMA activation rows
     std::vector<int> order;
     for (int i = 0; i < n; ++i) {
         if (problems[i].rows == 0) continue;
-        if (!rq::qmv_stream_covers(problems[i], sb_dt, m, group_size, bits))
+        if (!rq::qmv_stream_covers(problems[i], sb_dt, mk, group_size, bits))
             return fail(RQ_EUNSUPPORTED,
                         "rq_grouped_plan_init: problem %d is outside the planned GEMV (needs "
                         "16-bit scales, cols %% 512 == 0, 16-byte aligned scales/biases, and "
@@ -496,7 +497,7 @@ int rq_grouped_plan_init(const rq_problem* problems, int n, rq_dtype x_dt, rq_dt
     size_t lds = 0;
     for (int i = 0; i < nn; ++i) {
         descs[i] = problems[order[i]];
-        lds = std::max(lds, rq::qmv_stream_lds(m, descs[i].cols, group_size, bits));
+        lds = std::max(lds, rq::qmv_stream_lds(mk, descs[i].cols, group_size, bits));
     }
     const int64_t nblocks = plan_blocks(descs.data(), nn);
     const int64_t dbytes = plan_desc_bytes(nn);
@@ -541,8 +542,9 @@ int rq_grouped_plan_run(const rq_grouped_plan* plan, void* stream) {
     rq::QmvTable t;
     t.descs = (const rq_problem*)(uintptr_t)plan->opaque[0];
     t.blocks = (const uint32_t*)((const uint8_t*)t.descs + plan_desc_bytes(nn));
-    t.m = (int)plan->opaque[2];
     t.x_dt = (int)(plan->opaque[5] & 0xff);
+    t.xsplit = rq::qmv_xsplit(t.x_dt, plan->opaque[2]) ? 1 : 0;
+    t.m = (int)rq::qmv_rows(t.x_dt, plan->opaque[2]);
     t.y_dt = (int)((plan->opaque[5] >> 16) & 0xff);
     const int sb_dt = (int)((plan->opaque[5] >> 8) & 0xff);
     return launch_status(rq::launch_qmv_table(t, (int)nblocks, sb_dt, (int)plan->opaque[3],

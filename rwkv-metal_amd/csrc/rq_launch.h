@@ -45,8 +45,18 @@ hipError_t launch_qmv(const rq_problem* problems, int n, int x_dt, int sb_dt, in
 struct QmvTable {
     const rq_problem* descs;  // device: problem descriptors, longest K first
     const uint32_t* blocks;   // device: per block, problem << 16 | 64-row block of that problem
-    int m, x_dt, y_dt;
+    int m, x_dt, y_dt;        // m: MFMA activation rows (2x the problems' m when xsplit)
+    int xsplit;               // x runs as its hi/lo bf16 split (qmv_xsplit)
 };
+#ifndef RQ_QMV_XSPLIT
+#define RQ_QMV_XSPLIT 1  // 0: round fp32/f16 activations to bf16 in the GEMV as well
+#endif
+// fp32 and f16 activations at m <= 2: the decode GEMV multiplies x as two
+// bf16 rows, bf16(x) and bf16(x - bf16(x)) (16 significant bits: all of f16,
+// fp32 to ~2^-17 relative), in MFMA rows that would otherwise be idle, and
+// adds the two products before the output is stored.
+inline bool qmv_xsplit(int x_dt, int64_t m) { return RQ_QMV_XSPLIT && x_dt != RQ_BF16 && m <= 2; }
+inline int64_t qmv_rows(int x_dt, int64_t m) { return qmv_xsplit(x_dt, m) ? 2 * m : m; }
 constexpr int kQmvLdsBudget = 64 * 1024;  // LDS bytes a GEMV block may stage
 constexpr int kQmvRowsPerBlock = 64;      // rows of one streamed-GEMV block
 // LDS bytes of a streamed-GEMV block for one problem shape.

@@ -114,6 +114,7 @@ struct QmvArgs {
     int x_dt;
     int y_dt;
     int sb_vec;  // scales and biases are 16-byte aligned (vector staging allowed)
+    int xsplit;  // m counts the hi and lo bf16 rows of m/2 activation rows (qmv_xsplit)
 };
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -184,6 +185,22 @@ RQ_DEV void load_x_run_bf16(const void* x, int64_t off, uint32_t* d) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) d[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
     }
+}
+
+// The second part of the hi/lo split of two activations: bf16(a - bf16(a))
+// (the difference is exact in fp32).
+RQ_DEV uint32_t pair_lo(float a, float b) {
+    const uint32_t h = pack_bf16x2(a, b);
+    return pack_bf16x2(a - __uint_as_float(h << 16), b - __uint_as_float(h & 0xffff0000u));
+}
+
+// The lo parts of the split of the 32 fp32 or f16 activations of one run.
+RQ_DEV void load_x_run_lo(const void* x, int x_dt, int64_t off, uint32_t* d) {
+    float f[32];
+    if (x_dt == RQ_F32) load32_f32<RQ_F32>(x, off, f);
+    else load32_f32<RQ_F16>(x, off, f);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) d[i] = pair_lo(f[2 * i], f[2 * i + 1]);
 }
 
 // Streaming load of one run of packed codes.
@@ -346,18 +363,24 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
     sbp_t* sbs = (sbp_t*)(xsum + (((int64_t)M * G + 3) & ~3ll));
     if constexpr (SLDS) {
         if (threadIdx.x < 4) *(u32x4_t*)&xzero[threadIdx.x * 8] = u32x4_t{0u, 0u, 0u, 0u};
-        // Stage x[0..M) as bf16: 8 elements per thread per step.
+        // Stage x[0..M) as bf16: 8 elements per thread per step.  With the
+        // hi/lo split, rows M/2.. are the lo parts of rows 0..M/2-1.
         const int64_t n8 = (int64_t)M * K / 8;
+        const int64_t half8 = args.xsplit ? n8 / 2 : n8;
         for (int64_t e = threadIdx.x; e < n8; e += kBlock) {
             uint32_t d[4];
             if (x_dt == RQ_BF16) {
                 const uint4 v = ((const uint4*)x)[e];
                 d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
             } else {
+                const bool lo = e >= half8;
+                const int64_t es = lo ? e - half8 : e;
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    d[q] = pack_bf16x2(load_dt(x, x_dt, e * 8 + 2 * q),
-                                       load_dt(x, x_dt, e * 8 + 2 * q + 1));
+                for (int q = 0; q < 4; ++q) {
+                    const float a = load_dt(x, x_dt, es * 8 + 2 * q);
+                    const float b = load_dt(x, x_dt, es * 8 + 2 * q + 1);
+                    d[q] = lo ? pair_lo(a, b) : pack_bf16x2(a, b);
+                }
             }
             uint32_t pr[4];  // stored as pairs (x_i, x_{i+4}): the order of the code pairs
             reorder_pairs(d, pr);
@@ -480,9 +503,12 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
                     xg[c][i] = ((const float*)lds)[gi];
                 }
             } else if (a_slot_ok && run_ok && m < M) {
-                if (x_dt == RQ_BF16) load_x_run_bf16<RQ_BF16>(x, (int64_t)m * K + run * 32, xd);
-                else if (x_dt == RQ_F32) load_x_run_bf16<RQ_F32>(x, (int64_t)m * K + run * 32, xd);
-                else load_x_run_bf16<RQ_F16>(x, (int64_t)m * K + run * 32, xd);
+                const int msrc = args.xsplit ? M / 2 : M;  // rows msrc.. are lo parts
+                const int64_t off = (int64_t)(m < msrc ? m : m - msrc) * K + run * 32;
+                if (x_dt == RQ_BF16) load_x_run_bf16<RQ_BF16>(x, off, xd);
+                else if (m >= msrc) load_x_run_lo(x, x_dt, off, xd);
+                else if (x_dt == RQ_F32) load_x_run_bf16<RQ_F32>(x, off, xd);
+                else load_x_run_bf16<RQ_F16>(x, off, xd);
             } else {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) xd[i] = 0u;
@@ -606,6 +632,22 @@ __global__ __launch_bounds__(kBlock) RQ_QMV_OCC void qmv_kernel(const QmvArgs ar
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         const int64_t row = row0 + rb * 16 + lr;
+        if (args.xsplit) {
+            // M <= 4 rows, all in lane group 0's accumulator rows 0..M-1:
+            // output row i is the hi row i plus the lo row i + M/2
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = acc[rb][0][i];
+                if (slots == 4) v[i] += __shfl_xor(v[i], 16, 64);
+                if (slots >= 2) v[i] += __shfl_xor(v[i], 32, 64);
+            }
+            if (lg == 0 && row < R) {
+                store_dt(args.p[p].y, args.y_dt, row, v[0] + (M == 2 ? v[1] : v[2]));
+                if (M == 4) store_dt(args.p[p].y, args.y_dt, R + row, v[1] + v[3]);
+            }
+            continue;
+        }
 #pragma unroll
         for (int c = 0; c < NMC; ++c) {
 #pragma unroll
@@ -814,6 +856,22 @@ RQ_DEV XRaw load_x8(const void* x, int x_dt, int64_t e) {  // e: index of the 8-
     }
     return r;
 }
+// Eight fp32 or f16 activations as the lo part of their split, natural order.
+RQ_DEV void x8_to_bf16_lo(const XRaw& r, int x_dt, uint32_t* d) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float a, b;
+        if (x_dt == RQ_F32) {
+            const u32x4_t& v = q < 2 ? r.lo : r.hi;
+            a = __uint_as_float(v[2 * (q & 1)]);
+            b = __uint_as_float(v[2 * (q & 1) + 1]);
+        } else {
+            a = f16_bits_to_f32(r.lo[q] & 0xffffu);
+            b = f16_bits_to_f32(r.lo[q] >> 16);
+        }
+        d[q] = pair_lo(a, b);
+    }
+}
 RQ_DEV void x8_to_bf16(const XRaw& r, int x_dt, uint32_t* d) {
     if (x_dt == RQ_BF16) {
         d[0] = r.lo[0]; d[1] = r.lo[1]; d[2] = r.lo[2]; d[3] = r.lo[3];
@@ -830,7 +888,7 @@ RQ_DEV void x8_to_bf16(const XRaw& r, int x_dt, uint32_t* d) {
 }
 
 template <int BITS, int SDT, int NMC, int MI, int GSH>
-RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, int y_dt) {
+RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, int y_dt, int xsplit) {
     static_assert(SDT != RQ_F32, "streamed scales are 16-bit");
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
     typedef StreamWin<GSH> W;
@@ -878,9 +936,13 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
     {
         const void* __restrict__ x = P.x;
         const int64_t n8 = (int64_t)M * K / 8;
+        const int64_t half8 = xsplit ? n8 / 2 : n8;  // rows M/2.. are the lo parts
         for (int64_t e = threadIdx.x; e < n8; e += kBlock) {
             uint32_t d[4];
-            x8_to_bf16(load_x8(x, x_dt, e), x_dt, d);
+            const bool lopart = e >= half8;
+            const XRaw r = load_x8(x, x_dt, lopart ? e - half8 : e);
+            if (lopart) x8_to_bf16_lo(r, x_dt, d);
+            else x8_to_bf16(r, x_dt, d);
             uint32_t pr[4];
             reorder_pairs(d, pr);
             *(u32x4_t*)&xs[e * 8] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
@@ -1013,6 +1075,24 @@ RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, in
 
     // sum the four slots (lane groups), then lane group 0 stores rows < R
     const int64_t row = row0 + lr;
+    if (xsplit) {  // M = 2 or 4 rows: output row i is hi row i plus lo row i + M/2
+        float v[MI];
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            v[i] = acc[0][i];
+            v[i] += __shfl_xor(v[i], 16, 64);
+            v[i] += __shfl_xor(v[i], 32, 64);
+        }
+        if (lg == 0 && row < R) {
+            if constexpr (MI == 2) {
+                store_dt(P.y, y_dt, row, v[0] + v[1]);
+            } else if constexpr (MI == 4) {
+                store_dt(P.y, y_dt, row, v[0] + (M == 2 ? v[1] : v[2]));
+                if (M == 4) store_dt(P.y, y_dt, R + row, v[1] + v[3]);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < NMC; ++c)
 #pragma unroll
@@ -1043,14 +1123,14 @@ __global__ __launch_bounds__(kBlock) RQ_STREAM_OCC void qmv_stream_inline(const 
         if (args.block_start[mid] <= bid) lo = mid; else hi = mid - 1;
     }
     qmv_stream_body<BITS, SDT, NMC, MI, GSH>(args.p[lo], bid - args.block_start[lo], args.m,
-                                             args.x_dt, args.y_dt);
+                                             args.x_dt, args.y_dt, args.xsplit);
 }
 
 template <int BITS, int SDT, int NMC, int MI, int GSH>
 __global__ __launch_bounds__(kBlock) RQ_STREAM_OCC void qmv_stream_table(const rq::QmvTable a) {
     const uint32_t e = a.blocks[blockIdx.x];
     const rq_problem P = a.descs[e >> 16];
-    qmv_stream_body<BITS, SDT, NMC, MI, GSH>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
+    qmv_stream_body<BITS, SDT, NMC, MI, GSH>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt, a.xsplit);
 }
 
 // ------------------------------------------------------------ split GEMV
@@ -1145,13 +1225,15 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
 
     // ---- issue every load: x slice, (scale, bias) values, codes
     const int n8 = M * nv * 32;  // 8-element x pieces of the slice
+    const int msrc = args.xsplit ? M / 2 : M;  // rows msrc.. are the lo parts of rows 0..
     XRaw xr[XP];
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
         const int e = lane + 64 * i;
         if (e < n8) {
             const int m = e / (nv * 32), kk = (e - m * nv * 32) * 8;
-            xr[i] = load_x8(P.x, x_dt, ((int64_t)m * K + (int64_t)st0 * 256 + kk) >> 3);
+            const int ms = m < msrc ? m : m - msrc;
+            xr[i] = load_x8(P.x, x_dt, ((int64_t)ms * K + (int64_t)st0 * 256 + kk) >> 3);
         }
     }
     const RQ_GLOBAL uint8_t* sbsrc =
@@ -1192,7 +1274,8 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
         if (e < n8) {
             const int m = e / (nv * 32), kk = (e - m * nv * 32) * 8;
             uint32_t d[4];
-            x8_to_bf16(xr[i], x_dt, d);
+            if (m >= msrc) x8_to_bf16_lo(xr[i], x_dt, d);
+            else x8_to_bf16(xr[i], x_dt, d);
             uint32_t pr[4];
             reorder_pairs(d, pr);
             *(u32x4_t*)&xs[m * KW + kk] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
@@ -1355,6 +1438,17 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
         }
     }
     const int64_t row = row0 + lr;
+    if (args.xsplit) {
+        // M = 2 or 4 rows in one pass, row i in lane group i: output row i is
+        // hi row i plus lo row i + M/2, which lane group i + M/2 holds
+        float mine = 0.f;
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+            if (i == lg) mine = v[0][i];
+        const float other = __shfl(mine, (lane + 16 * msrc) & 63, 64);
+        if (lg < msrc && row < R) store_dt(P.y, args.y_dt, (int64_t)lg * R + row, mine + other);
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < NMC; ++c)
 #pragma unroll
@@ -1909,6 +2003,10 @@ namespace rq {
 // exactly for them).
 static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt, int sb_dt,
                                 int y_dt, int64_t m, int gs, hipStream_t stream) {
+    // from here on m counts MFMA activation rows: with the hi/lo split of
+    // fp32 / f16 x, twice the problem's rows
+    const int xsplit = qmv_xsplit(x_dt, m) ? 1 : 0;
+    m = qmv_rows(x_dt, m);
     const int gs_shift = __builtin_ctz(gs);
     const int MC = 16 >> (7 - gs_shift);
     int nmc = (int)((m + MC - 1) / MC);
@@ -1942,6 +2040,7 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
             a.gs_shift = gs_shift;
             a.x_dt = x_dt;
             a.y_dt = y_dt;
+            a.xsplit = xsplit;
             hipError_t e = launch_split(a, (int)blocks, K, sb_dt, gs, stream);
             if (e != hipSuccess) return e;
         }
@@ -1967,6 +2066,7 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
             a.gs_shift = gs_shift;
             a.x_dt = x_dt;
             a.y_dt = y_dt;
+            a.xsplit = xsplit;
             if (blocks == 0) continue;
             hipError_t e = launch_stream_inline(a, (int)blocks, sb_dt, gs, lds, stream);
             if (e != hipSuccess) return e;
@@ -2000,6 +2100,7 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
         a.gs_shift = gs_shift;
         a.x_dt = x_dt;
         a.y_dt = y_dt;
+        a.xsplit = xsplit;
         a.sb_vec = 1;
         for (int i = 0; i < cnt; ++i)
             a.sb_vec &= (((uintptr_t)a.p[i].scales | (uintptr_t)a.p[i].biases) & 15) == 0;

@@ -190,35 +190,78 @@ def _rel(y, ref):
     return ((y - ref).norm() / ref.norm()).item(), ((y - ref).abs().max() / ref.abs().max()).item()
 
 
+# (R, K, gs, bits): small launches run the split GEMV (16-bit scales) or
+# qmv_kernel (fp32 scales); 32768 rows run the streamed GEMV.
+FP32_SHAPES = [(2048, 2048, 64, 4), (512, 4096, 32, 5), (4096, 2048, 64, 8), (32768, 1024, 64, 4),
+               (32768, 512, 128, 3)]
+
+
 @pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("R,K,gs,bits", [(2048, 2048, 64, 4), (512, 4096, 32, 5), (4096, 2048, 64, 8)])
+@pytest.mark.parametrize("R,K,gs,bits", FP32_SHAPES)
 def test_fp32_activation_precision(O, rq, dev, R, K, gs, bits, sdt):
-    """The MFMA operands are bf16: fp32 activations are rounded to bf16 once
-    when they are staged (MLX's qmv multiplies in fp32, so this is the one
-    place the products differ in kind).  Pins how much that costs on fp32
-    residual-stream inputs, tighter than the general 1e-2 bar: the GEMV
-    (M = 1, 8) is the oracle's product of bf16(x) to fp32 accumulation order
-    (nothing else is rounded), and both the GEMV and the GEMM (M = 300, which
-    also rounds each dequantized weight s*q + b to bf16) stay within 3e-3
-    Frobenius / 4e-3 elementwise of the fp32 product."""
+    """fp32 activations (the reference's residual stream,
+    rwkv_metal/model/rwkv7_x070.py:51; RwkvqNativeLinear casts x to fp32,
+    rwkv_metal/lora/rwkvq_native.py:120).  At m <= 2 the decode GEMV multiplies
+    x as its bf16 hi/lo split (bf16(x), bf16(x - bf16(x))) and adds the two
+    products: within 1e-5 Frobenius / 3e-5 elementwise of MLX's fp32 product
+    (the oracle's, in float64), where one bf16 rounding of x costs ~1.6e-3.
+    Larger m (the wide GEMV at 8, the GEMM at 300) multiplies bf16(x) -- the
+    GEMM also rounds each s*q + b to bf16 -- and stays within 3e-3 / 4e-3;
+    the wide GEMV is the oracle's product of bf16(x) to fp32 summation
+    order."""
     w = weights(R, K, R + K + bits, sdt)
     wq, s, b = O.quantize(w, gs, bits)
     g = torch.Generator().manual_seed(R + K + bits)
-    for M in (1, 8, 300):
+    for M in (1, 2, 8, 300):
+        if M == 300 and R > 4096:
+            continue  # the GEMM is covered at the smaller shapes
         say(f"fp32 activations [{R},{K}] b{bits} g{gs} s={sdt} M={M}")
         x = torch.randn(M, K, generator=g)
         y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
         assert y.dtype == torch.float32
         ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
+        fro, elem = _rel(y, ref)
+        if M <= 2:
+            assert fro <= 1e-5 and elem <= 3e-5, f"M={M} vs fp32 x: {fro:.2e} {elem:.2e}"
+            continue
+        assert fro <= 3e-3 and elem <= 4e-3, f"M={M} vs fp32 x: {fro:.2e} {elem:.2e}"
         refb = O.quantized_matmul(x.to(torch.bfloat16).float(), wq, s, b, True, gs, bits,
                                   out_dtype=torch.float32, weights="exact")
-        fro, elem = _rel(y, ref)
-        assert fro <= 3e-3 and elem <= 4e-3, f"M={M} vs fp32 x: {fro:.2e} {elem:.2e}"
         frob, elemb = _rel(y, refb)
-        if M <= 8:
+        if M == 8:
             assert frob <= 1e-5 and elemb <= 2e-5, f"M={M} vs bf16(x): {frob:.2e} {elemb:.2e}"
         else:
             assert frob <= 2.5e-3, f"M={M} vs bf16(x): {frob:.2e}"
+
+
+def test_fp16_and_planned_fp32_activations_exact(O, rq, dev):
+    """The hi/lo split also carries f16 activations whole (11 significant
+    bits; bf16 scales, so y is fp32), and the planned one-launch schedule
+    (rq_grouped_plan_*) splits fp32 activations like single calls do."""
+    wq, s, b = O.quantize(weights(4096, 2048, 77), 64, 4)
+    for M in (1, 2):
+        x = acts(M, 2048, 78 + M, torch.float16)
+        say(f"f16 activations M={M}")
+        y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
+        assert y.dtype == torch.float32
+        ref = O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32, weights="exact")
+        fro, elem = _rel(y, ref)
+        assert fro <= 1e-5 and elem <= 3e-5, f"f16 M={M}: {fro:.2e} {elem:.2e}"
+    probs = []
+    for i in range(3):
+        wq, s, b = O.quantize(weights(1024 * (i + 1), 1024, 90 + i), 64, 4)
+        probs.append((wq, s, b))
+    for M in (1, 2):
+        xs = [torch.randn(M, 1024, generator=torch.Generator().manual_seed(95 + i)) for i in range(3)]
+        plan = rq.GroupedQmv([x.to(dev) for x in xs], [(a.to(dev), c.to(dev), d.to(dev)) for a, c, d in probs],
+                             64, 4, planned=True)
+        assert plan.plan is not None
+        ys = plan.run()
+        torch.cuda.synchronize()
+        for x, (wq, s, b), y in zip(xs, probs, ys):
+            ref = O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32, weights="exact")
+            fro, elem = _rel(y, ref)
+            assert fro <= 1e-5 and elem <= 3e-5, f"planned M={M}: {fro:.2e} {elem:.2e}"
 
 
 # Small single launches (the K-split kernel) over contraction lengths from
