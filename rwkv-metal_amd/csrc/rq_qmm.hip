@@ -1471,28 +1471,45 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
         }
         const uint8_t* xbase = (const uint8_t*)(x + m0 * R);
         if constexpr (BN == 160) {
-            // chunks 5 jq .. 5 jq + 4 (8 codes each) of row jr of each stage
+            // Lane L of producer wave pw takes row jr = 16 pw + L / 4 of each
+            // stage and its chunks 5 q .. 5 q + 4 (q = L % 4, 8 codes each), so
+            // one code-load instruction covers 16 rows' contiguous 80 B.  A
+            // row's (scale, bias) values of the tile's groups (at most 4 from
+            // g0, 6 at gs 32) are loaded once per lane quad -- lane q takes
+            // group g0 + q, and g0 + 4 + q at gs 32 -- and handed to the lanes
+            // that need them with ds_bpermute (a lane's 40 codes touch at most
+            // two groups, three at gs 32).
             constexpr int NC = 5, WPC = BITS / 4, NG = 3;
             typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-            const int jr = pt & 63, jq = pt >> 6;
+            const int jq = lane & 3, jr = pw * 16 + (lane >> 2);
             const uint32_t* wbase = wq + ((k0 >> 3) + NC * jq) * WPC;
             const int64_t kc0 = k0 + 8 * NC * jq;
-            const int64_t glo = kc0 >> gs_shift;
+            const int64_t g0 = k0 >> gs_shift;                // the tile's first group
+            const int rel0 = (int)((kc0 >> gs_shift) - g0);  // this lane's first group, from g0
+            const bool g32 = gs_shift == 5;
             int gsel[NC];
             uint32_t qdst[NC];
 #pragma unroll
             for (int i = 0; i < NC; ++i) {
-                gsel[i] = (int)(((kc0 + 8 * i) >> gs_shift) - glo);
+                gsel[i] = (int)(((kc0 + 8 * i) >> gs_shift) - (kc0 >> gs_shift));
                 qdst[i] = (uint32_t)(jr * ROWB + (nchunk(NC * jq + i, jr) << 4));
             }
-            int gcl[NG];  // group offsets, clamped inside the row (past-the-row ones are unused)
+            // the groups this lane loads, clamped inside the row (past-the-row
+            // ones are never selected)
+            const int ga = g0 + jq < G ? jq : (int)(G - 1 - g0);
+            const int gb = g0 + 4 + jq < G ? 4 + jq : (int)(G - 1 - g0);
+            const uint16_t* sbase = (const uint16_t*)scales + g0;
+            const uint16_t* bbase = (const uint16_t*)biases + g0;
+            int srcl[NG], slot[NG];  // bpermute byte address and load slot of pairs rel0 + j
 #pragma unroll
-            for (int j = 0; j < NG; ++j) gcl[j] = glo + j < G ? j : (int)(G - 1 - glo);
-            const uint16_t* sbase = (const uint16_t*)scales + glo;
-            const uint16_t* bbase = (const uint16_t*)biases + glo;
+            for (int j = 0; j < NG; ++j) {
+                const int rel = rel0 + j;
+                srcl[j] = ((lane & ~3) | (rel & 3)) * 4;
+                slot[j] = rel >> 2;
+            }
             u32x4_t xv[D][8];
             uint32_t cv[D][NC * WPC];
-            uint16_t sv[D][NG][2];
+            uint32_t sv[D][2];  // scale | bias << 16 of groups g0 + jq and g0 + 4 + jq
             auto issue = [&](int st, int r) {
                 const int sc = st < nst ? st : nst - 1;
                 const uint8_t* xb = xbase + (int64_t)sc * 128;
@@ -1512,11 +1529,11 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                         cv[r][2 * q + 1] = v[1];
                     }
                 }
-#pragma unroll
-                for (int j = 0; j < NG; ++j) {
-                    sv[r][j][0] = *(gh_t)(sbase + row * G + gcl[j]);
-                    sv[r][j][1] = *(gh_t)(bbase + row * G + gcl[j]);
-                }
+                sv[r][0] = (uint32_t)*(gh_t)(sbase + row * G + ga) |
+                           ((uint32_t)*(gh_t)(bbase + row * G + ga) << 16);
+                if (g32)
+                    sv[r][1] = (uint32_t)*(gh_t)(sbase + row * G + gb) |
+                               ((uint32_t)*(gh_t)(bbase + row * G + gb) << 16);
             };
 #pragma unroll
             for (int r = 0; r < D; ++r) issue(r, r);
@@ -1534,8 +1551,17 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                     float sf[NG], bf[NG];
 #pragma unroll
                     for (int j = 0; j < NG; ++j) {
-                        sf[j] = dt_traits<SDT>::to_f32(sv[u][j][0]);
-                        bf[j] = dt_traits<SDT>::to_f32(sv[u][j][1]);
+                        uint32_t pr = 0u;
+                        if (j < 2 || g32) {
+                            pr = (uint32_t)__builtin_amdgcn_ds_bpermute(srcl[j], (int)sv[u][0]);
+                            if (g32) {
+                                const uint32_t p1 =
+                                    (uint32_t)__builtin_amdgcn_ds_bpermute(srcl[j], (int)sv[u][1]);
+                                pr = slot[j] ? p1 : pr;
+                            }
+                        }
+                        sf[j] = dt_traits<SDT>::to_f32((uint16_t)(pr & 0xffffu));
+                        bf[j] = dt_traits<SDT>::to_f32((uint16_t)(pr >> 16));
                     }
 #pragma unroll
                     for (int i = 0; i < NC; ++i) {
@@ -1952,12 +1978,13 @@ hipError_t RQ_CAT(launch_qmm_n_b, RQ_BITS)(const void* x, int x_dt, const uint32
         const int tm = (int)((m + 255) / 256);
         // 160-column tiles where 128-column ones do not divide the output or
         // take more rounds of 256 CUs than it costs to run fewer, wider tiles:
-        // a 160-column tile runs ~1.5x as long as a 128-column one (measured
-        // at M = 4096, R = 2560), so 2560-wide outputs (one round of 256
-        // instead of two of 320) take them and 10240-wide ones (4 rounds of
-        // 1024 against 5 of 1280) do not
+        // a 160-column tile runs ~1.35x as long as a 128-column one (65.8 vs
+        // 48.6 us per round at R = 2560, M = 4096), so 2560-wide outputs (one
+        // round of 256 instead of two of 320) and 10240-wide ones at M = 2048
+        // (2 rounds of 512 against 3 of 640) take them, 10240-wide ones at
+        // M = 4096 (4 rounds of 1024 against 5 of 1280) do not
         auto rounds = [&](int64_t nt) { return (double)((nt + kK64Cus - 1) / kK64Cus); };
-        const bool wide = can160 && (!can128 || 1.5 * rounds((int64_t)tm * (cols / 160)) <
+        const bool wide = can160 && (!can128 || 1.35 * rounds((int64_t)tm * (cols / 160)) <
                                                     rounds((int64_t)tm * (cols / 128)));
         const int tn = (int)(cols / (wide ? 160 : 128));
         const int blocks = ((tm * tn + 7) / 8) * 8;

@@ -196,7 +196,7 @@ FP32_SHAPES = [(2048, 2048, 64, 4), (512, 4096, 32, 5), (4096, 2048, 64, 8), (32
                (32768, 512, 128, 3)]
 
 
-@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("R,K,gs,bits", FP32_SHAPES)
 def test_fp32_activation_precision(O, rq, dev, R, K, gs, bits, sdt):
     """fp32 activations (the reference's residual stream,
