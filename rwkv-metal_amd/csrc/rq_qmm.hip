@@ -1600,8 +1600,10 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
             }
             return;
         }
-        // the dequantization job: run jq of row jr of each stage
-        const int jr = pt & 63, jq = pt >> 6;
+        // the dequantization job: run jq of row jr of each stage; the four
+        // runs of a row go to one lane quad (16 rows per wave), so one code
+        // load covers 16 rows' contiguous 64 B
+        const int jr = pw * 16 + (lane >> 2), jq = lane & 3;
         const uint32_t* wbase = wq + (k0 >> 5) * BITS + jq * BITS;
         const int64_t gidx = (k0 + jq * 32) >> gs_shift;
         const uint16_t* sbase = (const uint16_t*)scales + gidx;
