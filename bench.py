@@ -67,11 +67,12 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline sweep only")
     ap.add_argument("--pmc-workload", nargs="?", const="gemv",
-                    choices=("gemv", "gemm", "gemm_pair"),
+                    choices=("gemv", "gemm", "gemm_pair", "decode"),
                     help="run the headline plan (gemv) or the config-3 [10240, 2560] prefill "
                          "GEMM at M=4096 (gemm) 3x, then 3 calibration copies; gemm_pair: "
                          "qmm_t_k64 and qmm_n_k64 on [2048, 2048] at M=4096 and qmm_t_k64 on "
-                         "[10240, 2560] at M=4096, 3x each; print nothing")
+                         "[10240, 2560] at M=4096, 3x each; decode: the config-2 sweep as one "
+                         "planned launch at M=1, then at M=8, 3x each; print nothing")
     ap.add_argument("--qlora-step-workload", action="store_true",
                     help="run 5 + 20 config-4 QLoRA layer steps (LoRALinear autograd, the "
                          "bench's fused path) for a kernel trace; print the per-step time")
@@ -100,6 +101,16 @@ def pmc_workload(torch, rq, dev, which="gemv"):
     """What the counter passes profile: the headline plan (one launch), or one
     config-3 prefill GEMM, PMC_RUNS times, then COPY_RUNS copies of COPY_BYTES
     (read COPY_BYTES, write COPY_BYTES) as the last dispatches of the process."""
+    if which == "decode":
+        probs, _ = make_sweep(rq, torch, dev, M=1, timed=False)
+        ws = [w for _, _, w in probs]
+        for M in (1, 8):
+            xs = [torch.randn(M, x.shape[-1], device=dev).to(torch.bfloat16) for _, x, _ in probs]
+            run = rq.GroupedQmv(xs, ws, 64, 4).run
+            for _ in range(PMC_RUNS):
+                run()
+            torch.cuda.synchronize()
+        return
     if which == "gemm_pair":
         runs = []
         for (R, K), transposes in (((2048, 2048), (True, False)), ((10240, 2560), (True,))):
