@@ -737,11 +737,11 @@ constexpr int kStreamSlotsMax = 4;  // largest m of the slotted streamed kernel;
 // long as the streamed codes need to turn the L2 over.  64 groups (whole
 // lines) would remove the rest of the refetch at K >= 4096 but need 8 more
 // VGPRs per lane, one wave per SIMD less at 4 bits.
-template <int GSH>
+template <int GSH, int WGV = RQ_QMV_WIN_G>
 struct StreamWin {
     static constexpr int GPS = 256 >> GSH;             // groups per stage: 8, 4, 2
     static constexpr int GPI = 4 * GPS;                // groups per iteration: 32, 16, 8
-    static constexpr int WG = RQ_QMV_WIN_G;            // groups per window
+    static constexpr int WG = WGV;                     // groups per window
     static constexpr int WW = WG * 2;                  // bytes per array per row per window
     static constexpr int IPW = WG / GPI;               // iterations per window: 2, 4, 8
     static constexpr int PB = GSH == 7 ? 8 : 16;       // load size: K % 512 == 0 keeps a row's
@@ -749,6 +749,7 @@ struct StreamWin {
     static constexpr int NP = WW / 2 / PB;             // loads per lane and window
     static constexpr int ROWB = 2 * WW + 16;           // LDS row stride (spreads the banks)
     static constexpr int WAVE_BYTES = 16 * ROWB;
+    static_assert(IPW >= 1 && WG % GPI == 0, "a window holds whole iterations");
 };
 
 template <int N>
@@ -817,10 +818,10 @@ RQ_DEV void load_two_runs(gptr_u32 p, uint32_t* out) {
 // group w*WG + part.  The window after the last one is never read: it loads
 // `spare` instead (the activations: L2-resident, 16-byte aligned, >= 1 KB),
 // so the load stays unconditional without fetching scale lines again.
-template <int GSH>
-RQ_DEV Words<StreamWin<GSH>::WW / 8> load_sb_window(gptr_u16 sbrow, int part, int G, int w,
-                                                     const void* spare) {
-    typedef StreamWin<GSH> W;
+template <int GSH, int WGV = RQ_QMV_WIN_G>
+RQ_DEV Words<StreamWin<GSH, WGV>::WW / 8> load_sb_window(gptr_u16 sbrow, int part, int G, int w,
+                                                          const void* spare) {
+    typedef StreamWin<GSH, WGV> W;
     constexpr int GP = W::PB / 2;  // groups per load
     Words<W::WW / 8> v;
     const bool live = w * W::WG < G;
@@ -1487,10 +1488,30 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
 //    the start of an iteration and written after its MFMAs, behind one
 //    barrier per iteration, so LDS does not grow with K.  Rows m >= M of
 //    the ring are zero, and so is a 1024-column line that idle A lanes read.
+//  * Launches whose rows all have K <= 2048 run a kernel with only the
+//    whole-x schedule (template WH, m <= 8).  Compiled together, the
+//    streamed loop's x registers raise the whole-x loop to 167 VGPRs, and
+//    the compiler's wait analysis, merged over both loops, makes the whole-x
+//    loop wait for code loads of later stages (vmcnt(2)/vmcnt(4) where
+//    vmcnt(6) suffices, vmcnt(1) at each window).  Alone it takes ~100 VGPRs
+//    with one wait per stage for exactly its codes, and (scale, bias)
+//    windows of 16 groups (32 at gs 32: one iteration) keep its block at
+//    40.2 KB of LDS: four blocks, 4 waves per SIMD, per CU (+6 % on the
+//    config-2 K = 2048 projections at M = 8).  Other launches run both
+//    schedules in one kernel and pick per problem: split into two launches,
+//    a mixed sweep lost on the first launch's tail what the second gained.
 // 4- and 8-bit codes: their pieces are whole words.
 constexpr int kWideNS = 4;                // stages per iteration = per staged x chunk
 constexpr int kWideKC = 256 * kWideNS;    // x columns per chunk
 constexpr int kWideRow = kWideKC + 8;     // LDS row stride in elements (+16 B spreads the banks)
+#ifndef RQ_QMV_WIDE_WIN_G
+#define RQ_QMV_WIDE_WIN_G 16
+#endif
+template <int GSH>
+constexpr int wide_win_g() {
+    return StreamWin<GSH>::GPI > RQ_QMV_WIDE_WIN_G ? StreamWin<GSH>::GPI : RQ_QMV_WIDE_WIN_G;
+}
+static_assert(rq::kWideWholeCols <= 2 * kWideKC, "the whole-x kernel stages at most two chunks");
 
 // 4 x 4 transpose of (lane group, register): afterwards register j of lane
 // group g holds what register g of lane group j held.
@@ -1538,12 +1559,15 @@ struct WideLds {
     static constexpr int X_ELEMS = DUMMY + 8;
 };
 
-template <int BITS, int SDT, int MP, int GSH, bool XF32>
+// WH: every problem of the launch has K <= kWideWholeCols and stages x
+// whole (the host launches no longer rows on it); otherwise each problem
+// takes the whole-x schedule when K <= 2048 and streams x in chunks beyond.
+template <int BITS, int SDT, int MP, int GSH, bool XF32, bool WH>
 RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int y_dt) {
     static_assert(BITS == 4 || BITS == 8, "wide GEMV: codes whose 8-code pieces are whole words");
     static_assert(SDT != RQ_F32, "streamed scales are 16-bit");
     static_assert(MP == 8 || MP == 16, "");
-    typedef StreamWin<GSH> W;
+    typedef StreamWin<GSH, (WH && MP == 8) ? wide_win_g<GSH>() : RQ_QMV_WIN_G> W;
     typedef WideLds<MP> L;
     __shared__ __attribute__((aligned(16))) uint16_t xring[L::X_ELEMS];
     __shared__ __attribute__((aligned(16))) uint8_t wins[kWaves * W::WAVE_BYTES];
@@ -1565,7 +1589,7 @@ RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int 
     // ---- first loads: window 0, then codes of stages 0..NS-2
     const gptr_u16 sbrow = (gptr_u16)((lg & 1) ? P.biases : P.scales) + rowc * G;
     const int part = (lg >> 1) * (W::WG / 2);
-    win_t wv = load_sb_window<GSH>(sbrow, part, G, 0, P.x);
+    win_t wv = load_sb_window<GSH, W::WG>(sbrow, part, G, 0, P.x);
     const gptr_u32 wqr = (gptr_u32)P.w_q + rowc * wpr + lg * 2 * BITS;
     auto load_codes = [&](int st, uint32_t* words) {
         const int sc = st < nst ? st : nst - 1;
@@ -1616,7 +1640,7 @@ RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int 
             *(u32x4_t*)&xring[off] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
         }
     };
-    const bool whole = niter <= 2;  // K <= 2048: both chunks staged up front
+    const bool whole = WH || niter <= 2;  // K <= 2048: both chunks staged up front
     {
         XRaw xr0[XQ], xr1[XQ];
         load_chunk(0, xr0);
@@ -1673,7 +1697,7 @@ RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int 
                 // this window of (scale, bias) values into LDS, the next one into registers
                 *(win_t*)win_w = wv;  // read below by other lanes of this wave (LDS runs in order)
                 __builtin_amdgcn_wave_barrier();
-                wv = load_sb_window<GSH>(sbrow, part, G, it / W::IPW + 1, P.x);
+                wv = load_sb_window<GSH, W::WG>(sbrow, part, G, it / W::IPW + 1, P.x);
             }
             XRaw xr[XQ];
             if constexpr (decltype(streaming)::value) load_chunk(it + 1, xr);
@@ -1772,8 +1796,12 @@ RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int 
             }
         }
     };
-    if (whole) run(std::integral_constant<bool, false>());
-    else run(std::integral_constant<bool, true>());
+    if constexpr (WH) {
+        run(std::integral_constant<bool, false>());
+    } else {
+        if (whole) run(std::integral_constant<bool, false>());
+        else run(std::integral_constant<bool, true>());
+    }
 
     const int64_t row = row0 + lr;
     if constexpr (MP == 8) {
@@ -1793,7 +1821,7 @@ RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int 
     }
 }
 
-template <int BITS, int SDT, int MP, int GSH, bool XF32>
+template <int BITS, int SDT, int MP, int GSH, bool XF32, bool WH>
 __global__ __launch_bounds__(kBlock) void qmv_wide_inline(const QmvArgs args) {
     const int bid = blockIdx.x;
     int lo = 0, hi = args.n - 1;
@@ -1801,38 +1829,41 @@ __global__ __launch_bounds__(kBlock) void qmv_wide_inline(const QmvArgs args) {
         const int mid = (lo + hi + 1) >> 1;
         if (args.block_start[mid] <= bid) lo = mid; else hi = mid - 1;
     }
-    qmv_wide_body<BITS, SDT, MP, GSH, XF32>(args.p[lo], bid - args.block_start[lo], args.m,
-                                            args.x_dt, args.y_dt);
+    qmv_wide_body<BITS, SDT, MP, GSH, XF32, WH>(args.p[lo], bid - args.block_start[lo], args.m,
+                                                args.x_dt, args.y_dt);
 }
 
-template <int BITS, int SDT, int MP, int GSH, bool XF32>
+template <int BITS, int SDT, int MP, int GSH, bool XF32, bool WH>
 __global__ __launch_bounds__(kBlock) void qmv_wide_table(const rq::QmvTable a) {
     const uint32_t e = a.blocks[blockIdx.x];
     const rq_problem P = a.descs[e >> 16];
-    qmv_wide_body<BITS, SDT, MP, GSH, XF32>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
+    qmv_wide_body<BITS, SDT, MP, GSH, XF32, WH>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
 }
 
-// F is called with integral_constant-typed (SDT, MP, GSH, XF32).
+// F is called with integral_constant-typed (SDT, MP, GSH, XF32, WH); the
+// whole-x-only kernel (WH) when `whole` and m <= 8.
 template <typename F>
-hipError_t wide_dispatch(int sb_dt, int64_t m, int gs, int x_dt, F&& f) {
+hipError_t wide_dispatch(int sb_dt, int64_t m, int gs, int x_dt, bool whole, F&& f) {
     const int gsh = __builtin_ctz(gs);
     typedef std::integral_constant<int, RQ_BF16> BF;
     typedef std::integral_constant<int, RQ_F16> FH;
-    typedef std::integral_constant<bool, true> XF;
-    typedef std::integral_constant<bool, false> XH;
-#define RQ_W_GSH(SD, MPV, XV)                                                          \
-    switch (gsh) {                                                                     \
-        case 5: return f(SD(), std::integral_constant<int, MPV>(),                     \
-                         std::integral_constant<int, 5>(), XV());                      \
-        case 6: return f(SD(), std::integral_constant<int, MPV>(),                     \
-                         std::integral_constant<int, 6>(), XV());                      \
-        case 7: return f(SD(), std::integral_constant<int, MPV>(),                     \
-                         std::integral_constant<int, 7>(), XV());                      \
-        default: return hipErrorInvalidValue;                                          \
+    typedef std::integral_constant<bool, true> T;
+    typedef std::integral_constant<bool, false> N;
+#define RQ_W_WH(SD, MPV, G, XV)                                                            \
+    if (whole && MPV == 8)                                                                 \
+        return f(SD(), std::integral_constant<int, MPV>(), std::integral_constant<int, G>(), \
+                 XV(), std::integral_constant<bool, MPV == 8>());                          \
+    return f(SD(), std::integral_constant<int, MPV>(), std::integral_constant<int, G>(), XV(), N());
+#define RQ_W_GSH(SD, MPV, XV)                       \
+    switch (gsh) {                                  \
+        case 5: { RQ_W_WH(SD, MPV, 5, XV) }         \
+        case 6: { RQ_W_WH(SD, MPV, 6, XV) }         \
+        case 7: { RQ_W_WH(SD, MPV, 7, XV) }         \
+        default: return hipErrorInvalidValue;       \
     }
 #define RQ_W_X(SD, MPV)                                  \
-    if (x_dt == RQ_F32) { RQ_W_GSH(SD, MPV, XF) }        \
-    RQ_W_GSH(SD, MPV, XH)
+    if (x_dt == RQ_F32) { RQ_W_GSH(SD, MPV, T) }         \
+    RQ_W_GSH(SD, MPV, N)
 #define RQ_W_MP(SD)                      \
     if (m <= 8) { RQ_W_X(SD, 8) }        \
     RQ_W_X(SD, 16)
@@ -1841,6 +1872,7 @@ hipError_t wide_dispatch(int sb_dt, int64_t m, int gs, int x_dt, F&& f) {
 #undef RQ_W_MP
 #undef RQ_W_X
 #undef RQ_W_GSH
+#undef RQ_W_WH
 }
 
 // Template dispatch shared by both launch forms: F is called with
@@ -1880,9 +1912,13 @@ hipError_t launch_stream_inline(const QmvArgs& a, int blocks, int sb_dt, int gs,
                                 hipStream_t stream) {
     if (a.m > kStreamSlotsMax) {
         if constexpr (RQ_BITS == 4 || RQ_BITS == 8) {
-            return wide_dispatch(sb_dt, a.m, gs, a.x_dt, [&](auto sd, auto mp, auto gsh, auto xf) {
+            // a bucket's problems share cols
+            const bool whole = a.p[0].cols <= rq::kWideWholeCols;
+            return wide_dispatch(sb_dt, a.m, gs, a.x_dt, whole,
+                                 [&](auto sd, auto mp, auto gsh, auto xf, auto wh) {
                 hipLaunchKernelGGL((qmv_wide_inline<RQ_BITS, decltype(sd)::value, decltype(mp)::value,
-                                                    decltype(gsh)::value, decltype(xf)::value>),
+                                                    decltype(gsh)::value, decltype(xf)::value,
+                                                    decltype(wh)::value>),
                                    dim3(blocks), dim3(kBlock), 0, stream, a);
                 return hipGetLastError();
             });
@@ -1972,13 +2008,16 @@ hipError_t launch_split(const QmvArgs& a, int blocks, int64_t cols, int sb_dt, i
     return sb_dt == RQ_BF16 ? by_m(BF()) : by_m(FH());
 }
 
-hipError_t launch_stream_table(const rq::QmvTable& a, int blocks, int sb_dt, int gs, size_t lds,
-                               hipStream_t stream) {
+hipError_t launch_stream_table(const rq::QmvTable& a, int blocks, int nlong, int sb_dt, int gs,
+                               size_t lds, hipStream_t stream) {
     if (a.m > kStreamSlotsMax) {
         if constexpr (RQ_BITS == 4 || RQ_BITS == 8) {
-            return wide_dispatch(sb_dt, a.m, gs, a.x_dt, [&](auto sd, auto mp, auto gsh, auto xf) {
+            // nlong: blocks of problems with cols > kWideWholeCols
+            return wide_dispatch(sb_dt, a.m, gs, a.x_dt, nlong == 0,
+                                 [&](auto sd, auto mp, auto gsh, auto xf, auto wh) {
                 hipLaunchKernelGGL((qmv_wide_table<RQ_BITS, decltype(sd)::value, decltype(mp)::value,
-                                                   decltype(gsh)::value, decltype(xf)::value>),
+                                                   decltype(gsh)::value, decltype(xf)::value,
+                                                   decltype(wh)::value>),
                                    dim3(blocks), dim3(kBlock), 0, stream, a);
                 return hipGetLastError();
             });
@@ -2134,9 +2173,9 @@ bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs, int bi
 }
 #endif
 
-hipError_t RQ_CAT(launch_qmv_table_b, RQ_BITS)(const QmvTable& t, int blocks, int sb_dt, int gs,
-                                               size_t lds, hipStream_t stream) {
-    return launch_stream_table(t, blocks, sb_dt, gs, lds, stream);
+hipError_t RQ_CAT(launch_qmv_table_b, RQ_BITS)(const QmvTable& t, int blocks, int nlong, int sb_dt,
+                                               int gs, size_t lds, hipStream_t stream) {
+    return launch_stream_table(t, blocks, nlong, sb_dt, gs, lds, stream);
 }
 
 hipError_t RQ_CAT(launch_qmv_b, RQ_BITS)(const rq_problem* problems, int n, int x_dt, int sb_dt,

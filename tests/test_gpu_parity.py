@@ -696,6 +696,40 @@ def test_planned_wide_qmv_dtypes(O, rq, dev, xdt, sdt):
         rel_check(y, ref, what=f"planned wide {xdt} {sdt}")
 
 
+# Launches whose rows all have K <= 2048 run the whole-x kernel (a separate
+# instantiation with its own (scale, bias) window size); with one longer
+# problem in the set the launch runs the kernel with both x schedules.
+WIDE_SHORT_SHAPES = [(100, 512), (64, 1024), (17, 2048), (40, 1536)]
+
+
+@pytest.mark.parametrize("M", [5, 8])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", [4, 8])
+def test_planned_wide_whole_x_kernel(O, rq, dev, bits, gs, M):
+    """The whole-x kernel against the oracle, and bit for bit against the
+    same problems run in a launch that also holds a K = 8192 problem."""
+    say(f"planned wide whole-x bits={bits} gs={gs} M={M}")
+    seed = 5600 + 10 * bits + gs + M
+    plan, refs, xs, ws = _planned(O, rq, dev, WIDE_SHORT_SHAPES, M, gs, bits, seed)
+    ys = [y.clone() for y in plan.run()]
+    for y, ref in zip(ys, refs):
+        rel_check(y, ref, what=f"planned wide whole-x b{bits} g{gs} M{M}")
+    wl = weights(33, 8192, seed + 99)
+    wq, s, b = O.quantize(wl, gs, bits)
+    mixed = rq.GroupedQmv(xs + [acts(M, 8192, seed + 99).to(dev)],
+                          ws + [(wq.to(dev), s.to(dev), b.to(dev))], gs, bits, planned=True)
+    for i, (y, ym) in enumerate(zip(ys, mixed.run())):
+        assert bits_equal(y, ym), f"problem {i}: whole-x kernel differs from the mixed launch"
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16])
+def test_planned_wide_whole_x_dtypes(O, rq, dev, xdt):
+    say(f"planned wide whole-x x={xdt}")
+    plan, refs, _, _ = _planned(O, rq, dev, WIDE_SHORT_SHAPES, 6, 64, 4, 5990, xdt, torch.float16)
+    for y, ref in zip(plan.run(), refs):
+        rel_check(y, ref, what=f"planned wide whole-x {xdt}")
+
+
 def test_planned_rejects_uncovered_sets(O, rq, dev):
     """cols not a multiple of 512, or 4 < m <= 16 with codes other than 4- or
     8-bit: planned=True raises, auto falls back."""
