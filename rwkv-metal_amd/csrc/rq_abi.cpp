@@ -8,7 +8,6 @@
 
 #include <algorithm>
 #include <cstdarg>
-#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -28,7 +27,7 @@ namespace rq {
                                  int, int64_t, int64_t, int64_t, int, void*, int, hipStream_t,  \
                                  const LoraArgs*);
 #define RQ_DECLARE_TABLE(B)                                                                    \
-    hipError_t launch_qmv_table_b##B(const QmvTable&, int, int, int, int, size_t, hipStream_t);
+    hipError_t launch_qmv_table_b##B(const QmvTable&, int, int, int, size_t, hipStream_t);
 RQ_DECLARE_TABLE(2)
 RQ_DECLARE_TABLE(3)
 RQ_DECLARE_TABLE(4)
@@ -36,15 +35,15 @@ RQ_DECLARE_TABLE(5)
 RQ_DECLARE_TABLE(6)
 RQ_DECLARE_TABLE(8)
 
-hipError_t launch_qmv_table(const QmvTable& t, int blocks, int nlong, int sb_dt, int gs, int bits,
+hipError_t launch_qmv_table(const QmvTable& t, int blocks, int sb_dt, int gs, int bits,
                             size_t lds, hipStream_t stream) {
     switch (bits) {
-        case 2: return launch_qmv_table_b2(t, blocks, nlong, sb_dt, gs, lds, stream);
-        case 3: return launch_qmv_table_b3(t, blocks, nlong, sb_dt, gs, lds, stream);
-        case 4: return launch_qmv_table_b4(t, blocks, nlong, sb_dt, gs, lds, stream);
-        case 5: return launch_qmv_table_b5(t, blocks, nlong, sb_dt, gs, lds, stream);
-        case 6: return launch_qmv_table_b6(t, blocks, nlong, sb_dt, gs, lds, stream);
-        case 8: return launch_qmv_table_b8(t, blocks, nlong, sb_dt, gs, lds, stream);
+        case 2: return launch_qmv_table_b2(t, blocks, sb_dt, gs, lds, stream);
+        case 3: return launch_qmv_table_b3(t, blocks, sb_dt, gs, lds, stream);
+        case 4: return launch_qmv_table_b4(t, blocks, sb_dt, gs, lds, stream);
+        case 5: return launch_qmv_table_b5(t, blocks, sb_dt, gs, lds, stream);
+        case 6: return launch_qmv_table_b6(t, blocks, sb_dt, gs, lds, stream);
+        case 8: return launch_qmv_table_b8(t, blocks, sb_dt, gs, lds, stream);
         default: return hipErrorInvalidValue;
     }
 }
@@ -501,12 +500,6 @@ int rq_grouped_plan_init(const rq_problem* problems, int n, rq_dtype x_dt, rq_dt
         lds = std::max(lds, rq::qmv_stream_lds(mk, descs[i].cols, group_size, bits));
     }
     const int64_t nblocks = plan_blocks(descs.data(), nn);
-    if (nblocks > INT32_MAX)
-        return fail(RQ_EUNSUPPORTED, "rq_grouped_plan_init: more than 2^31 row blocks");
-    // blocks of the problems with cols > kWideWholeCols (sorted first)
-    int64_t nlong = 0;
-    for (int i = 0; i < nn && descs[i].cols > rq::kWideWholeCols; ++i)
-        nlong += (descs[i].rows + rq::kQmvRowsPerBlock - 1) / rq::kQmvRowsPerBlock;
     const int64_t dbytes = plan_desc_bytes(nn);
     const int64_t need = dbytes + 4 * nblocks;
     if (nn > 0) {
@@ -530,7 +523,7 @@ int rq_grouped_plan_init(const rq_problem* problems, int n, rq_dtype x_dt, rq_dt
             return fail(RQ_ELAUNCH, "rq_grouped_plan_init: table upload failed: %s", hipGetErrorString(e));
     }
     plan->opaque[0] = (int64_t)(uintptr_t)table;
-    plan->opaque[1] = nblocks | (nlong << 32);
+    plan->opaque[1] = nblocks;
     plan->opaque[2] = m;
     plan->opaque[3] = group_size;
     plan->opaque[4] = bits;
@@ -543,8 +536,7 @@ int rq_grouped_plan_init(const rq_problem* problems, int n, rq_dtype x_dt, rq_dt
 int rq_grouped_plan_run(const rq_grouped_plan* plan, void* stream) {
     if (!plan || plan->opaque[7] != kPlanMagic)
         return fail(RQ_EINVAL, "rq_grouped_plan_run: not an initialised plan");
-    const int64_t nblocks = plan->opaque[1] & 0xffffffffll;
-    const int nlong = (int)(plan->opaque[1] >> 32);
+    const int64_t nblocks = plan->opaque[1];
     if (nblocks == 0) return ok();
     const int nn = (int)(plan->opaque[5] >> 24);
     rq::QmvTable t;
@@ -555,7 +547,7 @@ int rq_grouped_plan_run(const rq_grouped_plan* plan, void* stream) {
     t.m = (int)rq::qmv_rows(t.x_dt, plan->opaque[2]);
     t.y_dt = (int)((plan->opaque[5] >> 16) & 0xff);
     const int sb_dt = (int)((plan->opaque[5] >> 8) & 0xff);
-    return launch_status(rq::launch_qmv_table(t, (int)nblocks, nlong, sb_dt, (int)plan->opaque[3],
+    return launch_status(rq::launch_qmv_table(t, (int)nblocks, sb_dt, (int)plan->opaque[3],
                                               (int)plan->opaque[4], (size_t)plan->opaque[6],
                                               (hipStream_t)stream),
                          "rq_grouped_plan_run");

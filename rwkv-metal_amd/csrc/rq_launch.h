@@ -64,16 +64,7 @@ size_t qmv_stream_lds(int64_t m, int64_t cols, int gs, int bits);
 // Whether the streamed GEMV covers a problem (16-bit scales, cols % 512 == 0,
 // 16-byte aligned scales/biases, staging within budget).
 bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs, int bits);
-// The wide GEMV (4 < m <= 16) stages x whole for rows of up to this many
-// columns and streams it in chunks beyond; launches with no longer rows run
-// a kernel specialised for the whole-x schedule.
-#ifndef RQ_WIDE_WHOLE_COLS
-#define RQ_WIDE_WHOLE_COLS 2048
-#endif
-constexpr int64_t kWideWholeCols = RQ_WIDE_WHOLE_COLS;
-// A planned GEMV launch over t's `blocks` blocks; the first `nlong` belong to
-// problems with cols > kWideWholeCols (the plan sorts them first).
-hipError_t launch_qmv_table(const QmvTable& t, int blocks, int nlong, int sb_dt, int gs, int bits,
+hipError_t launch_qmv_table(const QmvTable& t, int blocks, int sb_dt, int gs, int bits,
                             size_t lds, hipStream_t stream);
 
 // Low-rank term fused into the output stage of the 64-wide-stage GEMMs:

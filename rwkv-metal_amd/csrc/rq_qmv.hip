@@ -1483,23 +1483,24 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
 //    same A fragment with a constant B (bf16 1.0), so only the pair-permuted
 //    bf16 x is staged: per group, acc += s D + (b - 128 s) X (8-bit: b X).
 //  * x lives in a two-slot LDS ring of 1024-column chunks (one iteration of
-//    4 stages each).  K <= 2048 is staged whole up front (no barrier in the
-//    loop); longer rows stream chunks: the next chunk's loads are issued at
-//    the start of an iteration and written after its MFMAs, behind one
-//    barrier per iteration, so LDS does not grow with K.  Rows m >= M of
-//    the ring are zero, and so is a 1024-column line that idle A lanes read.
-//  * Launches whose rows all have K <= 2048 run a kernel with only the
-//    whole-x schedule (template WH, m <= 8).  Compiled together, the
-//    streamed loop's x registers raise the whole-x loop to 167 VGPRs, and
-//    the compiler's wait analysis, merged over both loops, makes the whole-x
-//    loop wait for code loads of later stages (vmcnt(2)/vmcnt(4) where
-//    vmcnt(6) suffices, vmcnt(1) at each window).  Alone it takes ~100 VGPRs
-//    with one wait per stage for exactly its codes, and (scale, bias)
-//    windows of 16 groups (32 at gs 32: one iteration) keep its block at
-//    40.2 KB of LDS: four blocks, 4 waves per SIMD, per CU (+6 % on the
-//    config-2 K = 2048 projections at M = 8).  Other launches run both
-//    schedules in one kernel and pick per problem: split into two launches,
-//    a mixed sweep lost on the first launch's tail what the second gained.
+//    4 stages each), staged for the rows m < M; rows m >= M of the ring are
+//    zero, and so is a 1024-column line that idle A lanes read.  Two
+//    schedules:
+//    - m <= 8 (MP = 8): the ring holds a pair of chunks (2048 columns); a row
+//      of K <= 2048 is staged whole before the loop, a longer one restages
+//      the next pair behind two barriers every two iterations.  This loop
+//      takes ~116 VGPRs with one wait per stage for exactly its codes, and
+//      (scale, bias) windows of 16 groups (32 at gs 32: one iteration) keep
+//      the block at 40.2 KB of LDS: 4 waves per SIMD.
+//    - m > 8 (MP = 16): K <= 2048 is staged whole up front; longer rows stream chunks,
+//      the next chunk's loads issued at the start of an iteration and
+//      written after its MFMAs, behind one barrier per iteration.  Both
+//      loops live in one kernel.  At MP = 8 that form took 167 VGPRs (3 waves
+//      per SIMD), and the compiler's wait analysis, merged over both loops,
+//      made the whole-x loop wait for code loads of later stages
+//      (vmcnt(2)/vmcnt(4) where vmcnt(6) suffices, vmcnt(1) at each window);
+//      the pair schedule measured +3 % on the config-2 sweep at M = 8 (+5 %
+//      on its K = 2048 projections, equal on K = 8192).
 // 4- and 8-bit codes: their pieces are whole words.
 constexpr int kWideNS = 4;                // stages per iteration = per staged x chunk
 constexpr int kWideKC = 256 * kWideNS;    // x columns per chunk
@@ -1511,7 +1512,6 @@ template <int GSH>
 constexpr int wide_win_g() {
     return StreamWin<GSH>::GPI > RQ_QMV_WIDE_WIN_G ? StreamWin<GSH>::GPI : RQ_QMV_WIDE_WIN_G;
 }
-static_assert(rq::kWideWholeCols <= 2 * kWideKC, "the whole-x kernel stages at most two chunks");
 
 // 4 x 4 transpose of (lane group, register): afterwards register j of lane
 // group g holds what register g of lane group j held.
@@ -1559,15 +1559,15 @@ struct WideLds {
     static constexpr int X_ELEMS = DUMMY + 8;
 };
 
-// WH: every problem of the launch has K <= kWideWholeCols and stages x
-// whole (the host launches no longer rows on it); otherwise each problem
-// takes the whole-x schedule when K <= 2048 and streams x in chunks beyond.
-template <int BITS, int SDT, int MP, int GSH, bool XF32, bool WH>
+// XP: x staged by pairs of chunks (restaged behind barriers); otherwise
+// whole when K <= 2048 and streamed chunk by chunk beyond.
+template <int BITS, int SDT, int MP, int GSH, bool XF32>
 RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int y_dt) {
     static_assert(BITS == 4 || BITS == 8, "wide GEMV: codes whose 8-code pieces are whole words");
     static_assert(SDT != RQ_F32, "streamed scales are 16-bit");
     static_assert(MP == 8 || MP == 16, "");
-    typedef StreamWin<GSH, (WH && MP == 8) ? wide_win_g<GSH>() : RQ_QMV_WIN_G> W;
+    constexpr bool XP = MP == 8;  // x by pairs of chunks, restaged behind barriers
+    typedef StreamWin<GSH, XP ? wide_win_g<GSH>() : RQ_QMV_WIN_G> W;
     typedef WideLds<MP> L;
     __shared__ __attribute__((aligned(16))) uint16_t xring[L::X_ELEMS];
     __shared__ __attribute__((aligned(16))) uint8_t wins[kWaves * W::WAVE_BYTES];
@@ -1640,7 +1640,7 @@ RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int 
             *(u32x4_t*)&xring[off] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
         }
     };
-    const bool whole = WH || niter <= 2;  // K <= 2048: both chunks staged up front
+    const bool whole = XP || niter <= 2;  // both chunks staged up front
     {
         XRaw xr0[XQ], xr1[XQ];
         load_chunk(0, xr0);
@@ -1692,6 +1692,19 @@ RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int 
     f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
     auto run = [&](auto streaming) {
         for (int it = 0; it < niter; ++it) {
+            if constexpr (XP) {
+                // rows longer than two chunks: the next pair is staged behind two
+                // barriers once every wave is done with the previous one
+                if (it > 0 && (it & 1) == 0) {
+                    XRaw xa[XQ], xb[XQ];
+                    load_chunk(it, xa);
+                    load_chunk(it + 1, xb);
+                    __syncthreads();
+                    store_chunk(0, xa);
+                    store_chunk(1, xb);
+                    __syncthreads();
+                }
+            }
             const int itw = it % W::IPW;
             if (itw == 0) {
                 // this window of (scale, bias) values into LDS, the next one into registers
@@ -1796,7 +1809,7 @@ RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int 
             }
         }
     };
-    if constexpr (WH) {
+    if constexpr (XP) {
         run(std::integral_constant<bool, false>());
     } else {
         if (whole) run(std::integral_constant<bool, false>());
@@ -1821,7 +1834,7 @@ RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int 
     }
 }
 
-template <int BITS, int SDT, int MP, int GSH, bool XF32, bool WH>
+template <int BITS, int SDT, int MP, int GSH, bool XF32>
 __global__ __launch_bounds__(kBlock) void qmv_wide_inline(const QmvArgs args) {
     const int bid = blockIdx.x;
     int lo = 0, hi = args.n - 1;
@@ -1829,41 +1842,38 @@ __global__ __launch_bounds__(kBlock) void qmv_wide_inline(const QmvArgs args) {
         const int mid = (lo + hi + 1) >> 1;
         if (args.block_start[mid] <= bid) lo = mid; else hi = mid - 1;
     }
-    qmv_wide_body<BITS, SDT, MP, GSH, XF32, WH>(args.p[lo], bid - args.block_start[lo], args.m,
-                                                args.x_dt, args.y_dt);
+    qmv_wide_body<BITS, SDT, MP, GSH, XF32>(args.p[lo], bid - args.block_start[lo], args.m,
+                                            args.x_dt, args.y_dt);
 }
 
-template <int BITS, int SDT, int MP, int GSH, bool XF32, bool WH>
+template <int BITS, int SDT, int MP, int GSH, bool XF32>
 __global__ __launch_bounds__(kBlock) void qmv_wide_table(const rq::QmvTable a) {
     const uint32_t e = a.blocks[blockIdx.x];
     const rq_problem P = a.descs[e >> 16];
-    qmv_wide_body<BITS, SDT, MP, GSH, XF32, WH>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
+    qmv_wide_body<BITS, SDT, MP, GSH, XF32>(P, (int)(e & 0xffffu), a.m, a.x_dt, a.y_dt);
 }
 
-// F is called with integral_constant-typed (SDT, MP, GSH, XF32, WH); the
-// whole-x-only kernel (WH) when `whole` and m <= 8.
+// F is called with integral_constant-typed (SDT, MP, GSH, XF32).
 template <typename F>
-hipError_t wide_dispatch(int sb_dt, int64_t m, int gs, int x_dt, bool whole, F&& f) {
+hipError_t wide_dispatch(int sb_dt, int64_t m, int gs, int x_dt, F&& f) {
     const int gsh = __builtin_ctz(gs);
     typedef std::integral_constant<int, RQ_BF16> BF;
     typedef std::integral_constant<int, RQ_F16> FH;
-    typedef std::integral_constant<bool, true> T;
-    typedef std::integral_constant<bool, false> N;
-#define RQ_W_WH(SD, MPV, G, XV)                                                            \
-    if (whole && MPV == 8)                                                                 \
-        return f(SD(), std::integral_constant<int, MPV>(), std::integral_constant<int, G>(), \
-                 XV(), std::integral_constant<bool, MPV == 8>());                          \
-    return f(SD(), std::integral_constant<int, MPV>(), std::integral_constant<int, G>(), XV(), N());
-#define RQ_W_GSH(SD, MPV, XV)                       \
-    switch (gsh) {                                  \
-        case 5: { RQ_W_WH(SD, MPV, 5, XV) }         \
-        case 6: { RQ_W_WH(SD, MPV, 6, XV) }         \
-        case 7: { RQ_W_WH(SD, MPV, 7, XV) }         \
-        default: return hipErrorInvalidValue;       \
+    typedef std::integral_constant<bool, true> XF;
+    typedef std::integral_constant<bool, false> XH;
+#define RQ_W_GSH(SD, MPV, XV)                                                          \
+    switch (gsh) {                                                                     \
+        case 5: return f(SD(), std::integral_constant<int, MPV>(),                     \
+                         std::integral_constant<int, 5>(), XV());                      \
+        case 6: return f(SD(), std::integral_constant<int, MPV>(),                     \
+                         std::integral_constant<int, 6>(), XV());                      \
+        case 7: return f(SD(), std::integral_constant<int, MPV>(),                     \
+                         std::integral_constant<int, 7>(), XV());                      \
+        default: return hipErrorInvalidValue;                                          \
     }
 #define RQ_W_X(SD, MPV)                                  \
-    if (x_dt == RQ_F32) { RQ_W_GSH(SD, MPV, T) }         \
-    RQ_W_GSH(SD, MPV, N)
+    if (x_dt == RQ_F32) { RQ_W_GSH(SD, MPV, XF) }        \
+    RQ_W_GSH(SD, MPV, XH)
 #define RQ_W_MP(SD)                      \
     if (m <= 8) { RQ_W_X(SD, 8) }        \
     RQ_W_X(SD, 16)
@@ -1872,7 +1882,6 @@ hipError_t wide_dispatch(int sb_dt, int64_t m, int gs, int x_dt, bool whole, F&&
 #undef RQ_W_MP
 #undef RQ_W_X
 #undef RQ_W_GSH
-#undef RQ_W_WH
 }
 
 // Template dispatch shared by both launch forms: F is called with
@@ -1912,13 +1921,9 @@ hipError_t launch_stream_inline(const QmvArgs& a, int blocks, int sb_dt, int gs,
                                 hipStream_t stream) {
     if (a.m > kStreamSlotsMax) {
         if constexpr (RQ_BITS == 4 || RQ_BITS == 8) {
-            // a bucket's problems share cols
-            const bool whole = a.p[0].cols <= rq::kWideWholeCols;
-            return wide_dispatch(sb_dt, a.m, gs, a.x_dt, whole,
-                                 [&](auto sd, auto mp, auto gsh, auto xf, auto wh) {
+            return wide_dispatch(sb_dt, a.m, gs, a.x_dt, [&](auto sd, auto mp, auto gsh, auto xf) {
                 hipLaunchKernelGGL((qmv_wide_inline<RQ_BITS, decltype(sd)::value, decltype(mp)::value,
-                                                    decltype(gsh)::value, decltype(xf)::value,
-                                                    decltype(wh)::value>),
+                                                    decltype(gsh)::value, decltype(xf)::value>),
                                    dim3(blocks), dim3(kBlock), 0, stream, a);
                 return hipGetLastError();
             });
@@ -2008,16 +2013,13 @@ hipError_t launch_split(const QmvArgs& a, int blocks, int64_t cols, int sb_dt, i
     return sb_dt == RQ_BF16 ? by_m(BF()) : by_m(FH());
 }
 
-hipError_t launch_stream_table(const rq::QmvTable& a, int blocks, int nlong, int sb_dt, int gs,
-                               size_t lds, hipStream_t stream) {
+hipError_t launch_stream_table(const rq::QmvTable& a, int blocks, int sb_dt, int gs, size_t lds,
+                               hipStream_t stream) {
     if (a.m > kStreamSlotsMax) {
         if constexpr (RQ_BITS == 4 || RQ_BITS == 8) {
-            // nlong: blocks of problems with cols > kWideWholeCols
-            return wide_dispatch(sb_dt, a.m, gs, a.x_dt, nlong == 0,
-                                 [&](auto sd, auto mp, auto gsh, auto xf, auto wh) {
+            return wide_dispatch(sb_dt, a.m, gs, a.x_dt, [&](auto sd, auto mp, auto gsh, auto xf) {
                 hipLaunchKernelGGL((qmv_wide_table<RQ_BITS, decltype(sd)::value, decltype(mp)::value,
-                                                   decltype(gsh)::value, decltype(xf)::value,
-                                                   decltype(wh)::value>),
+                                                   decltype(gsh)::value, decltype(xf)::value>),
                                    dim3(blocks), dim3(kBlock), 0, stream, a);
                 return hipGetLastError();
             });
@@ -2173,9 +2175,9 @@ bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs, int bi
 }
 #endif
 
-hipError_t RQ_CAT(launch_qmv_table_b, RQ_BITS)(const QmvTable& t, int blocks, int nlong, int sb_dt,
-                                               int gs, size_t lds, hipStream_t stream) {
-    return launch_stream_table(t, blocks, nlong, sb_dt, gs, lds, stream);
+hipError_t RQ_CAT(launch_qmv_table_b, RQ_BITS)(const QmvTable& t, int blocks, int sb_dt, int gs,
+                                               size_t lds, hipStream_t stream) {
+    return launch_stream_table(t, blocks, sb_dt, gs, lds, stream);
 }
 
 hipError_t RQ_CAT(launch_qmv_b, RQ_BITS)(const rq_problem* problems, int n, int x_dt, int sb_dt,

@@ -696,38 +696,35 @@ def test_planned_wide_qmv_dtypes(O, rq, dev, xdt, sdt):
         rel_check(y, ref, what=f"planned wide {xdt} {sdt}")
 
 
-# Launches whose rows all have K <= 2048 run the whole-x kernel (a separate
-# instantiation with its own (scale, bias) window size); with one longer
-# problem in the set the launch runs the kernel with both x schedules.
-WIDE_SHORT_SHAPES = [(100, 512), (64, 1024), (17, 2048), (40, 1536)]
+# At m <= 8 the wide kernel stages x by pairs of 1024-column chunks and
+# restages the next pair behind two barriers: rows of one pair, of a pair and
+# a partial chunk (2560, 3584) and of four pairs (8192) in one launch.
+WIDE_PAIR_SHAPES = [(100, 512), (17, 2048), (40, 1536), (24, 2560), (20, 3584), (33, 8192)]
 
 
 @pytest.mark.parametrize("M", [5, 8])
 @pytest.mark.parametrize("gs", GROUPS)
 @pytest.mark.parametrize("bits", [4, 8])
-def test_planned_wide_whole_x_kernel(O, rq, dev, bits, gs, M):
-    """The whole-x kernel against the oracle, and bit for bit against the
-    same problems run in a launch that also holds a K = 8192 problem."""
-    say(f"planned wide whole-x bits={bits} gs={gs} M={M}")
+def test_planned_wide_pair_restaging(O, rq, dev, bits, gs, M):
+    """Against the oracle, and bit for bit against each problem run alone
+    (a launch's problems do not interact through the restaged ring)."""
+    say(f"planned wide pair restaging bits={bits} gs={gs} M={M}")
     seed = 5600 + 10 * bits + gs + M
-    plan, refs, xs, ws = _planned(O, rq, dev, WIDE_SHORT_SHAPES, M, gs, bits, seed)
+    plan, refs, xs, ws = _planned(O, rq, dev, WIDE_PAIR_SHAPES, M, gs, bits, seed)
     ys = [y.clone() for y in plan.run()]
-    for y, ref in zip(ys, refs):
-        rel_check(y, ref, what=f"planned wide whole-x b{bits} g{gs} M{M}")
-    wl = weights(33, 8192, seed + 99)
-    wq, s, b = O.quantize(wl, gs, bits)
-    mixed = rq.GroupedQmv(xs + [acts(M, 8192, seed + 99).to(dev)],
-                          ws + [(wq.to(dev), s.to(dev), b.to(dev))], gs, bits, planned=True)
-    for i, (y, ym) in enumerate(zip(ys, mixed.run())):
-        assert bits_equal(y, ym), f"problem {i}: whole-x kernel differs from the mixed launch"
+    for (R, K), y, ref in zip(WIDE_PAIR_SHAPES, ys, refs):
+        rel_check(y, ref, what=f"planned wide pairs b{bits} g{gs} M{M} [{R},{K}]")
+    for i, (x, w) in enumerate(zip(xs, ws)):
+        alone = rq.GroupedQmv([x], [w], gs, bits, planned=True).run()[0]
+        assert bits_equal(ys[i], alone), f"problem {i}: differs from the same problem run alone"
 
 
 @pytest.mark.parametrize("xdt", [torch.float32, torch.float16])
-def test_planned_wide_whole_x_dtypes(O, rq, dev, xdt):
-    say(f"planned wide whole-x x={xdt}")
-    plan, refs, _, _ = _planned(O, rq, dev, WIDE_SHORT_SHAPES, 6, 64, 4, 5990, xdt, torch.float16)
+def test_planned_wide_pair_restaging_dtypes(O, rq, dev, xdt):
+    say(f"planned wide pair restaging x={xdt}")
+    plan, refs, _, _ = _planned(O, rq, dev, WIDE_PAIR_SHAPES, 6, 64, 4, 5990, xdt, torch.float16)
     for y, ref in zip(plan.run(), refs):
-        rel_check(y, ref, what=f"planned wide whole-x {xdt}")
+        rel_check(y, ref, what=f"planned wide pairs {xdt}")
 
 
 def test_planned_rejects_uncovered_sets(O, rq, dev):
