@@ -125,15 +125,19 @@ __global__ __launch_bounds__(64 * LoraShape<RT>::W) void lora_down_kernel(
 // v_mfma_f32_16x16x32_bf16 contracts over 32 rows: A = 16 columns of wave
 // w's 16-column slice (lane: column lr, rows 8 lg .. +7), B = 16 ranks (lane:
 // rank lr, the same rows).  Both operands want the rows contiguous per lane
-// while the tensors are row-major [M, *], so every 64-row step is written to
-// LDS transposed, [column][row], in 16-byte row chunks XOR-swizzled by
-// (c ^ c >> 3) & 7: the fragment reads (16 columns per 16 lanes) and the
-// transposing 2-byte writes (column c0 + 8 t + j from 8 lanes t) both spread
-// over all 32 banks.
+// while the tensors are row-major [M, *]: every 64-row step is written to
+// LDS as it is, row-major, with 16-byte stores, and the fragments come from
+// gfx950's transposing ds_read_b64_tr_b16 (within 16 lanes, source lane
+// 4 s + a reads 4 columns 4 a .. +3 of row s, and result lane 4 a + b
+// receives column 4 a + b of the 4 rows; two reads give a lane 8 rows).  The
+// x / dY tile's 16-byte chunks are XOR-swizzled by 2 (row % 4), so the 4 rows
+// x 2 chunks of one transposed read hit 8 different bank groups.  (The
+// earlier layout, transposed in LDS by 2-byte stores, spent the step on
+// those stores: 26.7 us per config-4 projection.)
 
 constexpr int kGradBlock = 256;
 
-RQ_DEV int tkey(int c) { return (c ^ (c >> 3)) & 7; }
+RQ_DEV int pchunk(int c, int m) { return c ^ ((m & 3) << 1); }
 
 template <int RT>  // rank / 16
 __global__ __launch_bounds__(kGradBlock) void lora_grads_kernel(
@@ -144,8 +148,8 @@ __global__ __launch_bounds__(kGradBlock) void lora_grads_kernel(
     constexpr int RANK = 16 * RT;
     constexpr int QV = RANK * 64 / 8;            // 16-byte chunks of a 64-row step of Q
     constexpr int QL = (QV + kGradBlock - 1) / kGradBlock;
-    __shared__ __attribute__((aligned(16))) uint16_t pt[2][64 * 64];    // [column][row]
-    __shared__ __attribute__((aligned(16))) uint16_t qt[2][RANK * 64];  // [rank][row]
+    __shared__ __attribute__((aligned(16))) uint16_t pt[2][64 * 64];    // [row][column], chunks swizzled
+    __shared__ __attribute__((aligned(16))) uint16_t qt[2][64 * RANK];  // [row][rank]
     __shared__ uint32_t last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lg = lane >> 4, lr = lane & 15;
@@ -186,32 +190,34 @@ __global__ __launch_bounds__(kGradBlock) void lora_grads_kernel(
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int m = prow + 32 * h;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int c = pch * 8 + j;
-                pt[b][c * 64 + (((m >> 3) ^ tkey(c)) << 3) + (m & 7)] =
-                    (uint16_t)(pv[h][j >> 1] >> (16 * (j & 1)));
-            }
+            *(u32x4_t*)(pt[b] + m * 64 + pchunk(pch, m) * 8) = pv[h];
         }
 #pragma unroll
         for (int i = 0; i < QL; ++i) {
             const int q = tid + kGradBlock * i;
-            if (QV % kGradBlock == 0 || q < QV) {
-                const int m = q / (RANK / 8), jc = q % (RANK / 8);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int r = jc * 8 + j;
-                    qt[b][r * 64 + (((m >> 3) ^ tkey(r)) << 3) + (m & 7)] =
-                        (uint16_t)(qv[i][j >> 1] >> (16 * (j & 1)));
-                }
-            }
+            if (QV % kGradBlock == 0 || q < QV) *(u32x4_t*)(qt[b] + q * 8) = qv[i];
         }
     };
 
     f32x4_t acc[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const int ca = 16 * wave + lr;  // this lane's column of the A fragments
+    // transposed-read source addresses (elements): row 8 lg + 4 v + lr / 4 of
+    // the 32-row k-step, columns 4 (lr % 4) .. +3 of the 16-wide slice
+    typedef short s16x4_t __attribute__((ext_vector_type(4)));
+    typedef short s16x8_t __attribute__((ext_vector_type(8)));
+    typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_p;
+    uint32_t aoff[2], boff[2];
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+        const int row = 8 * lg + 4 * v + (lr >> 2);
+        const int col = 16 * wave + 4 * (lr & 3);
+        aoff[v] = (uint32_t)(row * 64 + pchunk(col >> 3, row) * 8 + (col & 7));
+        boff[v] = (uint32_t)(row * RANK + 4 * (lr & 3));
+    }
+    auto tread = [&](const uint16_t* base) {
+        return (lds_s16x4_p)(base);
+    };
     if (nsteps > 0) load(0);
     for (int st = 0; st < nsteps; ++st) {
         const int b = st & 1;
@@ -222,14 +228,19 @@ __global__ __launch_bounds__(kGradBlock) void lora_grads_kernel(
         __builtin_amdgcn_s_barrier();
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const int q = 4 * ks + lg;
+            // rows 32 ks .. : the swizzle key depends on row % 4 only
+            const s16x4_t a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(tread(pt[b] + aoff[0] + ks * 32 * 64));
+            const s16x4_t a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(tread(pt[b] + aoff[1] + ks * 32 * 64));
             const bf16x8_t av = __builtin_bit_cast(
-                bf16x8_t, *(const u32x4_t*)(pt[b] + ca * 64 + ((q ^ tkey(ca)) << 3)));
+                bf16x8_t, s16x8_t{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]});
 #pragma unroll
             for (int t = 0; t < RT; ++t) {
-                const int r = 16 * t + lr;
+                const s16x4_t b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    tread(qt[b] + boff[0] + ks * 32 * RANK + 16 * t));
+                const s16x4_t b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    tread(qt[b] + boff[1] + ks * 32 * RANK + 16 * t));
                 const bf16x8_t bv = __builtin_bit_cast(
-                    bf16x8_t, *(const u32x4_t*)(qt[b] + r * 64 + ((q ^ tkey(r)) << 3)));
+                    bf16x8_t, s16x8_t{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]});
                 acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[t], 0, 0, 0);
             }
         }
@@ -270,13 +281,37 @@ __global__ __launch_bounds__(kGradBlock) void lora_grads_kernel(
                (uint32_t)(S - 1);
     __syncthreads();
     if (!last) return;
+    // the S partials of this thread's elements, summed in chunk order; the
+    // loads go out QB chunks at a time, 64 values per thread (one at a time,
+    // each waiting for the previous sum, they made the reduction a chain of S
+    // memory latencies: 27.5 vs 15.0 us per config-4 r/k/v/o launch)
     const float* tp = part + (int64_t)tile * S * (64 * RANK);
-    for (int e = tid; e < 64 * RANK; e += kGradBlock) {
-        float v = __hip_atomic_load(tp + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (int q = 1; q < S; ++q)
-            v += __hip_atomic_load(tp + (int64_t)q * (64 * RANK) + e, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        store(e / RANK, e % RANK, v);
+    constexpr int EPT = 64 * RANK / kGradBlock;  // elements per thread
+    constexpr int QB = 64 / EPT;                 // chunks per batch of loads
+    static_assert(EPT * kGradBlock == 64 * RANK, "");
+    float v[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) v[i] = 0.f;
+    for (int q0 = 0; q0 < S; q0 += QB) {
+        float t[QB][EPT];
+#pragma unroll
+        for (int j = 0; j < QB; ++j)
+#pragma unroll
+            for (int i = 0; i < EPT; ++i)
+                t[j][i] = q0 + j < S ? __hip_atomic_load(tp + (int64_t)(q0 + j) * (64 * RANK) + tid +
+                                                             kGradBlock * i,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                     : 0.f;
+#pragma unroll
+        for (int j = 0; j < QB; ++j)
+#pragma unroll
+            for (int i = 0; i < EPT; ++i)
+                if (q0 + j < S) v[i] += t[j][i];
+    }
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid + kGradBlock * i;
+        store(e / RANK, e % RANK, v[i]);
     }
     if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
