@@ -1,6 +1,6 @@
 """Benchmark of the quantized-linear hot path on one MI355X.
 
-Headline (BASELINE.json `metric`, configs[1]): the RWKV-7 1.5B decode GEMV
+Headline (the benchmark's `metric`, its configs[1]): the RWKV-7 1.5B decode GEMV
 sweep -- 24 layers x {r, k, v, o [2048,2048], FFN key [8192,2048], FFN value
 [2048,8192]} + head [65536,2048], 4-bit g64 with bf16 scales/biases, weights
 ~N(0,0.02) with a distinct seed per layer and projection (755 MB of packed
@@ -13,7 +13,7 @@ inputs resident in HBM.
 Alongside: the same sweep at M=8, one GEMV launch per projection (eagerly, and
 replayed from one HIP graph), config 1 (0.1B FFN key: quantize, dequantize,
 GEMV at M=1/16 as single calls), the prefill
-GEMM (RWKV-7 2.9B shapes, M=4096/2048/512) and its
+GEMM (benchmark config 3, RWKV-7 2.9B shapes, M=4096/2048/512) and its
 transposed product in TFLOP/s, the QLoRA dX product at config-4 shapes, the
 config-5 mixed-bit model (7.2B shapes, 3-bit layers + 8-bit head: decode
 sweep GB/s, prefill M=2048 TFLOP/s), and the CPU oracle's GEMV timed on the
@@ -316,7 +316,7 @@ def make_sweep(rq, torch, dev, M, bits=4, gs=64, timed=True):
 
 
 def config1(torch, rq, dev, args):
-    """BASELINE config 1 (RWKV-7 0.1B FFN key, W [3072, 768], 4-bit g64): the
+    """benchmark config 1 (RWKV-7 0.1B FFN key, W [3072, 768], 4-bit g64): the
     quantize -> dequantize round trip and y = x . W^T at M = 1 and 16, each
     timed as back-to-back single calls (launch-latency-bound at this size:
     1.3 MB of packed weights)."""
@@ -366,7 +366,7 @@ def config5_sweep(torch, rq, dev):
 
 
 def config5(torch, rq, dev, args):
-    """RWKV-7 7.2B shapes (D=4096, FFN 16384, vocab 65536),
+    """benchmark config 5: RWKV-7 7.2B shapes (D=4096, FFN 16384, vocab 65536),
     3-bit g64 r/k/v/o and FFN, 8-bit g64 head, bf16 scales/biases.  Decode:
     all 32 layers' 3-bit projections in one planned launch plus the 8-bit
     head in a second, M=1, GB/s of packed weights + scales/biases.  Prefill:
@@ -445,7 +445,7 @@ def qlora_step_workload(torch, rq, dev):
 
 
 def qlora_step(torch, rq, dev, ws, args):
-    """one QLoRA training step of one RWKV-7 1.5B layer
+    """benchmark config 4: one QLoRA training step of one RWKV-7 1.5B layer
     (D=2048) on a frozen 4-bit g64 base -- for each of r, k, v, o, ffn_key,
     ffn_value: y = qmm(x, Wq) + (alpha/r) (x A^T) B^T, r = alpha = 16,
     A ~ N(0, 1/D), B ~ N(0, 0.01) (std), x [8, 512, K] bf16, then dX, dA, dB

@@ -115,7 +115,7 @@ def test_quantize_bit_exact(O, rq, dev, bits, gs, dtype):
 
 
 def test_quantize_config1_shape(O, rq, dev):
-    """RWKV-7 0.1B FFN key [3072, 768], 4-bit g64."""
+    """benchmark config 1: RWKV-7 0.1B FFN key [3072, 768], 4-bit g64."""
     w = weights(3072, 768, 1_000_000 + 4)
     say("quantize config1 [3072,768]")
     wq, s, b = rq.quantize(w.to(dev), 64, 4)
@@ -466,7 +466,7 @@ def test_qmm_t_other_dtypes(O, rq, dev, xdt):
     rel_check(y, ref, what="qmm_t dtypes")
 
 
-# ---------------------------------------------------- BASELINE configs
+# ---------------------------------------------------- benchmark configs
 
 @pytest.mark.parametrize("M", [1, 16])
 def test_config1_roundtrip_and_matmul(O, rq, dev, M):
@@ -855,7 +855,7 @@ def test_autograd_dx_is_transposed_qmm(O, rq, dev):
 
 @pytest.mark.parametrize("M", [96, 320])
 def test_qlora_layer_forward_backward(rq, dev, M):
-    """BASELINE config 4 math at a reduced shape: y = qmm(x,Wq) + (a/r)(xA^T)B^T;
+    """benchmark config 4 math at a reduced shape: y = qmm(x,Wq) + (a/r)(xA^T)B^T;
     grads of x, A, B against an fp32 dense reference on the dequantized base.
     M=320 runs the fused low-rank term (forward and dX GEMMs), M=96 the
     composed ops."""

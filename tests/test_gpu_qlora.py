@@ -1,7 +1,7 @@
 """GPU parity of the QLoRA layer's kernels (rwkv_metal/lora/lora.py:58-63 under
 nn.value_and_grad, rwkv_metal/lora/finetune.py:141): the adapter-gradient
 launch rq_lora_grads against fp32 products of the same bf16 operands, and the
-whole layer step at BASELINE config 4's full size against an fp32 dense
+whole layer step at benchmark config 4's full size against an fp32 dense
 reference on the dequantized base."""
 import pytest
 import torch
@@ -140,7 +140,7 @@ def test_qlora_one_launch_declines_other_ranks_and_bits(rq, dev):
 
 
 def test_config4_qlora_layer_step_full_size(rq, dev):
-    """BASELINE config 4 at full size: one RWKV-7 1.5B layer (D = 2048) on a
+    """benchmark config 4 at full size: one RWKV-7 1.5B layer (D = 2048) on a
     frozen 4-bit g64 base, 8 x 512 tokens, r = alpha = 16, A ~ N(0, 1/D),
     B ~ N(0, 0.01) (std); for each of r, k, v, o, ffn_key and ffn_value the
     forward y = qmm(x, Wq) + (alpha / r) (x A^T) B^T and the gradients dX, dA,

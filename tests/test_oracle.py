@@ -407,7 +407,7 @@ def _numpy_quantize_ties(w, gs, bits):
 
 def test_tie_count_pinned_by_numpy_config1(O):
     """rqo_count_ties against an independent numpy float32 statement of the
-    quantizer on BASELINE config 1 (RWKV-7 0.1B FFN key [3072, 768], 4-bit
+    quantizer on benchmark config 1 (RWKV-7 0.1B FFN key [3072, 768], 4-bit
     g64), whose codes must also equal the oracle's bit for bit."""
     g = torch.Generator().manual_seed(1_000_004)
     w = (torch.randn(3072, 768, generator=g) * 0.02).to(torch.bfloat16)
