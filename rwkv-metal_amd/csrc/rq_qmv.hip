@@ -1492,15 +1492,15 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
 //      takes ~116 VGPRs with one wait per stage for exactly its codes, and
 //      (scale, bias) windows of 16 groups (32 at gs 32: one iteration) keep
 //      the block at 40.2 KB of LDS: 4 waves per SIMD.
-//    - m > 8 (MP = 16): K <= 2048 is staged whole up front; longer rows stream chunks,
-//      the next chunk's loads issued at the start of an iteration and
-//      written after its MFMAs, behind one barrier per iteration.  Both
-//      loops live in one kernel.  At MP = 8 that form took 167 VGPRs (3 waves
-//      per SIMD), and the compiler's wait analysis, merged over both loops,
-//      made the whole-x loop wait for code loads of later stages
-//      (vmcnt(2)/vmcnt(4) where vmcnt(6) suffices, vmcnt(1) at each window);
-//      the pair schedule measured +3 % on the config-2 sweep at M = 8 (+5 %
-//      on its K = 2048 projections, equal on K = 8192).
+//    - m > 8 (MP = 16): K <= 2048 is staged whole up front; longer rows
+//      stream chunks, the next chunk's loads issued at the start of an
+//      iteration and written after its MFMAs, behind one barrier per
+//      iteration.  Both loops live in one kernel.  At MP = 8 that form took
+//      167 VGPRs (3 waves per SIMD), and the compiler's wait analysis,
+//      merged over both loops, made the whole-x loop wait for code loads of
+//      later stages (vmcnt(2)/vmcnt(4) where vmcnt(6) suffices, vmcnt(1) at
+//      each window); the pair schedule measured +3 % on the config-2 sweep
+//      at M = 8 (+5 % on its K = 2048 projections, equal on K = 8192).
 // 4- and 8-bit codes: their pieces are whole words.
 constexpr int kWideNS = 4;                // stages per iteration = per staged x chunk
 constexpr int kWideKC = 256 * kWideNS;    // x columns per chunk
@@ -1559,8 +1559,8 @@ struct WideLds {
     static constexpr int X_ELEMS = DUMMY + 8;
 };
 
-// XP: x staged by pairs of chunks (restaged behind barriers); otherwise
-// whole when K <= 2048 and streamed chunk by chunk beyond.
+// x schedule: at MP = 8 by pairs of chunks (restaged behind barriers); at
+// MP = 16 whole when K <= 2048 and streamed chunk by chunk beyond.
 template <int BITS, int SDT, int MP, int GSH, bool XF32>
 RQ_DEV void qmv_wide_body(const rq_problem& P, int lblock, int M, int x_dt, int y_dt) {
     static_assert(BITS == 4 || BITS == 8, "wide GEMV: codes whose 8-code pieces are whole words");
