@@ -828,6 +828,9 @@ def main():
         del graph
         extra["decode_m1_dependency_levels"] = dependency_levels(torch, rwkvq, xs, ws, outs,
                                                                  total_wbytes, args)
+        # the same order for a batch of 8 sequences
+        extra["decode_m8_dependency_levels"] = dependency_levels(torch, rwkvq, xs8, ws, outs8,
+                                                                 total_wbytes, args)
         extra["decode_per_shape_rotating_512mb"] = decode_per_shape(torch, rwkvq, dev, args)
         # prefill GEMM, config 3 (RWKV-7 2.9B shapes) at M = 4096 (aggregate) and
         # 2048 / 512; the transposed product (QLoRA dX) at M = 4096

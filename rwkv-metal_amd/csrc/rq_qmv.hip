@@ -1947,7 +1947,13 @@ constexpr int split_max_nsw(int pc) {
 }
 inline int split_pass_code(int64_t m) { return m > 4 ? 20 : (m >= 3 ? 12 : 8 + (int)m); }
 
-bool split_covers(const rq_problem& p, int sb_dt, int64_t m, int gs) {
+// LDS a split-GEMV block may take when the launch has at most one block per
+// CU (then nothing shares the CU's 160 KB): [2048, 8192] at m = 8 stages 8
+// rows x 512 columns of x per wave, 16 waves, ~145 KB.
+constexpr int kSplitLdsOneBlock = 152 * 1024;
+constexpr int64_t kSplitOneBlockMax = 256;  // blocks of a launch that fit one per CU
+
+bool split_covers(const rq_problem& p, int sb_dt, int64_t m, int gs, int budget) {
     if (sb_dt == RQ_F32 || m < 1 || m > 8 || p.cols % 256 != 0 || p.rows < 1) return false;
     const int nsw = split_nsw(p.cols);
     if (nsw == 0 || nsw > split_max_nsw(split_pass_code(m))) return false;
@@ -1960,7 +1966,7 @@ bool split_covers(const rq_problem& p, int sb_dt, int64_t m, int gs) {
     const uintptr_t code_align = (RQ_BITS & 1) ? 7 : 15;
     return row_bytes % sbw == 0 && (((uintptr_t)p.scales | (uintptr_t)p.biases) % sbw) == 0 &&
            ((uintptr_t)p.w_q & code_align) == 0 && ((uintptr_t)p.x & 15) == 0 &&
-           (int64_t)ks * split_wave_bytes((int)m, nsw, gsh, RQ_BITS) <= kLdsBudget;
+           (int64_t)ks * split_wave_bytes((int)m, nsw, gsh, RQ_BITS) <= budget;
 }
 
 hipError_t launch_split(const QmvArgs& a, int blocks, int64_t cols, int sb_dt, int gs,
@@ -2063,7 +2069,8 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
     const int cfg = rowblocks >= RQ_QMV_BIG_MIN ? 2 : (rowblocks >= 2048 ? 1 : 0);
     // Small launches: the split GEMV (one memory round trip per launch).
     bool split = cfg == 0 && RQ_QMV_SPLIT;
-    for (int i = 0; i < n && split; ++i) split = split_covers(*probs[i], sb_dt, m, gs);
+    const int split_budget = rowblocks <= kSplitOneBlockMax ? kSplitLdsOneBlock : kLdsBudget;
+    for (int i = 0; i < n && split; ++i) split = split_covers(*probs[i], sb_dt, m, gs, split_budget);
     if (split) {
         for (int base = 0; base < n; base += RQ_MAX_GROUPED) {
             const int cnt = (n - base) < RQ_MAX_GROUPED ? (n - base) : RQ_MAX_GROUPED;

@@ -307,6 +307,22 @@ def test_split_gemv_short_slices(O, rq, dev, bits, gs, M, xdt, sdt):
         rel_check(y, ref, what=f"split b{bits} g{gs} M{M} {R}x{K}")
 
 
+@pytest.mark.parametrize("M", [5, 8])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_split_gemv_whole_cu_lds(O, rq, dev, bits, M):
+    """Launches of at most one block per CU may stage up to 152 KB of x per
+    block: [2048, 8192] at m = 8 runs 16 waves of 2-stage slices (4-bit
+    codes; 8-bit codes at m > 4 take one stage per wave and fall back)."""
+    for R, K in [(2048, 8192), (130, 4352), (256, 7936)]:
+        w = weights(R, K, 70_000 + bits + K)
+        wq, s, b = O.quantize(w, 64, bits)
+        x = acts(M, K, 70_100 + M + K)
+        say(f"split gemv whole-CU LDS bits={bits} M={M} R={R} K={K}")
+        y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, bits)
+        ref = O.quantized_matmul(x, wq, s, b, True, 64, bits, out_dtype=torch.float32, weights="exact")
+        rel_check(y, ref, what=f"split whole-CU b{bits} M{M} {R}x{K}")
+
+
 def test_split_gemv_dependency_level(O, rq, dev):
     """One decode dependency level as one grouped launch (the r, k, v
     projections of a layer: three problems, three activations) and the
