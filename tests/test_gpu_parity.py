@@ -323,6 +323,33 @@ def test_split_gemv_whole_cu_lds(O, rq, dev, bits, M):
         rel_check(y, ref, what=f"split whole-CU b{bits} M{M} {R}x{K}")
 
 
+def test_split_gemv_whole_cu_boundary(O, rq, dev):
+    """84 KB of staged x per block at m = 8 (K = 4352: 9 waves of 2-stage
+    slices): 4096 rows (256 blocks) take the split GEMV with its larger LDS
+    budget, 4112 rows (257 blocks) another kernel; a grouped launch of three
+    problems with 255 blocks in all takes the split GEMV.  Every output row
+    against the oracle, and the grouped launch bit-equal to single calls."""
+    K = 4352
+    for R in (4096, 4112):
+        wq, s, b = O.quantize(weights(R, K, 71_000 + R), 64, 4)
+        x = acts(8, K, 71_100 + R)
+        say(f"split gemv whole-CU boundary R={R} K={K} M=8")
+        y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
+        ref = O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32, weights="exact")
+        rel_check(y, ref, what=f"whole-CU boundary {R}x{K}")
+    probs = []
+    for i, R in enumerate((1360, 1360, 1352)):
+        wq, s, b = O.quantize(weights(R, K, 71_200 + i), 64, 4)
+        probs.append((acts(8, K, 71_300 + i).to(dev), (wq.to(dev), s.to(dev), b.to(dev))))
+    say("split gemv whole-CU boundary: grouped launch of 255 blocks")
+    ys = rq.grouped_qmv([x for x, _ in probs], [w for _, w in probs], 64, 4)
+    for (x, (wq, s, b)), y in zip(probs, ys):
+        ref = O.quantized_matmul(x.cpu(), wq.cpu(), s.cpu(), b.cpu(), True, 64, 4,
+                                 out_dtype=torch.float32, weights="exact")
+        rel_check(y, ref, what="whole-CU boundary grouped")
+        assert bits_equal(y, rq.quantized_matmul(x, wq, s, b, True, 64, 4))
+
+
 def test_split_gemv_dependency_level(O, rq, dev):
     """One decode dependency level as one grouped launch (the r, k, v
     projections of a layer: three problems, three activations) and the
