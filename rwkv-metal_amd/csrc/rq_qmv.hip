@@ -115,6 +115,7 @@ struct QmvArgs {
     int y_dt;
     int sb_vec;  // scales and biases are 16-byte aligned (vector staging allowed)
     int xsplit;  // m counts the hi and lo bf16 rows of m/2 activation rows (qmv_xsplit)
+    int fold;    // qmv_split: rows 2r, 2r + 1 are the halves of weight row r (split_fold)
 };
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -1439,6 +1440,24 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
         }
     }
     const int64_t row = row0 + lr;
+    if (args.fold) {
+        // rows 2r + p are the halves p of weight row r and activation rows
+        // 2m + p the matching halves of x row m: lane (lg, lr) with lg and lr
+        // even holds half 0 of output (m, r), lane + 17 half 1
+        const int64_t rr = row >> 1;
+#pragma unroll
+        for (int c = 0; c < NMC; ++c) {
+            float mine = 0.f;
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+                if (i == lg) mine = v[c][i];
+            const float other = __shfl(mine, (lane + 17) & 63, 64);
+            const int m = 2 * c + (lg >> 1);
+            if (((lg | lr) & 1) == 0 && lg < MI && 2 * m < M && rr < (R >> 1))
+                store_dt(P.y, args.y_dt, (int64_t)m * (R >> 1) + rr, mine + other);
+        }
+        return;
+    }
     if (args.xsplit) {
         // M = 2 or 4 rows in one pass, row i in lane group i: output row i is
         // hi row i plus lo row i + M/2, which lane group i + M/2 holds
@@ -1947,6 +1966,24 @@ constexpr int split_max_nsw(int pc) {
 }
 inline int split_pass_code(int64_t m) { return m > 4 ? 20 : (m >= 3 ? 12 : 8 + (int)m); }
 
+// Folding a small launch (m <= 2): W [R, K] read as [2R, K/2] -- the same bytes, row
+// r's halves are rows 2r and 2r + 1, and so are its (scale, bias) values --
+// against x read as [2m, K/2] (x row m's halves are rows 2m, 2m + 1).  Output
+// (2m + p, 2r + q) is half p of x row m against half q of weight row r; the
+// kernel stores half 0 + half 1 of the p == q ones (QmvArgs::fold).  Twice
+// the 16-row tiles, each over half the stages: for launches that leave most
+// CUs idle ([2048, 8192]: 128 tiles of 32 stages become 256 of 16).
+#ifndef RQ_QMV_FOLD
+#define RQ_QMV_FOLD 1
+#endif
+constexpr int64_t kFoldMaxBlocks = 128;  // tiles of a launch that folds, at most
+
+inline rq_problem split_fold(rq_problem p) {
+    p.rows *= 2;
+    p.cols /= 2;
+    return p;
+}
+
 // LDS a split-GEMV block may take when the launch has at most one block per
 // CU (then nothing shares the CU's 160 KB): [2048, 8192] at m = 8 stages 8
 // rows x 512 columns of x per wave, 16 waves, ~145 KB.
@@ -2069,8 +2106,19 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
     const int cfg = rowblocks >= RQ_QMV_BIG_MIN ? 2 : (rowblocks >= 2048 ? 1 : 0);
     // Small launches: the split GEMV (one memory round trip per launch).
     bool split = cfg == 0 && RQ_QMV_SPLIT;
+    // Launches of at most kFoldMaxBlocks tiles fold (split_fold): twice the
+    // tiles, each over half of K.  Measured per launch: faster at m = 1 (e.g.
+    // [2048, 8192] 7.04 -> 5.77 us, [2048, 2048] 4.44 -> 4.19) and at m = 2
+    // with K >= 4096; at m = 2, K = 2048 and at m >= 3 (two passes of 8
+    // activation rows at m = 4) slower.
+    bool fold = split && RQ_QMV_FOLD && !xsplit && (m == 1 || (m == 2 && K >= 4096)) &&
+                K % 512 == 0 && rowblocks <= kFoldMaxBlocks;
+    for (int i = 0; i < n && fold; ++i)
+        fold = split_covers(split_fold(*probs[i]), sb_dt, 2 * m, gs,
+                            2 * rowblocks <= kSplitOneBlockMax ? kSplitLdsOneBlock : kLdsBudget);
     const int split_budget = rowblocks <= kSplitOneBlockMax ? kSplitLdsOneBlock : kLdsBudget;
-    for (int i = 0; i < n && split; ++i) split = split_covers(*probs[i], sb_dt, m, gs, split_budget);
+    for (int i = 0; i < n && split && !fold; ++i)
+        split = split_covers(*probs[i], sb_dt, m, gs, split_budget);
     if (split) {
         for (int base = 0; base < n; base += RQ_MAX_GROUPED) {
             const int cnt = (n - base) < RQ_MAX_GROUPED ? (n - base) : RQ_MAX_GROUPED;
@@ -2078,18 +2126,19 @@ static hipError_t launch_bucket(const rq_problem* const* probs, int n, int x_dt,
             std::memset(&a, 0, sizeof(a));
             int64_t blocks = 0;
             for (int i = 0; i < cnt; ++i) {
-                a.p[i] = *probs[base + i];
+                a.p[i] = fold ? split_fold(*probs[base + i]) : *probs[base + i];
                 a.block_start[i] = (int)blocks;
-                blocks += (probs[base + i]->rows + 15) / 16;
+                blocks += (a.p[i].rows + 15) / 16;
             }
             a.block_start[cnt] = (int)blocks;
             a.n = cnt;
-            a.m = (int)m;
+            a.m = (int)(fold ? 2 * m : m);
             a.gs_shift = gs_shift;
             a.x_dt = x_dt;
             a.y_dt = y_dt;
             a.xsplit = xsplit;
-            hipError_t e = launch_split(a, (int)blocks, K, sb_dt, gs, stream);
+            a.fold = fold ? 1 : 0;
+            hipError_t e = launch_split(a, (int)blocks, fold ? K / 2 : K, sb_dt, gs, stream);
             if (e != hipSuccess) return e;
         }
         return hipSuccess;

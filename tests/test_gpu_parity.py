@@ -323,6 +323,44 @@ def test_split_gemv_whole_cu_lds(O, rq, dev, bits, M):
         rel_check(y, ref, what=f"split whole-CU b{bits} M{M} {R}x{K}")
 
 
+# Launches of at most 128 16-row tiles with K % 512 == 0 and bf16 x fold at
+# m = 1, and at m = 2 when K >= 4096: W [R, K] runs as [2R, K/2] against x as
+# [2m, K/2] and the store adds each output's two halves (m = 3, 4 and the
+# shorter rows at m = 2 take the unfolded split GEMV on the same shapes).
+FOLD_SHAPES = [(2048, 8192), (2048, 2048), (100, 4096), (37, 1024), (130, 512), (16, 16384)]
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_split_gemv_fold(O, rq, dev, bits, gs, M):
+    for R, K in FOLD_SHAPES:
+        w = weights(R, K, 72_000 + 11 * bits + gs + K)
+        wq, s, b = O.quantize(w, gs, bits)
+        x = acts(M, K, 72_100 + 3 * M + K)
+        say(f"split gemv fold bits={bits} gs={gs} M={M} R={R} K={K}")
+        y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, gs, bits)
+        ref = O.quantized_matmul(x, wq, s, b, True, gs, bits, out_dtype=torch.float32, weights="exact")
+        rel_check(y, ref, what=f"fold b{bits} g{gs} M{M} {R}x{K}")
+
+
+def test_split_gemv_fold_grouped(O, rq, dev):
+    """A folded grouped launch (two [512, 4096] problems and a [384, 4096]
+    one, 88 tiles in all) against the oracle and bit-equal to single calls."""
+    probs = []
+    for i, R in enumerate((512, 512, 384)):
+        wq, s, b = O.quantize(weights(R, 4096, 72_200 + i), 64, 4)
+        probs.append((acts(2, 4096, 72_300 + i).to(dev), (wq.to(dev), s.to(dev), b.to(dev))))
+    say("split gemv fold: grouped launch of 88 tiles")
+    ys = rq.grouped_qmv([x for x, _ in probs], [w for _, w in probs], 64, 4)
+    for (x, (wq, s, b)), y in zip(probs, ys):
+        ref = O.quantized_matmul(x.cpu(), wq.cpu(), s.cpu(), b.cpu(), True, 64, 4,
+                                 out_dtype=torch.float32, weights="exact")
+        rel_check(y, ref, what="fold grouped")
+        y1 = rq.grouped_qmv([x], [(wq, s, b)], 64, 4)[0]
+        assert bits_equal(y, y1)
+
+
 def test_split_gemv_whole_cu_boundary(O, rq, dev):
     """84 KB of staged x per block at m = 8 (K = 4352: 9 waves of 2-stage
     slices): 4096 rows (256 blocks) take the split GEMV with its larger LDS
