@@ -328,6 +328,19 @@ def config1(torch, rq, dev, args):
     n = max(20, args.steps)
     out["quantize_us"] = round(time_region(torch, lambda: rq.quantize(w, gs, bits), n, 10) * 1e6, 2)
     out["dequantize_us"] = round(time_region(torch, lambda: rq.dequantize(wq, s, b, gs, bits), n, 10) * 1e6, 2)
+    # the same calls replayed from a HIP graph: the GPU side without the
+    # Python op dispatch that bounds the single calls above
+    for name, fn in (("quantize", lambda: rq.quantize(w, gs, bits)),
+                     ("dequantize", lambda: rq.dequantize(wq, s, b, gs, bits))):
+        reps = 20
+        fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        out[f"{name}_hip_graph_us"] = round(time_region(torch, graph.replay, 10, 3) / reps * 1e6, 2)
+        del graph
     for M in (1, 16):
         x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
         bq = rq.BoundQmm(x, wq, s, b, True, gs, bits)
