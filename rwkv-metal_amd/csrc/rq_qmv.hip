@@ -1175,10 +1175,18 @@ __host__ __device__ inline int split_nsw(int64_t cols) {
         if (nst <= (int64_t)nsw * kSplitMaxWaves) return nsw;
     return 0;
 }
+// Arrays of activation sums staged in LDS: two for 3-bit codes (all and
+// low-half positions), one for m <= 2; 4- and 8-bit codes at m >= 3 take the
+// sums from a constant-B MFMA on the same A fragments instead (measured per
+// launch: [2048, 8192] at m = 8 13.71 -> 12.10 us, [2048, 2048] 7.30 ->
+// 6.61; at m <= 2 the extra MFMAs cost more than the few staged sums).
+__host__ __device__ constexpr int split_nsum(int bits, int m) {
+    return bits == 3 ? 2 : (m <= 2 ? 1 : 0);
+}
 __host__ __device__ inline int split_wave_bytes(int m, int nsw, int gsh, int bits) {
     const int xsh = gsh < 6 ? gsh : 6;
     const int sbb = nsw * ((256 >> gsh) * 2);
-    return 128 + m * nsw * 512 + (bits == 3 ? 2 : 1) * m * ((nsw * 256) >> xsh) * 4 +
+    return 128 + m * nsw * 512 + split_nsum(bits, m) * m * ((nsw * 256) >> xsh) * 4 +
            16 * (2 * sbb + 16);
 }
 
@@ -1187,7 +1195,10 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
     static_assert(SDT != RQ_F32, "split GEMV scales are 16-bit");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
     constexpr int XSH = GSH < 6 ? GSH : 6;
-    constexpr int NSUM = BITS == 3 ? 2 : 1;
+    // activation sums from a constant-B MFMA (m >= 3: the passes of codes 12
+    // and 20), else staged in LDS
+    constexpr bool XMF = BITS != 3 && !(NMC == 1 && MI <= 2);
+    constexpr int NSUM = split_nsum(BITS, NMC == 1 && MI <= 2 ? MI : 4);
     constexpr int KW = NSW * 256;                 // codes per row in a wave's slice
     constexpr int SBB = NSW * SplitSB<GSH>::SB1;  // bytes per row and array in a slice
     constexpr int SBH = SBB / 2;                  // bytes of it one lane loads
@@ -1217,7 +1228,7 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
     const int64_t rowc = (row0 + lr) < R ? (row0 + lr) : R - 1;
     const int64_t wpr = (K >> 5) * BITS;
 
-    // wave-private LDS: zero line | x slice [M][KW] | sums | (scale, bias) rows
+    // wave-private LDS: zero line | x slice [M][KW] | sums (NSUM arrays) | (scale, bias) rows
     const int wbytes = split_wave_bytes(M, NSW, GSH, BITS);
     uint8_t* wl = lds8 + wave * wbytes;
     uint16_t* xs = (uint16_t*)(wl + 128);
@@ -1281,23 +1292,25 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
             uint32_t pr[4];
             reorder_pairs(d, pr);
             *(u32x4_t*)&xs[m * KW + kk] = u32x4_t{pr[0], pr[1], pr[2], pr[3]};
-            float sum = 0.f, lo4 = 0.f;
+            if constexpr (!XMF) {
+                float sum = 0.f, lo4 = 0.f;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float v = __uint_as_float(d[q] << 16) + __uint_as_float(d[q] & 0xffff0000u);
-                sum += v;
-                if (q < 2) lo4 += v;
-            }
-            // a sum covers 2^(XSH-3) consecutive pieces = consecutive lanes
+                for (int q = 0; q < 4; ++q) {
+                    const float v = __uint_as_float(d[q] << 16) + __uint_as_float(d[q] & 0xffff0000u);
+                    sum += v;
+                    if (q < 2) lo4 += v;
+                }
+                // a sum covers 2^(XSH-3) consecutive pieces = consecutive lanes
 #pragma unroll
-            for (int w = 1; w < (1 << (XSH - 3)); w <<= 1) {
-                sum += __shfl_xor(sum, w, 64);
-                if constexpr (BITS == 3) lo4 += __shfl_xor(lo4, w, 64);
-            }
-            if ((e & ((1 << (XSH - 3)) - 1)) == 0) {
-                const int si = m * gxw + (kk >> XSH);
-                xsum[si] = sum;
-                if constexpr (BITS == 3) xlo[si] = lo4;
+                for (int w = 1; w < (1 << (XSH - 3)); w <<= 1) {
+                    sum += __shfl_xor(sum, w, 64);
+                    if constexpr (BITS == 3) lo4 += __shfl_xor(lo4, w, 64);
+                }
+                if ((e & ((1 << (XSH - 3)) - 1)) == 0) {
+                    const int si = m * gxw + (kk >> XSH);
+                    xsum[si] = sum;
+                    if constexpr (BITS == 3) xlo[si] = lo4;
+                }
             }
         }
     }
@@ -1346,6 +1359,10 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
     f32x4_t acc[NMC];
 #pragma unroll
     for (int c = 0; c < NMC; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // XMF: the activation sums of a lane group's codes are the same A
+    // fragments against bf16 1.0 (D rows as the product's: slot lg, row m)
+    constexpr uint32_t kOne = 0x3F803F80u;
+    const bf16x8_t ones = as_bf16x8(kOne, kOne, kOne, kOne);
     const uint16_t* wl16 = (const uint16_t*)wl;
     const float* wlf = (const float*)wl;
 #pragma unroll
@@ -1360,7 +1377,7 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
                 cb[q] = (BITS == 8) ? bi : fmaf(sc[q], -128.f, bi);
                 cl[q] = 120.f * sc[q];
             }
-            f32x4_t d[NMC][2];
+            f32x4_t d[NMC][2], xm[NMC][GL];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 bf16x8_t bop[4];
@@ -1375,12 +1392,17 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
                 for (int c = 0; c < NMC; ++c) {
                     const u32x4_t* src =
                         (const u32x4_t*)&wl16[a_base[c] + (uint32_t)t * a_step[c] + h * 32];
+                    constexpr int hx = GL == 2 ? 1 : 0;  // sums per run (gs 32) or per stage
                     d[c][h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                    if (XMF && (GL == 2 || h == 0)) xm[c][h & hx] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const u32x4_t v = src[j];
-                        d[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            as_bf16x8(v[0], v[1], v[2], v[3]), bop[j], d[c][h], 0, 0, 0);
+                        const bf16x8_t a = as_bf16x8(v[0], v[1], v[2], v[3]);
+                        d[c][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bop[j], d[c][h], 0, 0, 0);
+                        if constexpr (XMF)
+                            xm[c][h & hx] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                a, ones, xm[c][h & hx], 0, 0, 0);
                     }
                 }
             }
@@ -1388,6 +1410,16 @@ __global__ __launch_bounds__(kSplitBlock) void qmv_split(const QmvArgs args) {
             for (int c = 0; c < NMC; ++c)
 #pragma unroll
                 for (int i = 0; i < MI; ++i) {
+                    if constexpr (XMF) {
+                        if constexpr (GL == 2) {
+                            acc[c][i] = fmaf(sc[0], d[c][0][i], fmaf(cb[0], xm[c][0][i], acc[c][i]));
+                            acc[c][i] = fmaf(sc[1], d[c][1][i], fmaf(cb[1], xm[c][GL - 1][i], acc[c][i]));
+                        } else {
+                            acc[c][i] = fmaf(sc[0], d[c][0][i] + d[c][1][i],
+                                             fmaf(cb[0], xm[c][0][i], acc[c][i]));
+                        }
+                        continue;
+                    }
                     const float* xg = wlf + g_idx[c][i] + (uint32_t)t * g_step[c][i];
                     if constexpr (BITS == 3) {
                         const float* xl = xg + M * gxw;
