@@ -197,7 +197,12 @@ int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* s
  * offsets, then the partial tiles.  The workspace must be zero-filled before
  * its first use; every call leaves the counters at zero, so one workspace
  * serves any later problem that fits it.  Calls that run at the same time
- * need separate workspaces.  k/64 + n/64 is at most 16384. */
+ * need separate workspaces.  k/64 + n/64 is at most 16384.
+ * rq_lora_grads_workspace_bytes returns a byte count (>= 0) or, for sizes
+ * rq_lora_grads would reject, a negative rq error code (RQ_EINVAL) with
+ * rq_last_error() set; check the sign before passing it to hipMalloc:
+ *     int64_t nb = rq_lora_grads_workspace_bytes(m, k, n, rank, 1, 1);
+ *     if (nb < 0) { fprintf(stderr, "%s\n", rq_last_error()); return nb; } */
 int64_t rq_lora_grads_workspace_bytes(int64_t m, int64_t k, int64_t n, int64_t rank, int has_da,
                                       int has_db);
 int rq_lora_grads(const void* x, const void* u, const void* dy, const void* z, int64_t m,
@@ -209,9 +214,11 @@ int rq_lora_grads(const void* x, const void* u, const void* dy, const void* z, i
  * harnesses that forbid hipMalloc).  It has no counterpart in the reference.
  * Same arguments, results (bit for bit) and kernels; the counters and
  * partial tiles live in a static device buffer of 8 MiB + 64 KiB per GPU,
- * held until the process ends, whose address is looked up (and its counters
- * cleared on `stream`) at the first call on each device, with the device of
- * `stream` current.  The call allocates nothing.  Problems whose partial
+ * held until the process ends, whose address is looked up at the first call
+ * on each device, with the device of `stream` current.  Its counters are
+ * cleared by a fill kernel on `stream` at the first call that is not being
+ * captured into a graph (a call under capture puts the clear into the graph
+ * ahead of its own launch until then).  The call allocates nothing.  Problems whose partial
  * tiles would not fit are rejected with RQ_EINVAL (the row split is capped
  * at 8 MiB, so that is k/64 + n/64 > 16384).  Every call on a GPU shares that
  * GPU's buffer: calls that overlap in time on one GPU (other streams, other

@@ -330,6 +330,7 @@ static __device__ __align__(256) uint8_t scratch[rq::kLoraScratchBytes];
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+bool g_scratch_zeroed[kMaxDevices] = {};
 
 }  // namespace
 
@@ -345,14 +346,23 @@ hipError_t lora_scratch(void** out, hipStream_t stream) {
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = p;
+    }
+    if (!g_scratch_zeroed[dev]) {
         // the counters must start at zero (each launch leaves them so); a fill
-        // kernel rather than a memset node, so the stream may be capturing
+        // kernel rather than a memset node, so the stream may be capturing.
+        // Launched into a graph being captured it runs only when the graph is
+        // replayed (before that graph's own gradient launch), so the device
+        // counts as cleared only after an eager clear.
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &cap);
+        if (e != hipSuccess) return e;
         const int words = (int)(kLoraGradCounterBytes / 4);
         hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, stream,
-                           (uint32_t*)p, words);
+                           (uint32_t*)g_scratch_ptr[dev], words);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
-        g_scratch_ptr[dev] = p;
+        if (cap == hipStreamCaptureStatusNone) g_scratch_zeroed[dev] = true;
     }
     *out = g_scratch_ptr[dev];
     return hipSuccess;

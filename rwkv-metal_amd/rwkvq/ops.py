@@ -23,6 +23,7 @@ ROCm GPU; there is no CPU path.
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 from typing import List, Sequence, Tuple
 
@@ -345,18 +346,24 @@ def lora_down(x: Tensor, a: Tensor) -> Tensor:
     return z.reshape(*x.shape[:-1], rank)
 
 
-_grad_workspaces: dict = {}
+_grad_workspaces: "collections.OrderedDict" = collections.OrderedDict()
+_GRAD_WORKSPACES_MAX = 8
 
 
 def _lora_workspace(device: torch.device, stream: int, nbytes: int) -> Tensor:
     """A zero-filled workspace for rq_lora_grads, one per (device, stream):
     every call leaves it zeroed for the next, and calls on one stream run in
-    order, so they can share it."""
+    order, so they can share it.  At most _GRAD_WORKSPACES_MAX are kept, least
+    recently used first out.  Each is allocated while its stream is current,
+    so torch's caching allocator hands a dropped one only to later
+    allocations on that same stream, after the work queued there."""
     key = (device.index, stream)
-    ws = _grad_workspaces.get(key)
+    ws = _grad_workspaces.pop(key, None)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
-        _grad_workspaces[key] = ws
+    _grad_workspaces[key] = ws
+    while len(_grad_workspaces) > _GRAD_WORKSPACES_MAX:
+        _grad_workspaces.popitem(last=False)
     return ws
 
 

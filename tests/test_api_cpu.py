@@ -5,37 +5,7 @@ import pytest
 import torch
 from torch import nn
 
-
-class TMix(nn.Module):
-    def __init__(self, d):
-        super().__init__()
-        self.r_proj, self.k_proj = nn.Linear(d, d, bias=False), nn.Linear(d, d, bias=False)
-        self.v_proj, self.o_proj = nn.Linear(d, d, bias=False), nn.Linear(d, d, bias=False)
-        self.w_lora = nn.Linear(d, 32, bias=False)   # low-rank branch, never quantized
-
-
-class CMix(nn.Module):
-    def __init__(self, d):
-        super().__init__()
-        self.key, self.value = nn.Linear(d, 4 * d, bias=False), nn.Linear(4 * d, d, bias=False)
-
-
-class Block(nn.Module):
-    def __init__(self, d):
-        super().__init__()
-        self.tmix, self.cmix = TMix(d), CMix(d)
-
-
-class Tiny(nn.Module):
-    """The reference model's module layout (rwkv_metal/model/rwkv7_x070.py)."""
-
-    def __init__(self, d=128, n=3, vocab=256, device="meta"):
-        super().__init__()
-        with torch.device(device):
-            self.emb = nn.Embedding(vocab, d)
-            self.blocks = nn.ModuleList([Block(d) for _ in range(n)])
-            self.head = nn.Linear(d, vocab, bias=False)
-        self.to(torch.bfloat16)
+from rwkv_layout import Tiny  # the reference model's module layout
 
 
 def test_ops_refuse_cpu_tensors(rq):

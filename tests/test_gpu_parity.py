@@ -1079,38 +1079,114 @@ def test_bound_qmm_matches_op(O, rq, dev, transpose):
         rq.BoundQmm(x, wq, s, b, transpose, gs, bits, out=torch.empty(1, device=dev))
 
 
-def test_quantized_checkpoint_roundtrip_gpu(O, rq, dev, tmp_path):
-    """A model quantized on the GPU (quantize_base_model, 3-bit body and 8-bit
-    head via a per-module predicate), saved with save_quantized and loaded into
-    a fresh float model with load_quantized, gives bit-identical outputs."""
-    from torch import nn
+QUANT_TARGETS = ("emb", "head") + tuple(f"blocks.{i}.cmix.{n}" for i in range(2)
+                                          for n in ("key", "value"))
+
+
+def _check_quantized_module(O, mod, w_src, gs, bits, what):
+    """mod's packed words, scales and biases equal O.quantize of the source
+    weight bit for bit."""
+    owq, os_, ob = O.quantize(w_src, gs, bits)
+    assert mod.bits == bits and mod.group_size == gs, what
+    assert bits_equal(mod.weight, owq), f"{what}: packed words"
+    assert bits_equal(mod.scales, os_), f"{what}: scales"
+    assert bits_equal(mod.biases, ob), f"{what}: biases"
+    return owq, os_, ob
+
+
+def _check_products(O, model, idx, packed, what):
+    """Every quantized module's HIP output against the oracle on the packed
+    tensors: the embedding rows bit-exact to O.dequantize, the linear products
+    within rel-err 1e-2 of O.quantized_matmul over the same bf16 inputs."""
+    parts = model.forward_parts(idx)
+    inputs = {"head": parts["emb"]}
+    for i in range(len(model.blocks)):
+        inputs[f"blocks.{i}.cmix.key"] = parts["emb"]
+        inputs[f"blocks.{i}.cmix.value"] = parts[f"blocks.{i}.cmix.key"]
+    wq, s, b, gs, bits = packed["emb"]
+    rows = O.dequantize(wq, s, b, gs, bits)[idx.cpu().reshape(-1)].reshape(parts["emb"].shape)
+    assert bits_equal(parts["emb"], rows), f"{what}: embedding rows"
+    for path, x in inputs.items():
+        wq, s, b, gs, bits = packed[path]
+        ref = O.quantized_matmul(x.cpu(), wq, s, b, True, gs, bits, out_dtype=torch.float32,
+                                 weights="exact")
+        rel_check(parts[path], ref, what=f"{what}: {path}")
+
+
+def test_quantize_base_model_gpu_bit_exact(O, rq, dev):
+    """quantize_base_model (rwkv_metal/lora/finetune.py:70-91) on a CUDA model
+    with the reference's module layout: exactly BIG_QUANT_TARGETS (cmix.key,
+    cmix.value, head, emb; finetune.py:42) are swapped, each swapped module's
+    (weight, scales, biases) is bit-exact to O.quantize of the original weight,
+    the tmix projections and the low-rank branch keep their float weights, and
+    the swapped modules' outputs match the oracle's products."""
+    from rwkv_layout import Tiny
+    m = Tiny(d=256, n=2, vocab=512, device=dev, seed=71)
+    src = {k: v.detach().cpu().clone() for k, v in m.state_dict().items()}
+    say("quantize_base_model bits=4 gs=64")
+    assert rq.quantize_base_model(m, bits=4, group_size=64) is m
+    packed = {}
+    for path, mod in m.named_modules():
+        if isinstance(mod, (rq.QuantizedLinear, rq.QuantizedEmbedding)):
+            assert path in QUANT_TARGETS, f"{path} quantized but not a target"
+            assert isinstance(mod, rq.QuantizedEmbedding) == (path == "emb"), path
+            packed[path] = (*_check_quantized_module(O, mod, src[f"{path}.weight"], 64, 4, path),
+                            64, 4)
+    assert sorted(packed) == sorted(QUANT_TARGETS)
+    for i, blk in enumerate(m.blocks):
+        for name in ("r_proj", "k_proj", "v_proj", "o_proj", "w_lora"):
+            lin = getattr(blk.tmix, name)
+            assert type(lin) is torch.nn.Linear, f"blocks.{i}.tmix.{name} was swapped"
+            assert bits_equal(lin.weight, src[f"blocks.{i}.tmix.{name}.weight"])
+    idx = torch.tensor([[0, 5, 77, 511], [3, 3, 200, 1]], device=dev)
+    _check_products(O, m, idx, packed, "quantize_base_model")
+
+
+def test_quantized_checkpoint_against_oracle(O, rq, dev, tmp_path):
+    """save_quantized / load_quantized (the packed checkpoint of an nn.quantize'd
+    model, keys <path>.weight/.scales/.biases as MLX saves them;
+    rwkv_metal/model/convert.py:437, rwkv_metal/lora/lora.py:140-148) with a
+    3-bit body and an 8-bit head chosen per module: the file's tensors are
+    O.quantize of the source weights bit for bit, the loaded model gets the
+    same bits and group sizes back from the stored shapes, and its HIP outputs
+    match the oracle's products of the file's tensors."""
+    from safetensors.torch import load_file
+    from rwkv_layout import Tiny
     from rwkvq import io as rio
 
-    class M(nn.Module):
-        def __init__(self):
-            super().__init__()
-            self.emb = nn.Embedding(512, 256)
-            self.key = nn.Linear(256, 1024, bias=False)
-            self.value = nn.Linear(1024, 256, bias=True)
-            self.head = nn.Linear(256, 512, bias=False)
-
-    torch.manual_seed(3)
-    src = M().to(dev, torch.bfloat16)
-    rq.quantize_model(src, 64, 3, class_predicate=lambda p, m: (
-        {"bits": 8} if p == "head" else isinstance(m, (nn.Linear, nn.Embedding))))
+    src_model = Tiny(d=256, n=2, vocab=512, device=dev, seed=73)
+    src = {k: v.detach().cpu().clone() for k, v in src_model.state_dict().items()}
+    setting = {p: (64, 8 if p == "head" else 3) for p in QUANT_TARGETS}
+    say("checkpoint: quantize 3-bit body / 8-bit head, save, load")
+    rq.quantize_model(src_model, 64, 3, class_predicate=lambda p, mod: (
+        {"bits": 8} if p == "head" else p in QUANT_TARGETS))
     path = str(tmp_path / "m.safetensors")
-    rio.save_quantized(src, path)
-    dst = M().to(dev, torch.bfloat16)
+    rio.save_quantized(src_model, path)
+    assert rio.quantization_config(path) == {"group_size": 64, "bits": 3,
+                                             "head": {"group_size": 64, "bits": 8}}
+    f = load_file(path)
+    packed = {}
+    for p, (gs, bits) in setting.items():
+        owq, os_, ob = O.quantize(src[f"{p}.weight"], gs, bits)
+        assert f[f"{p}.weight"].dtype == torch.uint32, p
+        assert torch.equal(f[f"{p}.weight"].view(torch.int32), owq), f"{p}: file words"
+        assert bits_equal(f[f"{p}.scales"], os_) and bits_equal(f[f"{p}.biases"], ob), p
+        packed[p] = (f[f"{p}.weight"].view(torch.int32), f[f"{p}.scales"], f[f"{p}.biases"],
+                     gs, bits)
+    for k, v in src.items():        # every float tensor is stored as it was
+        if k.rpartition(".")[0] not in setting:
+            assert bits_equal(f[k], v), k
+
+    dst = Tiny(d=256, n=2, vocab=512, device=dev, seed=999)   # different float weights
     rio.load_quantized(dst, path)
-    idx = torch.tensor([[1, 7, 511]], device=dev)
-    say("checkpoint roundtrip")
-
-    def run(m):
-        h = m.emb(idx)
-        return m.head(m.value(m.key(h)))
-
-    assert dst.head.bits == 8 and dst.key.bits == 3
-    assert torch.equal(run(src), run(dst))
+    for p, (gs, bits) in setting.items():
+        mod = dst.get_submodule(p)
+        assert (mod.group_size, mod.bits) == (gs, bits), p
+        assert bits_equal(mod.weight, packed[p][0]), p
+    for i in range(2):              # unquantized modules took the file's weights
+        assert bits_equal(dst.blocks[i].tmix.r_proj.weight, src[f"blocks.{i}.tmix.r_proj.weight"])
+    idx = torch.tensor([[1, 7, 511, 0]], device=dev)
+    _check_products(O, dst, idx, packed, "loaded checkpoint")
 
 
 # ------------------------------------------------------------ sb6 / K3
