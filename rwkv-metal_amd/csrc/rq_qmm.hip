@@ -337,28 +337,37 @@ __global__ __launch_bounds__(kBlock) void qmm_n_kernel(
 // Blocks are assigned to tiles so that each XCD works on a contiguous run of
 // tiles (shared activation rows and weight rows stay in that XCD's L2).
 
-// One run of 32 codes -> 16 dwords of bf16 pairs, ŵ = bf16(scale*code + bias),
-// using byte converts (v_cvt_f32_ubyte0..3) for 4- and 8-bit codes.  The
-// nibble masks are hidden from the optimiser (empty asm): otherwise it folds
-// mask and byte select into one bit-field extract per code, a second VALU
-// op per code in front of a v_cvt_f32_ubyte0.  Per 8 codes at 4 bits: 3
-// mask ops, 8 converts, 8 fmas, 4 packs.
+// Eight 4-bit codes of one word -> 4 dwords of bf16 pairs (codes 0,1 .. 6,7),
+// ŵ = bf16(s*code + b).  gfx950's v_cvt_scalef32_pk_f32_fp8 turns two bytes
+// into two fp32 values in one instruction: an e4m3 byte 0x0q is exactly
+// q / 512 (its subnormals and first binade are evenly spaced, 2^-9 apart),
+// and the conversion applies only the exponent of its scale (measured on
+// the box), so a scale of 512 gives q exactly.  Per 8 codes: 3 mask ops, 4
+// converts, 8 fmas, 4 packs (byte converts took 8 converts).
+RQ_DEV void dequant_word4(uint32_t word, float s, float b, uint32_t* out) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    const uint32_t lo = word & 0x0F0F0F0Fu;         // codes 0,2,4,6
+    const uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;  // codes 1,3,5,7
+    const f32x2_t l0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.f, false);
+    const f32x2_t l1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.f, true);
+    const f32x2_t h0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.f, false);
+    const f32x2_t h1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.f, true);
+    out[0] = pack_bf16x2(fmaf(s, l0[0], b), fmaf(s, h0[0], b));
+    out[1] = pack_bf16x2(fmaf(s, l0[1], b), fmaf(s, h0[1], b));
+    out[2] = pack_bf16x2(fmaf(s, l1[0], b), fmaf(s, h1[0], b));
+    out[3] = pack_bf16x2(fmaf(s, l1[1], b), fmaf(s, h1[1], b));
+}
+
+// One run of 32 codes -> 16 dwords of bf16 pairs, ŵ = bf16(scale*code + bias):
+// 4-bit codes by dequant_word4, 8-bit ones by byte converts
+// (v_cvt_f32_ubyte0..3; the bytes are hidden from the optimiser by an empty
+// asm, otherwise it folds each byte select into a bit-field extract, a second
+// VALU op per code in front of a v_cvt_f32_ubyte0).
 template <int BITS>
 RQ_DEV void dequant_run_fast(const uint32_t* words, float s, float b, uint32_t* out) {
     if constexpr (BITS == 4) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            uint32_t lo = words[w] & 0x0F0F0F0Fu;         // codes 0,2,4,6 of the word
-            uint32_t hi = (words[w] >> 4) & 0x0F0F0F0Fu;  // codes 1,3,5,7
-            asm("" : "+v"(lo));
-            asm("" : "+v"(hi));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float c0 = (float)(uint8_t)(lo >> (8 * i));
-                const float c1 = (float)(uint8_t)(hi >> (8 * i));
-                out[4 * w + i] = pack_bf16x2(fmaf(s, c0, b), fmaf(s, c1, b));
-            }
-        }
+        for (int w = 0; w < 4; ++w) dequant_word4(words[w], s, b, out + 4 * w);
     } else if constexpr (BITS == 8) {
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
@@ -1238,14 +1247,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                     const f32x2_t sv = *(const f32x2_t*)(sb + soff[i]);
                     uint32_t d[JC / 2];
                     if constexpr (JW == 1) {
-                        uint32_t lo = cv[u % D][i][0] & 0x0F0F0F0Fu;
-                        uint32_t hi = (cv[u % D][i][0] >> 4) & 0x0F0F0F0Fu;
-                        asm("" : "+v"(lo));
-                        asm("" : "+v"(hi));
-#pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            d[k] = pack_bf16x2(fmaf(sv[0], (float)(uint8_t)(lo >> (8 * k)), sv[1]),
-                                               fmaf(sv[0], (float)(uint8_t)(hi >> (8 * k)), sv[1]));
+                        dequant_word4(cv[u % D][i][0], sv[0], sv[1], d);
                     } else {
                         dequant_run_fast<BITS>(cv[u % D][i], sv[0], sv[1], d);
                     }
@@ -1569,6 +1571,8 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                         const float bc = gsel[i] == 0 ? bf[0] : (gsel[i] == 1 ? bf[1] : bf[2]);
                         uint32_t d[4];
                         if constexpr (WPC == 1) {
+                            // byte converts here: the fp8 pair conversion of dequant_word4
+                            // measured 3-4 % slower in this kernel ([8192, 2048] at M = 4096)
                             uint32_t lo = cv[u][i] & 0x0F0F0F0Fu;         // codes 0, 2, 4, 6
                             uint32_t hi = (cv[u][i] >> 4) & 0x0F0F0F0Fu;  // codes 1, 3, 5, 7
                             asm("" : "+v"(lo));

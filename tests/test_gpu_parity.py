@@ -521,6 +521,39 @@ def test_qmm_t_k64_tile_order_covers_every_tile(rq, dev):
     assert bool((err <= 1e-2 * ref.abs().max() + 1e-3).all())
 
 
+@pytest.mark.parametrize("gs", GROUPS)
+@pytest.mark.parametrize("bits", BITS)
+def test_qmm_t_k64_256_row_tiles(O, rq, dev, bits, gs):
+    """The 256-row tiles of the 64-wide-stage GEMM (eight MFMA waves of 64 x
+    BN/2 beside four producer waves) for every bit width and group size: M =
+    1100 gives 5 row tiles, the last one partial, by 64 (160-column, 4-bit) or
+    80 column tiles.  Every output element against an fp32 product of the
+    weights s*q + b from the bit-exact unpacked codes."""
+    M, R, K = 1100, 10240, 16 * gs
+    w = weights(R, K, 41 * bits + gs).to(dev)
+    wq, s, b = rq.quantize(w, gs, bits)
+    x = acts(M, K, 43 * bits + gs).to(dev)
+    say(f"qmm_t k64 256-row tiles bits={bits} gs={gs}")
+    y = rq.quantized_matmul(x, wq, s, b, True, gs, bits)
+    ref = _gpu_dense_ref(rq, x, wq, s, b, gs, bits, True)
+    rel_check(y, ref, what=f"qmm_t k64 256-row b{bits} g{gs}")
+    err = (y.float() - ref).abs()
+    assert bool((err <= 1e-2 * ref.abs().max() + 1e-3).all())
+
+
+def test_qmm_t_k64_256_row_tiles_oracle(O, rq, dev):
+    """One 256-row-tile problem against the CPU oracle itself (M = 800: 4 row
+    tiles by 64 column tiles of 160)."""
+    M, R, K = 800, 10240, 512
+    w = weights(R, K, 47)
+    wq, s, b = O.quantize(w, 64, 4)
+    x = acts(M, K, 53)
+    say("qmm_t k64 256-row tiles vs oracle")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
+    rel_check(y, O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32,
+                                    weights="exact"), what="k64 256-row oracle")
+
+
 @pytest.mark.parametrize("R", [130, 77, 64])
 def test_qmm_n_unaligned_rows(O, rq, dev, R):
     """Row counts whose activation rows are not 16-byte multiples (scalar loads)."""
