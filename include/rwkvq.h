@@ -106,7 +106,9 @@ int rq_dequantize(const uint32_t* w_q, const void* scales, const void* biases, r
  * product.  At 2 < m <= 16 fp32 / f16 x is rounded to bf16 once, and the GEMM
  * also rounds each s*q + b to bf16: on N(0,1) fp32 x about 1.6e-3 (GEMV) and
  * 2.3e-3 (GEMM) Frobenius-relative from the fp32 product.  bf16 x loses
- * nothing to either. */
+ * nothing to either.  At m >= 256 with 16-bit scales the GEMMs take bf16 and
+ * fp32 x on the same kernels: fp32 x is rounded to bf16 as it is staged, so
+ * its result equals that of bf16(x) with the same y_dt, bit for bit. */
 int rq_qmm(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
            const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
            int group_size, int bits, int transpose, void* y, rq_dtype y_dt, void* stream);
@@ -169,7 +171,7 @@ int rq_lora_down(const void* x, int64_t m, int64_t k, const void* a, int64_t ran
  * (the transpose=0 product of the QLoRA backward, finetune.py:141):
  * z = dY . lora_b, L = lora_a^T.  rank in {16, 32, 48, 64}; the term is
  * accumulated in fp32 with the GEMM and rounded once into y_dt.  Runs on the
- * 64-wide-stage GEMMs only (bf16 x, m >= 256, 16-bit scales 16-byte aligned;
+ * 64-wide-stage GEMMs only (bf16 or fp32 x, m >= 256, 16-bit scales 16-byte aligned;
  * transpose=1: cols a multiple of 8 groups; transpose=0: rows % 64 == 0,
  * cols % 128 == 0, or cols % 160 == 0 with 4- or 8-bit codes); other
  * problems return RQ_EUNSUPPORTED and the caller
@@ -208,6 +210,17 @@ int64_t rq_lora_grads_workspace_bytes(int64_t m, int64_t k, int64_t n, int64_t r
 int rq_lora_grads(const void* x, const void* u, const void* dy, const void* z, int64_t m,
                   int64_t k, int64_t n, int64_t rank, float scale, void* da, void* db,
                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/* rq_lora_grads with fp32 x and dy (the reference's default activations:
+ * fp32 residual stream, rwkv_metal/model/rwkv7_x070.py:51,189-194; the same
+ * adapter gradients of rwkv_metal/lora/lora.py:58-63 under nn.value_and_grad,
+ * rwkv_metal/lora/finetune.py:141).  u, z, da and db stay bf16.  x and dy are
+ * rounded to bf16 as the kernel stages them (the products are bf16 MFMAs with
+ * fp32 accumulation, as in rq_lora_grads); otherwise the same arguments,
+ * workspace rules (rq_lora_grads_workspace_bytes) and determinism. */
+int rq_lora_grads_f32(const float* x, const void* u, const float* dy, const void* z, int64_t m,
+                      int64_t k, int64_t n, int64_t rank, float scale, void* da, void* db,
+                      void* workspace, int64_t workspace_bytes, void* stream);
 
 /* rq_lora_grads without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops,

@@ -307,28 +307,43 @@ int64_t rq_lora_grads_workspace_bytes(int64_t m, int64_t k, int64_t n, int64_t r
     return (int64_t)p.work_bytes;
 }
 
-int rq_lora_grads(const void* x, const void* u, const void* dy, const void* z, int64_t m,
-                  int64_t k, int64_t n, int64_t rank, float scale, void* da, void* db,
-                  void* workspace, int64_t workspace_bytes, void* stream) {
-    if (int rc = check_lora_grads("rq_lora_grads", x, u, dy, z, m, k, n, rank, da, db)) return rc;
+static int lora_grads_common(const char* what, const void* x, const void* u, const void* dy,
+                             const void* z, int64_t m, int64_t k, int64_t n, int64_t rank,
+                             float scale, void* da, void* db, void* workspace,
+                             int64_t workspace_bytes, void* stream, bool xdy_f32) {
+    if (int rc = check_lora_grads(what, x, u, dy, z, m, k, n, rank, da, db)) return rc;
     hipStream_t s = (hipStream_t)stream;
     // m == 0 runs too: every job then stores a zero tile (no memset, so the
     // call may be captured in a HIP graph)
     const rq::LoraGradPlan p =
         rq::lora_grads_plan(m, k, n, (int)rank, da != nullptr, db != nullptr);
     if (p.tiles_a + p.tiles_b > rq::kLoraGradMaxTiles)
-        return fail(RQ_EINVAL, "rq_lora_grads: k/64 + n/64 exceeds %d", rq::kLoraGradMaxTiles);
+        return fail(RQ_EINVAL, "%s: k/64 + n/64 exceeds %d", what, rq::kLoraGradMaxTiles);
     const int64_t need = (int64_t)p.work_bytes;
     if (need > 0) {
         if (!workspace || workspace_bytes < need)
-            return fail(RQ_EINVAL, "rq_lora_grads: workspace has %lld bytes, needs %lld",
+            return fail(RQ_EINVAL, "%s: workspace has %lld bytes, needs %lld", what,
                         (long long)workspace_bytes, (long long)need);
         if (!aligned16(workspace))
-            return fail(RQ_EALIGN, "rq_lora_grads: workspace must be 16-byte aligned");
+            return fail(RQ_EALIGN, "%s: workspace must be 16-byte aligned", what);
     }
     return launch_status(rq::launch_lora_grads(x, u, dy, z, m, k, n, (int)rank, scale, da, db, p,
-                                               workspace, s),
-                         "rq_lora_grads");
+                                               workspace, s, xdy_f32),
+                         what);
+}
+
+int rq_lora_grads(const void* x, const void* u, const void* dy, const void* z, int64_t m,
+                  int64_t k, int64_t n, int64_t rank, float scale, void* da, void* db,
+                  void* workspace, int64_t workspace_bytes, void* stream) {
+    return lora_grads_common("rq_lora_grads", x, u, dy, z, m, k, n, rank, scale, da, db,
+                             workspace, workspace_bytes, stream, false);
+}
+
+int rq_lora_grads_f32(const float* x, const void* u, const float* dy, const void* z, int64_t m,
+                      int64_t k, int64_t n, int64_t rank, float scale, void* da, void* db,
+                      void* workspace, int64_t workspace_bytes, void* stream) {
+    return lora_grads_common("rq_lora_grads_f32", x, u, dy, z, m, k, n, rank, scale, da, db,
+                             workspace, workspace_bytes, stream, true);
 }
 
 int rq_lora_grads_noalloc(const void* x, const void* u, const void* dy, const void* z, int64_t m,
@@ -379,7 +394,7 @@ int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* s
                                         cols, group_size, bits, y, y_dt, (hipStream_t)stream, &lo);
     if (e == hipErrorNotSupported)
         return fail(RQ_EUNSUPPORTED,
-                    "rq_qmm_lora: the fused low-rank term needs the 64-wide-stage GEMMs (bf16 x, "
+                    "rq_qmm_lora: the fused low-rank term needs the 64-wide-stage GEMMs (bf16 or fp32 x, "
                     "m >= 256, 16-bit 16-byte aligned scales; transpose=1: cols a multiple of 8 "
                     "groups; transpose=0: rows %% 64 == 0, cols %% 128 == 0); use rq_qmm and add "
                     "the term separately");
@@ -411,7 +426,7 @@ int rq_qlora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scal
     if (e == hipErrorNotSupported)
         return fail(RQ_EUNSUPPORTED,
                     "rq_qlora: the in-kernel down-projection covers rank 16 with 4- or 8-bit codes "
-                    "on the 64-wide-stage GEMMs (bf16 x, m >= 256, 16-bit 16-byte aligned scales; "
+                    "on the 64-wide-stage GEMMs (bf16 or fp32 x, m >= 256, 16-bit 16-byte aligned scales; "
                     "transpose=1: cols a multiple of 8 groups; transpose=0: rows %% 64 == 0, "
                     "cols %% 128 == 0); use rq_lora_down and rq_qmm_lora");
     return launch_status(e, "rq_qlora");

@@ -115,9 +115,11 @@ LoraGradPlan lora_grads_plan(int64_t m, int64_t k, int64_t n, int rank, bool has
 // on that device).
 constexpr size_t kLoraScratchBytes = kLoraGradCounterBytes + (size_t)kLoraGradPartialCap;
 hipError_t lora_scratch(void** out, hipStream_t stream);
+// xdy_f32: x and dy are fp32 (u, z, da, db bf16).
 hipError_t launch_lora_grads(const void* x, const void* u, const void* dy, const void* z,
                              int64_t m, int64_t k, int64_t n, int rank, float scale, void* da,
-                             void* db, const LoraGradPlan& p, void* work, hipStream_t stream);
+                             void* db, const LoraGradPlan& p, void* work, hipStream_t stream,
+                             bool xdy_f32 = false);
 
 // MFMA GEMM, transpose=True: y[m, rows] = x[m, cols] . W^T.
 hipError_t launch_qmm_t(const void* x, int x_dt, const uint32_t* wq, const void* scales,

@@ -139,10 +139,10 @@ constexpr int kGradBlock = 256;
 
 RQ_DEV int pchunk(int c, int m) { return c ^ ((m & 3) << 1); }
 
-template <int RT>  // rank / 16
+template <int RT, bool PF>  // rank / 16; PF: x and dY are fp32 (rounded to bf16 as they are staged)
 __global__ __launch_bounds__(kGradBlock) void lora_grads_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ u,
-    const uint16_t* __restrict__ dy, const uint16_t* __restrict__ z, int64_t M, int64_t K,
+    const void* __restrict__ x, const uint16_t* __restrict__ u,
+    const void* __restrict__ dy, const uint16_t* __restrict__ z, int64_t M, int64_t K,
     int64_t N, float scale, uint16_t* __restrict__ da, uint16_t* __restrict__ db,
     float* __restrict__ part, uint32_t* __restrict__ cnt, int tiles_a, int S, int64_t mchunk) {
     constexpr int RANK = 16 * RT;
@@ -155,7 +155,8 @@ __global__ __launch_bounds__(kGradBlock) void lora_grads_kernel(
     const int lg = lane >> 4, lr = lane & 15;
     const int tile = (int)(blockIdx.x / S), s = (int)(blockIdx.x % S);
     const bool is_a = tile < tiles_a;
-    const uint16_t* P = is_a ? x : dy;
+    const uint8_t* P = (const uint8_t*)(is_a ? x : dy);
+    constexpr int PB = PF ? 4 : 2;  // bytes per x / dY element
     const uint16_t* Q = is_a ? u : z;
     const int64_t C = is_a ? K : N;
     const int64_t c0 = (int64_t)(is_a ? tile : tile - tiles_a) * 64;
@@ -167,14 +168,19 @@ __global__ __launch_bounds__(kGradBlock) void lora_grads_kernel(
     // 8 (t % 8) .. +7 (C % 8 == 0: a chunk is wholly inside or outside)
     const int prow = tid >> 3, pch = tid & 7;
     const bool pcol = c0 + pch * 8 < C;
-    u32x4_t pv[2], qv[QL];
+    u32x4_t pv[2][PF ? 2 : 1], qv[QL];
     auto load = [&](int st) {
         const int64_t m = mb + (int64_t)st * 64;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int64_t r = m + prow + 32 * h;
-            pv[h] = u32x4_t{0u, 0u, 0u, 0u};
-            if (r < me && pcol) pv[h] = *(const u32x4_t*)(P + r * C + c0 + pch * 8);
+#pragma unroll
+            for (int e = 0; e < (PF ? 2 : 1); ++e) pv[h][e] = u32x4_t{0u, 0u, 0u, 0u};
+            if (r < me && pcol) {
+                const u32x4_t* src = (const u32x4_t*)(P + (r * C + c0 + pch * 8) * PB);
+                pv[h][0] = src[0];
+                if constexpr (PF) pv[h][1] = src[1];
+            }
         }
 #pragma unroll
         for (int i = 0; i < QL; ++i) {
@@ -190,7 +196,13 @@ __global__ __launch_bounds__(kGradBlock) void lora_grads_kernel(
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int m = prow + 32 * h;
-            *(u32x4_t*)(pt[b] + m * 64 + pchunk(pch, m) * 8) = pv[h];
+            u32x4_t v = pv[h][0];
+            if constexpr (PF)
+                v = u32x4_t{pack_bf16x2(__uint_as_float(pv[h][0][0]), __uint_as_float(pv[h][0][1])),
+                            pack_bf16x2(__uint_as_float(pv[h][0][2]), __uint_as_float(pv[h][0][3])),
+                            pack_bf16x2(__uint_as_float(pv[h][1][0]), __uint_as_float(pv[h][1][1])),
+                            pack_bf16x2(__uint_as_float(pv[h][1][2]), __uint_as_float(pv[h][1][3]))};
+            *(u32x4_t*)(pt[b] + m * 64 + pchunk(pch, m) * 8) = v;
         }
 #pragma unroll
         for (int i = 0; i < QL; ++i) {
@@ -389,18 +401,22 @@ LoraGradPlan lora_grads_plan(int64_t m, int64_t k, int64_t n, int rank, bool has
 
 hipError_t launch_lora_grads(const void* x, const void* u, const void* dy, const void* z,
                              int64_t m, int64_t k, int64_t n, int rank, float scale, void* da,
-                             void* db, const LoraGradPlan& p, void* work, hipStream_t stream) {
+                             void* db, const LoraGradPlan& p, void* work, hipStream_t stream,
+                             bool xdy_f32) {
     const int tiles = p.tiles_a + p.tiles_b;
     if (tiles == 0) return hipSuccess;
     uint32_t* cnt = (uint32_t*)work;
     float* part = (float*)((uint8_t*)work + kLoraGradCounterBytes);
     const dim3 grid((unsigned)(tiles * p.splits)), block(kGradBlock);
-    const uint16_t *xp = (const uint16_t*)x, *up = (const uint16_t*)u;
-    const uint16_t *dyp = (const uint16_t*)dy, *zp = (const uint16_t*)z;
+    const uint16_t *up = (const uint16_t*)u, *zp = (const uint16_t*)z;
     uint16_t *dap = (uint16_t*)da, *dbp = (uint16_t*)db;
 #define RQ_GRADS(RT)                                                                           \
-    hipLaunchKernelGGL((lora_grads_kernel<RT>), grid, block, 0, stream, xp, up, dyp, zp, m, k, n,  \
-                       scale, dap, dbp, part, cnt, p.tiles_a, p.splits, p.mchunk)
+    if (xdy_f32)                                                                               \
+        hipLaunchKernelGGL((lora_grads_kernel<RT, true>), grid, block, 0, stream, x, up, dy, zp,  \
+                           m, k, n, scale, dap, dbp, part, cnt, p.tiles_a, p.splits, p.mchunk);  \
+    else                                                                                       \
+        hipLaunchKernelGGL((lora_grads_kernel<RT, false>), grid, block, 0, stream, x, up, dy, zp, \
+                           m, k, n, scale, dap, dbp, part, cnt, p.tiles_a, p.splits, p.mchunk)
     switch (rank) {
         case 16: RQ_GRADS(1); break;
         case 32: RQ_GRADS(2); break;

@@ -1069,6 +1069,31 @@ RQ_DEV void fused_lora_tail(f32x4_t (&acc)[TM][TN], const f32x4_t (&accz)[TM], f
         }
 }
 
+// A producer's 16-byte chunk of 8 activations for a bf16 LDS tile.  bf16
+// activations load it as is; fp32 ones (XF) load 32 bytes and round them to
+// bf16 (RNE) when the chunk is stored, so the tile, the MFMA operands and
+// everything after them are the same for both.
+template <bool XF>
+struct XChunk {
+    static constexpr int EB = XF ? 4 : 2;  // bytes per activation element
+    typedef const __attribute__((address_space(1))) u32x4_t* gv_t;
+    u32x4_t v[XF ? 2 : 1];
+    RQ_DEV void load(const uint8_t* p) {
+        v[0] = *(gv_t)p;
+        if constexpr (XF) v[1] = *((gv_t)p + 1);
+    }
+    RQ_DEV u32x4_t bf16() const {
+        if constexpr (XF) {
+            return u32x4_t{pack_bf16x2(__uint_as_float(v[0][0]), __uint_as_float(v[0][1])),
+                           pack_bf16x2(__uint_as_float(v[0][2]), __uint_as_float(v[0][3])),
+                           pack_bf16x2(__uint_as_float(v[1][0]), __uint_as_float(v[1][1])),
+                           pack_bf16x2(__uint_as_float(v[1][2]), __uint_as_float(v[1][3]))};
+        } else {
+            return v[0];
+        }
+    }
+};
+
 // ------------------------------------------------------------- qmm_t_k64
 //
 // The warp-specialised GEMM with 64-element contraction stages (bf16
@@ -1095,9 +1120,9 @@ RQ_DEV void fused_lora_tail(f32x4_t (&acc)[TM][TN], const f32x4_t (&accz)[TM], f
 //    software-pipelined by hand (B fragments of the next k-step and A
 //    fragments two MFMA groups ahead), with scheduling barriers keeping the
 //    order: the compiler's own order waited on every fragment read.
-template <int BITS, int SDT, int BN, int GSH, int BM, bool FZ = false>
+template <int BITS, int SDT, int BN, int GSH, int BM, bool FZ = false, bool XF = false>
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
+    const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, void* __restrict__ y,
     int y_dt, int tiles_m, int tiles_n, rq::LoraArgs lora) {
     static_assert(BM == 256 || BM == 128 || BM == 64, "block rows");
@@ -1149,10 +1174,10 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
             const int chunk = lane & 7;
             int64_t grow = m0 + row;
             grow = grow < M ? grow : M - 1;
-            xoff[i] = (uint32_t)((grow - m0) * K * 2 + chunk * 16);
+            xoff[i] = (uint32_t)((grow - m0) * K * XChunk<XF>::EB + chunk * 8 * XChunk<XF>::EB);
             xdst[i] = (uint32_t)(row * 128 + ((chunk ^ (row & 7)) * 16));
         }
-        const uint8_t* xbase = (const uint8_t*)(x + m0 * K);
+        const uint8_t* xbase = (const uint8_t*)x + m0 * K * XChunk<XF>::EB;
         // dequant jobs: job j = pt + 256 i is part j % JPR (JW words) of tile row j / JPR
         const uint32_t* wtile = wq + n0 * wpr;
         uint32_t coff[NJ], qoff[NJ], soff[NJ], qc0[NJ];
@@ -1172,13 +1197,13 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
         const uint16_t* srow_p = (const uint16_t*)scales + wrow * G;
         const uint16_t* brow_p = (const uint16_t*)biases + wrow * G;
 
-        u32x4_t xv[D][XL];
+        XChunk<XF> xv[D][XL];
         uint32_t cv[D][NJ][JW];
         auto issue = [&](int st, int r) {
             const int sc = st < nst ? st : nst - 1;
-            const uint8_t* xb = xbase + (int64_t)sc * 128;
+            const uint8_t* xb = xbase + (int64_t)sc * 64 * XChunk<XF>::EB;
 #pragma unroll
-            for (int i = 0; i < XL; ++i) xv[r][i] = *(gv_t)(xb + xoff[i]);
+            for (int i = 0; i < XL; ++i) xv[r][i].load(xb + xoff[i]);
             const uint32_t* ws = wtile + (int64_t)sc * SW;
 #pragma unroll
             for (int i = 0; i < NJ; ++i) {
@@ -1239,7 +1264,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                     load_sb(per + 2);
                 }
 #pragma unroll
-                for (int i = 0; i < XL; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u % D][i];
+                for (int i = 0; i < XL; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u % D][i].bf16();
                 const float* sb = sbf[per & 1] + 2 * ((u * 64) >> GSH);
 #pragma unroll
                 for (int i = 0; i < NJ; ++i) {
@@ -1428,9 +1453,9 @@ RQ_DEV int nkey(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 // physical 16-byte chunk of chunk c in tile row r
 RQ_DEV int nchunk(int c, int r) { return (c & ~7) | ((c ^ nkey(r)) & 7); }
 
-template <int BITS, int SDT, int BN = 128, bool FZ = false>
+template <int BITS, int SDT, int BN = 128, bool FZ = false, bool XF = false>
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
+    const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, int gs_shift,
     void* __restrict__ y, int y_dt, int tiles_m, int tiles_n, rq::LoraArgs lora) {
     constexpr int BM = 256, WN = BN / 2;
@@ -1468,10 +1493,10 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
             const int chunk = lane & 7;
             int64_t grow = m0 + row;
             grow = grow < M ? grow : M - 1;
-            xoff[i] = (uint32_t)((grow - m0) * R * 2 + chunk * 16);
+            xoff[i] = (uint32_t)((grow - m0) * R * XChunk<XF>::EB + chunk * 8 * XChunk<XF>::EB);
             xdst[i] = (uint32_t)(row * 128 + ((chunk ^ (row & 7)) * 16));
         }
-        const uint8_t* xbase = (const uint8_t*)(x + m0 * R);
+        const uint8_t* xbase = (const uint8_t*)x + m0 * R * XChunk<XF>::EB;
         if constexpr (BN == 160) {
             // Lane L of producer wave pw takes row jr = 16 pw + L / 4 of each
             // stage and its chunks 5 q .. 5 q + 4 (q = L % 4, 8 codes each), so
@@ -1509,14 +1534,14 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                 srcl[j] = ((lane & ~3) | (rel & 3)) * 4;
                 slot[j] = rel >> 2;
             }
-            u32x4_t xv[D][8];
+            XChunk<XF> xv[D][8];
             uint32_t cv[D][NC * WPC];
             uint32_t sv[D][2];  // scale | bias << 16 of groups g0 + jq and g0 + 4 + jq
             auto issue = [&](int st, int r) {
                 const int sc = st < nst ? st : nst - 1;
-                const uint8_t* xb = xbase + (int64_t)sc * 128;
+                const uint8_t* xb = xbase + (int64_t)sc * 64 * XChunk<XF>::EB;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) xv[r][i] = *(gv_t)(xb + xoff[i]);
+                for (int i = 0; i < 8; ++i) xv[r][i].load(xb + xoff[i]);
                 const int64_t row = (int64_t)sc * 64 + jr;
                 const uint32_t* ws = wbase + row * wpr;
                 if constexpr (WPC == 1) {
@@ -1549,7 +1574,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                     uint8_t* xs = u ? xs1 : xs0;
                     uint8_t* bq = u ? bq1 : bq0;
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u][i];
+                    for (int i = 0; i < 8; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u][i].bf16();
                     float sf[NG], bf[NG];
 #pragma unroll
                     for (int j = 0; j < NG; ++j) {
@@ -1616,14 +1641,14 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
 #pragma unroll
         for (int q = 0; q < 4; ++q) qdst[q] = (uint32_t)(jr * ROWB + (((4 * jq + q) ^ nkey(jr)) << 4));
 
-        u32x4_t xv[D][8];
+        XChunk<XF> xv[D][8];
         uint32_t cv[D][BITS];
         uint16_t sv[D][2];
         auto issue = [&](int st, int r) {
             const int sc = st < nst ? st : nst - 1;
-            const uint8_t* xb = xbase + (int64_t)sc * 128;
+            const uint8_t* xb = xbase + (int64_t)sc * 64 * XChunk<XF>::EB;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xv[r][i] = *(gv_t)(xb + xoff[i]);
+            for (int i = 0; i < 8; ++i) xv[r][i].load(xb + xoff[i]);
             const int64_t row = (int64_t)sc * 64 + jr;
             const uint32_t* ws = wbase + row * wpr;
             if constexpr (BITS % 4 == 0) {
@@ -1652,7 +1677,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
                 uint8_t* xs = u ? xs1 : xs0;
                 uint8_t* bq = u ? bq1 : bq0;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u][i];
+                for (int i = 0; i < 8; ++i) *(u32x4_t*)(xs + xdst[i]) = xv[u][i].bf16();
                 uint32_t d[16];
                 dequant_run_fast<BITS>(cv[u], dt_traits<SDT>::to_f32(sv[u][0]),
                                        dt_traits<SDT>::to_f32(sv[u][1]), d);
@@ -1813,9 +1838,11 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
                                       int y_dt, hipStream_t stream, const LoraArgs* lora) {
     const int gs_shift = __builtin_ctz(gs);
     const LoraArgs lo = lora ? *lora : LoraArgs{nullptr, nullptr, 0, 0.f};
-    const bool k64 = m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 &&
-                     cols % 64 == 0 && (cols / gs) % 8 == 0 &&
-                     (((uintptr_t)scales | (uintptr_t)biases) & 15) == 0;
+    // bf16 or fp32 activations (fp32 rounded to bf16 as the producers stage them)
+    const bool k64 = m >= 256 && (x_dt == RQ_BF16 || x_dt == RQ_F32) && RQ_GEMM_K64 &&
+                     sb_dt != RQ_F32 && cols % 64 == 0 && (cols / gs) % 8 == 0 &&
+                     (((uintptr_t)x | (uintptr_t)scales | (uintptr_t)biases) & 15) == 0;
+    const bool xf = x_dt == RQ_F32;
     if (lora && lora->a) {
         // the fused QLoRA layer with its down-projection in the kernel: rank 16,
         // 4- or 8-bit codes, 128-column tiles (the 160-column ones have no
@@ -1826,10 +1853,12 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
         const int bm = ((m + 255) / 256) * tn < RQ_K64_BM128_BELOW ? 128 : 256;
         const int tm = (int)((m + bm - 1) / bm);
         const int blocks = ((tm * tn + 7) / 8) * 8;
-#define RQ_FZ_BM(SD, GSHV, BMV)                                                                   \
-    hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, 128, GSHV, BMV, true>), dim3(blocks),              \
-                       dim3(kWsBlock), 0, stream, (const uint16_t*)x, wq, scales, biases, m, rows, \
-                       cols, y, y_dt, tm, tn, lo)
+#define RQ_FZ_BMX(SD, GSHV, BMV, XFV)                                                             \
+    hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, 128, GSHV, BMV, true, XFV>), dim3(blocks),         \
+                       dim3(kWsBlock), 0, stream, x, wq, scales, biases, m, rows, cols, y, y_dt,   \
+                       tm, tn, lo)
+#define RQ_FZ_BM(SD, GSHV, BMV) \
+    if (xf) { RQ_FZ_BMX(SD, GSHV, BMV, true); } else { RQ_FZ_BMX(SD, GSHV, BMV, false); }
 #define RQ_FZ(SD, GSHV) \
     if (bm == 256) { RQ_FZ_BM(SD, GSHV, 256); } else { RQ_FZ_BM(SD, GSHV, 128); }
 #define RQ_FZ_GS(SD)                          \
@@ -1842,6 +1871,7 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
 #undef RQ_FZ_GS
 #undef RQ_FZ
 #undef RQ_FZ_BM
+#undef RQ_FZ_BMX
         return hipGetLastError();
 #else
         return hipErrorNotSupported;
@@ -1864,10 +1894,12 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
         }
         const int tm = (int)((m + bm - 1) / bm);
         const int blocks = ((tm * tn + 7) / 8) * 8;
-#define RQ_K64_BM(SD, BNV, GSHV, BMV)                                                             \
-    hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, BNV, GSHV, BMV>), dim3(blocks), dim3(kWsBlock), 0,\
-                       stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols, y, y_dt, tm, tn,  \
-                       lo)
+#define RQ_K64_BMX(SD, BNV, GSHV, BMV, XFV)                                                       \
+    hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, BNV, GSHV, BMV, false, XFV>), dim3(blocks),        \
+                       dim3(kWsBlock), 0, stream, x, wq, scales, biases, m, rows, cols, y, y_dt,   \
+                       tm, tn, lo)
+#define RQ_K64_BM(SD, BNV, GSHV, BMV) \
+    if (xf) { RQ_K64_BMX(SD, BNV, GSHV, BMV, true); } else { RQ_K64_BMX(SD, BNV, GSHV, BMV, false); }
 #define RQ_K64(SD, BNV, GSHV)                                                                     \
     if (bm == 256) { RQ_K64_BM(SD, BNV, GSHV, 256); } else { RQ_K64_BM(SD, BNV, GSHV, 128); }
 #define RQ_K64_GS(SD, BNV)                                                                        \
@@ -1897,6 +1929,7 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
 #undef RQ_K64_GS
 #undef RQ_K64
 #undef RQ_K64_BM
+#undef RQ_K64_BMX
         return hipGetLastError();
     }
     if (lora) return hipErrorNotSupported;  // the low-rank term rides on the k64 kernels only
@@ -1956,9 +1989,22 @@ hipError_t RQ_CAT(launch_qmm_n_b, RQ_BITS)(const void* x, int x_dt, const uint32
     // columns (160: 4- and 8-bit codes)
     const bool can128 = cols % 128 == 0;
     const bool can160 = (RQ_BITS == 4 || RQ_BITS == 8) && RQ_GEMM_N160 && cols % 160 == 0;
-    const bool k64 = m >= 256 && x_dt == RQ_BF16 && RQ_GEMM_K64 && sb_dt != RQ_F32 &&
-                     rows % 64 == 0 && (can128 || can160) && ((uintptr_t)x & 15) == 0 &&
-                     (((uintptr_t)scales | (uintptr_t)biases) & 7) == 0;
+    // bf16 or fp32 dY (fp32 rounded to bf16 as the producers stage it)
+    const bool k64 = m >= 256 && (x_dt == RQ_BF16 || x_dt == RQ_F32) && RQ_GEMM_K64 &&
+                     sb_dt != RQ_F32 && rows % 64 == 0 && (can128 || can160) &&
+                     ((uintptr_t)x & 15) == 0 && (((uintptr_t)scales | (uintptr_t)biases) & 7) == 0;
+    const bool xf = x_dt == RQ_F32;
+#define RQ_NK64(SD, BNV, FZV)                                                                       \
+    do {                                                                                           \
+        if (xf)                                                                                    \
+            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, SD, BNV, FZV, true>), dim3(blocks),            \
+                               dim3(kWsBlock), 0, stream, x, wq, scales, biases, m, rows, cols,   \
+                               __builtin_ctz(gs), y, y_dt, tm, tn, lo);                           \
+        else                                                                                       \
+            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, SD, BNV, FZV, false>), dim3(blocks),           \
+                               dim3(kWsBlock), 0, stream, x, wq, scales, biases, m, rows, cols,   \
+                               __builtin_ctz(gs), y, y_dt, tm, tn, lo);                           \
+    } while (0)
     if (lora && lora->a) {
         // the fused QLoRA layer's dX with u = dY . B in the kernel (rank 16,
         // 4- or 8-bit codes)
@@ -1967,14 +2013,8 @@ hipError_t RQ_CAT(launch_qmm_n_b, RQ_BITS)(const void* x, int x_dt, const uint32
         const int tm = (int)((m + 255) / 256);
         const int tn = (int)(cols / 128);
         const int blocks = ((tm * tn + 7) / 8) * 8;
-        if (sb_dt == RQ_BF16)
-            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_BF16, 128, true>), dim3(blocks), dim3(kWsBlock), 0,
-                               stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
-                               __builtin_ctz(gs), y, y_dt, tm, tn, lo);
-        else
-            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_F16, 128, true>), dim3(blocks), dim3(kWsBlock), 0,
-                               stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
-                               __builtin_ctz(gs), y, y_dt, tm, tn, lo);
+        if (sb_dt == RQ_BF16) RQ_NK64(RQ_BF16, 128, true);
+        else RQ_NK64(RQ_F16, 128, true);
         return hipGetLastError();
 #else
         return hipErrorNotSupported;
@@ -1996,27 +2036,16 @@ hipError_t RQ_CAT(launch_qmm_n_b, RQ_BITS)(const void* x, int x_dt, const uint32
         const int blocks = ((tm * tn + 7) / 8) * 8;
 #if RQ_BITS == 4 || RQ_BITS == 8
         if (wide) {
-            if (sb_dt == RQ_BF16)
-                hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_BF16, 160>), dim3(blocks), dim3(kWsBlock), 0,
-                                   stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
-                                   __builtin_ctz(gs), y, y_dt, tm, tn, lo);
-            else
-                hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_F16, 160>), dim3(blocks), dim3(kWsBlock), 0,
-                                   stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
-                                   __builtin_ctz(gs), y, y_dt, tm, tn, lo);
+            if (sb_dt == RQ_BF16) RQ_NK64(RQ_BF16, 160, false);
+            else RQ_NK64(RQ_F16, 160, false);
             return hipGetLastError();
         }
 #endif
-        if (sb_dt == RQ_BF16)
-            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_BF16>), dim3(blocks), dim3(kWsBlock), 0,
-                               stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
-                               __builtin_ctz(gs), y, y_dt, tm, tn, lo);
-        else
-            hipLaunchKernelGGL((qmm_n_k64<RQ_BITS, RQ_F16>), dim3(blocks), dim3(kWsBlock), 0,
-                               stream, (const uint16_t*)x, wq, scales, biases, m, rows, cols,
-                               __builtin_ctz(gs), y, y_dt, tm, tn, lo);
+        if (sb_dt == RQ_BF16) RQ_NK64(RQ_BF16, 128, false);
+        else RQ_NK64(RQ_F16, 128, false);
         return hipGetLastError();
     }
+#undef RQ_NK64
     if (lora) return hipErrorNotSupported;  // the low-rank term rides on the k64 kernels only
     constexpr int BM = 128;
     const dim3 grid((unsigned)((cols + BN - 1) / BN), (unsigned)((m + BM - 1) / BM));

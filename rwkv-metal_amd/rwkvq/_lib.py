@@ -59,6 +59,8 @@ SIGNATURES = {
     "rq_lora_grads_workspace_bytes": ([_i64, _i64, _i64, _i64, _i32, _i32], _i64),
     "rq_lora_grads": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _vp,
                        _i64, _vp], _i32),
+    "rq_lora_grads_f32": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp,
+                           _vp, _i64, _vp], _i32),
     "rq_lora_grads_noalloc": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp,
                                _vp, _vp], _i32),
     "rq_embedding": ([_vp, _i64, _vp, _vp, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _i32, _vp],

@@ -10,9 +10,10 @@
 
 y = base(x) + (alpha/rank) * (x @ A^T) @ B^T with A ~ N(0, 1)/sqrt(in_features)
 and B = 0 (lora.py:54-56).  Only lora_a / lora_b are trainable (lora.py:101-102).
-Over a QuantizedLinear base with bf16 activations the low-rank term is fused
-into the packed-weight GEMMs, forward and dX (rq_qmm_lora, _QLoRAFunction);
-other bases and dtypes compose the ops.
+Over a QuantizedLinear base with bf16 or fp32 activations (bf16 adapters)
+the low-rank term is fused into the packed-weight GEMMs, forward and dX
+(rq_qlora / rq_qmm_lora, _QLoRAFunction); other bases and dtypes compose the
+ops.
 The model layout is the reference's: model.blocks[i].tmix.{r,k,v,o}_proj and
 model.blocks[i].cmix.{key,value}.
 
@@ -134,10 +135,14 @@ class LoRALinear(nn.Module):
 
     def _fusable(self, x: Tensor) -> bool:
         """The low-rank term can ride on the packed-weight GEMMs: quantized
-        base, bf16 activations and adapters, a supported rank, no active
-        dropout on z (its mask would have to be saved for the backward)."""
+        base, bf16 adapters, a supported rank, no active dropout on z (its
+        mask would have to be saved for the backward), and bf16 activations
+        or fp32 ones (the reference's default residual stream,
+        rwkv_metal/model/rwkv7_x070.py:51,189-194), which the kernels round to
+        bf16 as they stage them; y and dX are then fp32."""
         return (isinstance(self.linear, QuantizedLinear) and x.is_cuda
-                and x.dtype == self.lora_a.dtype == self.lora_b.dtype == torch.bfloat16
+                and x.dtype in (torch.bfloat16, torch.float32)
+                and self.lora_a.dtype == self.lora_b.dtype == torch.bfloat16
                 and self.rank in (16, 32, 48, 64)
                 and (self.dropout is None or not self.training))
 

@@ -326,12 +326,16 @@ def lora_down(x: Tensor, a: Tensor) -> Tensor:
     z = x A^T in the forward, u = dY B (a = B^T) in the backward
     (rwkv_metal/lora/lora.py:58-63).  bf16 CUDA operands with a rank of 16,
     32, 48 or 64 and an inner size that is a multiple of 32 run rq_lora_down
-    (one HIP launch); other operands take torch's matmul."""
+    (one HIP launch); other operands take torch's matmul, fp32 x against a
+    bf16 adapter in fp32 with z rounded once to bf16 (the form the fused
+    kernels produce)."""
     if x.shape[-1] != a.shape[-1]:
         raise ValueError(f"lora_down: x has inner size {x.shape[-1]}, a has {a.shape[-1]}")
     rank, k = a.shape[0], a.shape[-1]
     if not (x.is_cuda and x.dtype == a.dtype == torch.bfloat16 and rank in (16, 32, 48, 64)
             and k % 32 == 0 and k > 0):
+        if x.dtype == torch.float32 and a.dtype == torch.bfloat16:
+            return (x @ a.float().t()).to(torch.bfloat16)
         return x @ a.t()
     _on_gpu(x, a)
     x2 = _ready(x.reshape(-1, k))
@@ -371,16 +375,20 @@ def lora_grads(x: Tensor | None, u: Tensor | None, dy: Tensor | None, z: Tensor 
                scale: float) -> Tuple[Tensor | None, Tensor | None]:
     """The QLoRA adapter gradients of rwkv_metal/lora/lora.py:58-63 under
     nn.value_and_grad (finetune.py:141): dA = scale * u^T x [rank, K] and
-    dB = scale * dY^T z [N, rank], bf16, in one rq_lora_grads launch.  Pass
-    None for both operands of a gradient that is not needed."""
+    dB = scale * dY^T z [N, rank], bf16, in one rq_lora_grads launch
+    (rq_lora_grads_f32 when x and dY are fp32, the reference's default
+    activations; u and z are bf16 either way).  Pass None for both operands
+    of a gradient that is not needed."""
     want_a, want_b = x is not None, dy is not None
     ref = x if want_a else dy
     if ref is None:
         return None, None
     q = u if want_a else z
     rank = q.shape[-1]
-    if not (ref.is_cuda and rank in (16, 32, 48, 64)
-            and all(t is None or t.dtype == torch.bfloat16 for t in (x, u, dy, z))
+    xdt = ref.dtype
+    if not (ref.is_cuda and rank in (16, 32, 48, 64) and xdt in (torch.bfloat16, torch.float32)
+            and all(t is None or t.dtype == xdt for t in (x, dy))
+            and all(t is None or t.dtype == torch.bfloat16 for t in (u, z))
             and (not want_a or x.shape[-1] % 8 == 0) and (not want_b or dy.shape[-1] % 8 == 0)):
         da = (scale * (u.float().t() @ x.float())).to(u.dtype) if want_a else None
         db = (scale * (dy.float().t() @ z.float())).to(z.dtype) if want_b else None
@@ -402,11 +410,12 @@ def lora_grads(x: Tensor | None, u: Tensor | None, dy: Tensor | None, z: Tensor 
         nbytes = L.rq_lora_grads_workspace_bytes(m, K, N, rank, int(want_a), int(want_b))
         check(nbytes if nbytes < 0 else 0, "lora_grads")
         ws = _lora_workspace(ref.device, stream, int(nbytes)) if nbytes > 0 else None
-        rc = L.rq_lora_grads(_ptr(x2) if want_a else 0, _ptr(u2) if want_a else 0,
-                             _ptr(dy2) if want_b else 0, _ptr(z2) if want_b else 0, m, K, N,
-                             rank, float(scale), _ptr(da) if want_a else 0,
-                             _ptr(db) if want_b else 0, ws.data_ptr() if ws is not None else 0,
-                             ws.numel() if ws is not None else 0, stream)
+        fn = L.rq_lora_grads_f32 if xdt == torch.float32 else L.rq_lora_grads
+        rc = fn(_ptr(x2) if want_a else 0, _ptr(u2) if want_a else 0,
+                _ptr(dy2) if want_b else 0, _ptr(z2) if want_b else 0, m, K, N,
+                rank, float(scale), _ptr(da) if want_a else 0,
+                _ptr(db) if want_b else 0, ws.data_ptr() if ws is not None else 0,
+                ws.numel() if ws is not None else 0, stream)
     check(rc, "lora_grads")
     return da, db
 
@@ -414,7 +423,7 @@ def lora_grads(x: Tensor | None, u: Tensor | None, dy: Tensor | None, z: Tensor 
 def _qmm_lora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, z: Tensor,
                     lora: Tensor, scale: float, transpose: bool, group_size: int, bits: int):
     """rq_qmm_lora on 2-D operands; None where the fused kernels do not apply."""
-    if not (x.dtype == z.dtype == lora.dtype == torch.bfloat16):
+    if not (x.dtype in (torch.bfloat16, torch.float32) and z.dtype == lora.dtype == torch.bfloat16):
         return None
     x, w_q, scales = _ready(x), _ready(w_q), _ready(scales)
     biases, z, lora = _ready(biases.to(scales.dtype)), _ready(z), _ready(lora)
@@ -450,7 +459,8 @@ def qlora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, a: Tenso
     if (x.dim() != 2 or x.shape[1] != n_in or tuple(a.shape) != (rank, n_in)
             or tuple(lora.shape) != (n_out, rank)):
         raise ValueError("qlora_fused: x, a and lora shapes do not agree")
-    if not (x.dtype == a.dtype == lora.dtype == torch.bfloat16) or rank != 16:
+    if not (x.dtype in (torch.bfloat16, torch.float32) and a.dtype == lora.dtype == torch.bfloat16
+            and rank == 16):
         return None
     _on_gpu(x, w_q, scales, biases, a, lora)
     x, w_q, scales, a, lora = _ready(x), _ready(w_q), _ready(scales), _ready(a), _ready(lora)

@@ -29,7 +29,7 @@ def test_header_declares_the_expected_surface():
         "rq_pack", "rq_unpack", "rq_qmm_grouped", "rq_grouped_plan_table_bytes",
         "rq_grouped_plan_init", "rq_grouped_plan_run", "rq_embedding", "rq_sb6_dequantize",
         "rq_sb6_to_affine", "rq_qmm_lora", "rq_lora_down", "rq_lora_grads_workspace_bytes",
-        "rq_lora_grads", "rq_lora_grads_noalloc", "rq_qlora"])
+        "rq_lora_grads", "rq_lora_grads_f32", "rq_lora_grads_noalloc", "rq_qlora"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -175,6 +175,13 @@ def test_lora_grads_workspace_and_rejections(L):
     assert "workspace" in _err(L)
     # dA only: dY and z are not read, so they may be NULL
     assert L.rq_lora_grads(p, p, 0, 0, 4096, 2048, 2048, 16, 1.0, p, 0, 0, 0, None) == -1
+    assert "workspace" in _err(L)
+    # the fp32-operand form checks the same things and names itself
+    assert L.rq_lora_grads_f32(p, p, p, p, 4096, 2048, 2048, 24, 1.0, p, p, p, 1 << 30, None) == -1
+    assert "rq_lora_grads_f32" in _err(L) and "rank" in _err(L)
+    assert L.rq_lora_grads_f32(p + 8, p, p, p, 4096, 2048, 2048, 16, 1.0, p, p, p, 1 << 30,
+                               None) == -2
+    assert L.rq_lora_grads_f32(p, p, p, p, 4096, 2048, 2048, 16, 1.0, p, p, p, 64, None) == -1
     assert "workspace" in _err(L)
 
 
