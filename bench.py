@@ -411,12 +411,14 @@ def config5(torch, rq, dev, args):
     return out
 
 
-def qlora_layers(torch, rq, dev, ws):
+def qlora_layers(torch, rq, dev, ws, xdt=None):
     """Config 4's QLoRA layer: for each projection a LoRALinear (r = alpha =
-    16, A ~ N(0, 1/D), B ~ N(0, 0.01) std) over the frozen 4-bit g64 base
-    `ws[i]`, with x [8, 512, K] and dY [8, 512, R] bf16.  Returns the
+    16, A ~ N(0, 1/D), B ~ N(0, 0.01) std, bf16) over the frozen 4-bit g64
+    base `ws[i]`, with x [8, 512, K] and dY [8, 512, R] in `xdt` (bf16 by
+    default; fp32 is the reference's residual stream).  Returns the
     (layer, x, dY) triples and the step's flops (base forward + dX GEMMs and
     the adapter GEMMs)."""
+    xdt = xdt or torch.bfloat16
     r, alpha, M = 16, 16.0, 8 * 512
     layers, flops = [], 0.0
     for name, R, K in PROJ:
@@ -428,8 +430,8 @@ def qlora_layers(torch, rq, dev, ws):
         with torch.no_grad():
             lay.lora_a.copy_((torch.randn(r, K, generator=g, device=dev) / K ** 0.5).to(torch.bfloat16))
             lay.lora_b.copy_((torch.randn(R, r, generator=g, device=dev) * 0.01).to(torch.bfloat16))
-        x = torch.randn(8, 512, K, device=dev).to(torch.bfloat16).requires_grad_(True)
-        dy = torch.randn(8, 512, R, device=dev).to(torch.bfloat16)
+        x = torch.randn(8, 512, K, device=dev).to(xdt).requires_grad_(True)
+        dy = torch.randn(8, 512, R, device=dev).to(xdt)
         layers.append((lay, x, dy))
         flops += 4.0 * M * R * K + 6.0 * M * r * (R + K)
     return layers, flops
@@ -489,6 +491,17 @@ def qlora_step(torch, rq, dev, ws, args):
                     "tflops": round(flops / t / 1e12, 1)}
     out["speedup_fused"] = round(out["composed"]["ms_per_layer_step"]
                                  / out["fused"]["ms_per_layer_step"], 3)
+    # the same fused step with fp32 x and dY (the reference's default
+    # activations, rwkv_metal/model/rwkv7_x070.py:51): y and dX fp32
+    layers32, _ = qlora_layers(torch, rq, dev, ws, torch.float32)
+
+    def fused32():
+        for lay, x, dy in layers32:
+            torch.autograd.grad(lay(x), (x, lay.lora_a, lay.lora_b), dy)
+    t = time_region(torch, fused32, max(5, args.steps // 10), 3)
+    out["fused_fp32_x"] = {"ms_per_layer_step": round(t * 1e3, 3),
+                           "tflops": round(flops / t / 1e12, 1),
+                           "vs_bf16_fused": round(t * 1e3 / out["fused"]["ms_per_layer_step"], 3)}
     return out
 
 
@@ -863,6 +876,11 @@ def main():
                 if M == 4096:
                     tot_flops += fl
                     tot_t += t
+                    # the reference's default fp32 activations (fp32 output)
+                    t32 = time_region(torch, rwkvq.BoundQmm(x.float(), wq, s, b, True, gs,
+                                                            bits).run,
+                                      max(5, args.steps // 2), GEMM_WARMUP)
+                    pre[f"{R}x{K}_M4096_fp32_x"] = round(fl / t32 / 1e12, 1)
             dy = torch.randn(4096, R, device=dev).to(torch.bfloat16)
             tn = time_region(torch, rwkvq.BoundQmm(dy, wq, s, b, False, gs, bits).run,
                              max(5, args.steps // 2), GEMM_WARMUP)

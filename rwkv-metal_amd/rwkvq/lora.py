@@ -51,49 +51,59 @@ class _QLoRAFunction(torch.autograd.Function):
     one launch that computes u = dY B inside the transpose=False GEMM and adds
     scale * u A; dA = scale * u^T x and dB = scale * dY^T z are one
     rq_lora_grads launch.  Other ranks run z and u as rq_lora_down launches
-    and the term with rq_qmm_lora.  The frozen base gets no gradient."""
+    and the term with rq_qmm_lora.  The frozen base gets no gradient.
+
+    fp32 x (the reference's default activations) is rounded to bf16 once, by
+    one cast, and so is fp32 dY: every kernel rounds its fp32 operands to bf16
+    as it stages them anyway (the results are the bits the fp32 inputs give),
+    but the GEMMs re-read their activation tiles once per column tile, so
+    twice the bytes per re-read cost more than the cast.  y and dX stay fp32,
+    and x is saved for the backward in bf16."""
 
     @staticmethod
     def forward(ctx, x2, lora_a, lora_b, base, scale):
         gs, bits = base.group_size, base.bits
-        yz = ops.qlora_fused(x2, base.weight, base.scales, base.biases, lora_a, lora_b, scale,
-                             True, gs, bits)
+        xdt = x2.dtype
+        xb = x2.to(torch.bfloat16) if xdt == torch.float32 else x2
+        yz = ops.qlora_fused(xb, base.weight, base.scales, base.biases, lora_a, lora_b, scale,
+                             True, gs, bits, out_dtype=ops._promote(xdt, base.scales.dtype))
         if yz is not None:
             y, z = yz      # one launch: z = x A^T inside the GEMM
         else:
             z = ops.lora_down(x2, lora_a)
             y = ops.quantized_matmul_lora(x2, base.weight, base.scales, base.biases, z, lora_b,
                                           scale, True, gs, bits)
-        ctx.save_for_backward(x2, z, lora_a, lora_b)
-        ctx.base, ctx.scale = base, scale
+        ctx.save_for_backward(xb, z, lora_a, lora_b)
+        ctx.base, ctx.scale, ctx.xdt = base, scale, xdt
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        x2, z, lora_a, lora_b = ctx.saved_tensors
-        base, scale = ctx.base, ctx.scale
+        xb, z, lora_a, lora_b = ctx.saved_tensors
+        base, scale, xdt = ctx.base, ctx.scale, ctx.xdt
         gs, bits = base.group_size, base.bits
-        dy = dy.contiguous().to(x2.dtype)
+        dy = dy.contiguous().to(xdt)
+        dyb = dy.to(torch.bfloat16) if xdt == torch.float32 else dy
         bt = lora_b.t().contiguous()
         dx = da = db = None
         dxu = None
         if ctx.needs_input_grad[0]:
             at = lora_a.t().contiguous()
-            dxu = ops.qlora_fused(dy, base.weight, base.scales, base.biases, bt, at, scale, False,
-                                  gs, bits)
+            dxu = ops.qlora_fused(dyb, base.weight, base.scales, base.biases, bt, at, scale, False,
+                                  gs, bits, out_dtype=ops._promote(xdt, base.scales.dtype))
             if dxu is not None:
                 dx, u = dxu  # one launch: u = dY B inside the GEMM
             else:
                 u = ops.lora_down(dy, bt)
                 dx = ops.quantized_matmul_lora(dy, base.weight, base.scales, base.biases, u, at,
                                                scale, False, gs, bits)
-            dx = dx.to(x2.dtype)
+            dx = dx.to(xdt)
         else:
-            u = ops.lora_down(dy, bt)
+            u = ops.lora_down(dyb, bt)
         # both adapter gradients in one launch, fp32 accumulation, one rounding
         want_a, want_b = ctx.needs_input_grad[1], ctx.needs_input_grad[2]
-        da, db = ops.lora_grads(x2 if want_a else None, u if want_a else None,
-                                dy if want_b else None, z if want_b else None, scale)
+        da, db = ops.lora_grads(xb if want_a else None, u if want_a else None,
+                                dyb if want_b else None, z if want_b else None, scale)
         if da is not None:
             da = da.to(lora_a.dtype)
         if db is not None:

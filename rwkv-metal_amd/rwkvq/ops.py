@@ -444,13 +444,15 @@ def _qmm_lora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, z: T
 
 def qlora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, a: Tensor,
                 lora: Tensor, scale: float, transpose: bool = True, group_size: int = 64,
-                bits: int = 4):
+                bits: int = 4, out_dtype: torch.dtype | None = None):
     """The QLoRA layer product in one rq_qlora launch, its down-projection
     inside the GEMM: (y, z) with z = x @ a^T [m, rank] (bf16) and
     y = quantized_matmul(x, ...) + scale * z @ lora^T.  Forward: a = lora_a,
     lora = lora_b; dX: a = lora_b^T, lora = lora_a^T (transpose=False), z is
-    then u = dY @ lora_b.  x is 2-D.  None where the fused kernels do not
-    apply (see rq_qlora); no autograd (rwkvq.lora differentiates the layer)."""
+    then u = dY @ lora_b.  x is 2-D.  y is in out_dtype if given (bf16 or
+    fp32), else in MLX's promotion of x and the scales.  None where the fused
+    kernels do not apply (see rq_qlora); no autograd (rwkvq.lora
+    differentiates the layer)."""
     _check_args(group_size, bits)
     w_q = _words(w_q)
     K = _check_packed(w_q, scales, biases, group_size, bits)
@@ -466,7 +468,7 @@ def qlora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, a: Tenso
     x, w_q, scales, a, lora = _ready(x), _ready(w_q), _ready(scales), _ready(a), _ready(lora)
     biases = _ready(biases.to(scales.dtype))
     m = x.shape[0]
-    y = torch.empty(m, n_out, dtype=_promote(x.dtype, scales.dtype), device=x.device)
+    y = torch.empty(m, n_out, dtype=out_dtype or _promote(x.dtype, scales.dtype), device=x.device)
     z = torch.empty(m, rank, dtype=torch.bfloat16, device=x.device)
     if m == 0:
         return y, z
