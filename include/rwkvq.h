@@ -113,6 +113,27 @@ int rq_qmm(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales
            const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
            int group_size, int bits, int transpose, void* y, rq_dtype y_dt, void* stream);
 
+/* rq_qmm(transpose=1) for prefill / training batches whose output tiles are
+ * too few to fill the GPU over a long contraction (the same
+ * mx.quantized_matmul at M = B*T, rwkv_metal/model/rwkv7_x070.py:131-144,
+ * rwkv_metal/lora/finetune.py:115-117): the 64-wide-stage GEMM splits cols
+ * into whole 8-group shares, writes fp32 partial tiles to `workspace` and a
+ * second launch adds them in split order and rounds once into y_dt
+ * (deterministic: the same bits on every call).  The split is chosen from a
+ * cost model of this GPU; where it would not pay (or the 64-wide-stage
+ * conditions of rq_qmm do not hold) this is exactly rq_qmm and the workspace
+ * is not touched.  rq_qmm_splitk_workspace_bytes gives the bytes the call
+ * needs for these sizes (0: none), or a negative rq error code (RQ_EINVAL,
+ * rq_last_error set) for arguments rq_qmm would reject.  The workspace is
+ * device memory, 16-byte aligned, needs no initialisation, and calls that
+ * overlap in time need separate workspaces. */
+int64_t rq_qmm_splitk_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int group_size,
+                                      int bits);
+int rq_qmm_splitk(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
+                  const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
+                  int group_size, int bits, void* y, rq_dtype y_dt, void* workspace,
+                  int64_t workspace_bytes, void* stream);
+
 /* nn.QuantizedEmbedding lookup (upstream MLX; the "emb" target of
  * rwkv_metal/lora/finetune.py:42, looked up at rwkv_metal/model/rwkv7_x070.py:302):
  * out[i, :] = rq_dequantize of table row idx[i], for i < n, in one launch (the

@@ -25,7 +25,10 @@ namespace rq {
                                  const LoraArgs*);                                              \
     hipError_t launch_qmm_n_b##B(const void*, int, const uint32_t*, const void*, const void*,    \
                                  int, int64_t, int64_t, int64_t, int, void*, int, hipStream_t,  \
-                                 const LoraArgs*);
+                                 const LoraArgs*);                                              \
+    hipError_t launch_qmm_t_splitk_b##B(const void*, int, const uint32_t*, const void*,          \
+                                        const void*, int, int64_t, int64_t, int64_t, int, int,   \
+                                        int, float*, hipStream_t);
 #define RQ_DECLARE_TABLE(B)                                                                    \
     hipError_t launch_qmv_table_b##B(const QmvTable&, int, int, int, size_t, hipStream_t);
 RQ_DECLARE_TABLE(2)
@@ -241,6 +244,110 @@ int rq_unpack(const uint32_t* w_q, int64_t rows, int64_t cols, int bits, uint8_t
     if (!codes || !w_q) return fail(RQ_EINVAL, "rq_unpack: NULL pointer");
     if (!aligned16(codes) || !aligned16(w_q)) return fail(RQ_EALIGN, "rq_unpack: pointers must be 16-byte aligned");
     return launch_status(rq::launch_unpack(w_q, rows, cols, bits, codes, (hipStream_t)stream), "rq_unpack");
+}
+
+// Split-K plan for the 64-wide-stage transpose=1 GEMM.  A cost model over
+// measured per-stage times of one MI355X (1.13 us per 64-wide stage of a
+// 256-row tile, 0.875 us of a 128-row one, 0.43 us of a 64 x 96 one; 256
+// CUs, one block each) and the partial tiles' traffic (written and read once
+// at ~5 TB/s, plus ~3 us for the reduction launch): the split that beats the
+// unsplit launcher's own tile choice by 10 % or more, else none.  Splitting
+// pays where few tiles meet a long contraction (config 3's [2560, 10240] at
+// M = 512 / 2048), not where the partials cost as much as the work.
+struct SplitKPlan {
+    int bm = 256, splits = 1;
+};
+
+static bool splitk_applies(rq_dtype x_dt, rq_dtype sb_dt, int64_t m, int64_t cols, int gs,
+                           const void* x, const void* scales, const void* biases) {
+    return m >= 256 && (x_dt == RQ_BF16 || x_dt == RQ_F32) && sb_dt != RQ_F32 && cols % 64 == 0 &&
+           (cols / gs) % 8 == 0 &&
+           (((uintptr_t)x | (uintptr_t)scales | (uintptr_t)biases) & 15) == 0;
+}
+
+static SplitKPlan splitk_plan(int64_t m, int64_t rows, int64_t cols, int gs, int bits) {
+    const int P = gs / 8;                            // 64-wide stages per 8-group period
+    const int64_t nper = cols / (8 * (int64_t)gs);   // periods of the contraction
+    const int bn = (bits == 4 && rows % 160 == 0) ? 160 : 128;
+    const int64_t tn = (rows + bn - 1) / bn;
+    auto cost = [&](int bm, int64_t tiles, int64_t splits, double stage_us) {
+        const int64_t rounds = (tiles * splits + 255) / 256;
+        const int64_t periods = (nper + splits - 1) / splits;
+        double t = (double)rounds * (double)(periods * P) * stage_us;
+        if (splits > 1) t += 2.0 * (double)splits * (double)(m * rows) * 4.0 / 5e6 + 3.0;
+        (void)bm;
+        return t;
+    };
+    // the unsplit launcher's choice (launch_qmm_t_b*)
+    const int64_t t256 = ((m + 255) / 256) * tn, t128 = ((m + 127) / 128) * tn;
+    double plain;
+    if (t256 >= 200) plain = cost(256, t256, 1, 1.13);
+    else if (bits == 4 && t128 < 128) plain = cost(64, ((m + 63) / 64) * ((rows + 95) / 96), 1, 0.43);
+    else plain = cost(128, t128, 1, 0.875);
+    SplitKPlan best;
+    double bt = 0.9 * plain;
+    for (int bm : {256, 128}) {
+        const int64_t tiles = bm == 256 ? t256 : t128;
+        const double stage_us = bm == 256 ? 1.13 : 0.875;
+        for (int64_t s = 2; s <= nper && s <= 32 && tiles * s <= 1024; ++s) {
+            const double t = cost(bm, tiles, s, stage_us);
+            if (t < bt) {
+                bt = t;
+                best.bm = bm;
+                best.splits = (int)s;
+            }
+        }
+    }
+    return best;
+}
+
+int64_t rq_qmm_splitk_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int group_size,
+                                      int bits) {
+    if (int rc = check_common(rows, cols, group_size, bits)) return rc;
+    if (m < 0) return fail(RQ_EINVAL, "rq_qmm_splitk_workspace_bytes: negative m");
+    if (m < 256 || cols % 64 || (cols / group_size) % 8) return 0;
+    const SplitKPlan p = splitk_plan(m, rows, cols, group_size, bits);
+    return p.splits > 1 ? (int64_t)p.splits * m * rows * 4 : 0;
+}
+
+int rq_qmm_splitk(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
+                  const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
+                  int group_size, int bits, void* y, rq_dtype y_dt, void* workspace,
+                  int64_t workspace_bytes, void* stream) {
+    if (int rc = check_common(rows, cols, group_size, bits)) return rc;
+    if (!valid_dt(x_dt) || !valid_dt(sb_dt) || !valid_dt(y_dt)) return fail(RQ_EINVAL, "unsupported dtype");
+    if (m < 0) return fail(RQ_EINVAL, "negative m");
+    SplitKPlan p;
+    if (splitk_applies(x_dt, sb_dt, m, cols, group_size, x, scales, biases))
+        p = splitk_plan(m, rows, cols, group_size, bits);
+    if (p.splits <= 1)  // not worth splitting (or not the 64-wide-stage GEMM): rq_qmm itself
+        return rq_qmm(x, x_dt, w_q, scales, biases, sb_dt, m, rows, cols, group_size, bits, 1, y,
+                      y_dt, stream);
+    if (rows == 0) return ok();
+    if (!y || !x || !w_q || !scales || !biases) return fail(RQ_EINVAL, "rq_qmm_splitk: NULL pointer");
+    if (!aligned16(x) || !aligned16(w_q))
+        return fail(RQ_EALIGN, "rq_qmm_splitk: x and w_q must be 16-byte aligned");
+    const int64_t need = (int64_t)p.splits * m * rows * 4;
+    if (!workspace || workspace_bytes < need)
+        return fail(RQ_EINVAL, "rq_qmm_splitk: workspace has %lld bytes, needs %lld",
+                    (long long)workspace_bytes, (long long)need);
+    if (!aligned16(workspace)) return fail(RQ_EALIGN, "rq_qmm_splitk: workspace must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    float* part = (float*)workspace;
+    hipError_t e;
+    switch (bits) {
+#define RQ_SKB(B)                                                                                 \
+    case B:                                                                                      \
+        e = rq::launch_qmm_t_splitk_b##B(x, x_dt, w_q, scales, biases, sb_dt, m, rows, cols,       \
+                                         group_size, p.bm, p.splits, part, s);                  \
+        break;
+        RQ_SKB(2) RQ_SKB(3) RQ_SKB(4) RQ_SKB(5) RQ_SKB(6) RQ_SKB(8)
+#undef RQ_SKB
+        default: e = hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return launch_status(e, "rq_qmm_splitk");
+    return launch_status(rq::launch_splitk_reduce(part, p.splits, m, rows, y, y_dt, s),
+                         "rq_qmm_splitk");
 }
 
 int rq_qmm(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,

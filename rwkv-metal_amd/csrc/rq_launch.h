@@ -67,6 +67,11 @@ bool qmv_stream_covers(const rq_problem& p, int sb_dt, int64_t m, int gs, int bi
 hipError_t launch_qmv_table(const QmvTable& t, int blocks, int sb_dt, int gs, int bits,
                             size_t lds, hipStream_t stream);
 
+// Split-K GEMM (transpose=1): fp32 partial tiles of `splits` shares of the
+// contraction into part [splits][m][rows], then their in-order sum into y.
+hipError_t launch_splitk_reduce(const float* part, int splits, int64_t m, int64_t rows, void* y,
+                                int y_dt, hipStream_t stream);
+
 // Low-rank term fused into the output stage of the 64-wide-stage GEMMs:
 // y += scale * z . L^T with z [m, rank] and L [n_out, rank], both bf16,
 // rank a multiple of 16 and at most 64.  A launcher given one returns

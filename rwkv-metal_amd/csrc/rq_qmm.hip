@@ -1124,7 +1124,7 @@ template <int BITS, int SDT, int BN, int GSH, int BM, bool FZ = false, bool XF =
 __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, int64_t M, int64_t R, int64_t K, void* __restrict__ y,
-    int y_dt, int tiles_m, int tiles_n, rq::LoraArgs lora) {
+    int y_dt, int tiles_m, int tiles_n, rq::LoraArgs lora, int splits, float* __restrict__ part) {
     static_assert(BM == 256 || BM == 128 || BM == 64, "block rows");
     constexpr int WN = BN / 2;
     constexpr int TM = BM / 32, TN = WN / 16;   // 16x16 MFMA tiles per wave (2x2 waves)
@@ -1141,18 +1141,29 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * BLD];
     __shared__ __attribute__((aligned(16))) float sbf[2][BN * 16];  // fp32 (scale, bias), [row][8 groups]
 
+    // split-K (splits > 1): block tt is tile tt % ntiles over the ks = tt / ntiles-th
+    // share of the contraction, whole 8-group periods each, written as an fp32
+    // partial tile to part[ks] (an XCD's contiguous run of blocks then shares
+    // one K range: the same activation and weight panels in its L2)
     const int ntiles = tiles_m * tiles_n;
-    const int per_xcd = (ntiles + 7) / 8;
-    const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-    if (t >= ntiles) return;
+    const int nblk = ntiles * splits;
+    const int per_xcd = (nblk + 7) / 8;
+    const int tt = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+    if (tt >= nblk) return;
+    const int ks = tt / ntiles, t = tt - ks * ntiles;
     int mt, nt;
     k64_tile(t, tiles_m, tiles_n, mt, nt);
     const int64_t m0 = (int64_t)mt * BM, n0 = (int64_t)nt * BN;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t wpr = (K >> 5) * BITS, G = K >> GSH;
-    const int nst = (int)(K >> 6);
+    // this block's periods [pb, pe) of the contraction (all of them unsplit)
+    const int nper_all = (int)((K >> 6) / P);
+    const int pb = (int)((int64_t)ks * nper_all / splits), pe = (int)((int64_t)(ks + 1) * nper_all / splits);
+    const int nst = splits > 1 ? (pe - pb) * P : (int)(K >> 6);
     const int nper = (nst + P - 1) / P;
+    const int64_t st0 = (int64_t)pb * P;  // first stage
+    if (nst <= 0) return;
 
     constexpr int SW = 2 * BITS;                              // packed words per row per stage
     constexpr int JW = (BITS == 4 && (BN == 160 || BN == 96)) ? 1 : BITS;  // words per dequant job
@@ -1177,9 +1188,9 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
             xoff[i] = (uint32_t)((grow - m0) * K * XChunk<XF>::EB + chunk * 8 * XChunk<XF>::EB);
             xdst[i] = (uint32_t)(row * 128 + ((chunk ^ (row & 7)) * 16));
         }
-        const uint8_t* xbase = (const uint8_t*)x + m0 * K * XChunk<XF>::EB;
+        const uint8_t* xbase = (const uint8_t*)x + (m0 * K + st0 * 64) * XChunk<XF>::EB;
         // dequant jobs: job j = pt + 256 i is part j % JPR (JW words) of tile row j / JPR
-        const uint32_t* wtile = wq + n0 * wpr;
+        const uint32_t* wtile = wq + n0 * wpr + st0 * SW;
         uint32_t coff[NJ], qoff[NJ], soff[NJ], qc0[NJ];
 #pragma unroll
         for (int i = 0; i < NJ; ++i) {
@@ -1194,8 +1205,10 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
         const bool has_row = pt < BN;
         int64_t wrow = n0 + (has_row ? pt : 0);
         wrow = wrow < R ? wrow : R - 1;
-        const uint16_t* srow_p = (const uint16_t*)scales + wrow * G;
-        const uint16_t* brow_p = (const uint16_t*)biases + wrow * G;
+        const int64_t g_base = (st0 * 64) >> GSH;  // the range's first group
+        const uint16_t* srow_p = (const uint16_t*)scales + wrow * G + g_base;
+        const uint16_t* brow_p = (const uint16_t*)biases + wrow * G + g_base;
+        const int g_rem = (int)(G - g_base);  // groups of the row from there
 
         XChunk<XF> xv[D][XL];
         uint32_t cv[D][NJ][JW];
@@ -1223,7 +1236,7 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
         u32x4_t s_nxt = {0u, 0u, 0u, 0u}, b_nxt = s_nxt;
         auto load_sb = [&](int per) {
             int g0 = per * 8;
-            g0 = g0 < (int)G - 8 ? g0 : (int)G - 8;
+            g0 = g0 < g_rem - 8 ? g0 : g_rem - 8;  // past the row: an unused reload
             if (has_row) {
                 s_nxt = *(gv_t)(srow_p + g0);
                 b_nxt = *(gv_t)(brow_p + g0);
@@ -1412,8 +1425,13 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     // strips of 32 rows (BM 256: 8 KB of the free slot per wave) or 16 (BM 128: 4 KB)
     constexpr int SA = BM == 256 ? 2 : 1;
     static_assert(16 * SA * (BN + 16) <= BM * 32, "a wave's staging strip fits its share of a slot");
-    store_wave_tile<TM, TN, SA>(acc, ((nst & 1) ? xs1 : xs0) + wave * (BM * 32), y, y_dt, M, R,
-                                m0 + wm * (BM / 2), n0 + wn * WN, lane);
+    if (splits > 1)  // fp32 partial tile of split ks
+        store_wave_tile<TM, TN, SA>(acc, ((nst & 1) ? xs1 : xs0) + wave * (BM * 32),
+                                    part + (int64_t)ks * M * R, RQ_F32, M, R, m0 + wm * (BM / 2),
+                                    n0 + wn * WN, lane);
+    else
+        store_wave_tile<TM, TN, SA>(acc, ((nst & 1) ? xs1 : xs0) + wave * (BM * 32), y, y_dt, M,
+                                    R, m0 + wm * (BM / 2), n0 + wn * WN, lane);
 }
 
 
@@ -1856,7 +1874,7 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
 #define RQ_FZ_BMX(SD, GSHV, BMV, XFV)                                                             \
     hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, 128, GSHV, BMV, true, XFV>), dim3(blocks),         \
                        dim3(kWsBlock), 0, stream, x, wq, scales, biases, m, rows, cols, y, y_dt,   \
-                       tm, tn, lo)
+                       tm, tn, lo, 1, nullptr)
 #define RQ_FZ_BM(SD, GSHV, BMV) \
     if (xf) { RQ_FZ_BMX(SD, GSHV, BMV, true); } else { RQ_FZ_BMX(SD, GSHV, BMV, false); }
 #define RQ_FZ(SD, GSHV) \
@@ -1897,7 +1915,7 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
 #define RQ_K64_BMX(SD, BNV, GSHV, BMV, XFV)                                                       \
     hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, BNV, GSHV, BMV, false, XFV>), dim3(blocks),        \
                        dim3(kWsBlock), 0, stream, x, wq, scales, biases, m, rows, cols, y, y_dt,   \
-                       tm, tn, lo)
+                       tm, tn, lo, 1, nullptr)
 #define RQ_K64_BM(SD, BNV, GSHV, BMV) \
     if (xf) { RQ_K64_BMX(SD, BNV, GSHV, BMV, true); } else { RQ_K64_BMX(SD, BNV, GSHV, BMV, false); }
 #define RQ_K64(SD, BNV, GSHV)                                                                     \
@@ -1976,6 +1994,48 @@ hipError_t RQ_CAT(launch_qmm_t_b, RQ_BITS)(const void* x, int x_dt, const uint32
     RQ_DISPATCH_DT(x_dt, XD,
         hipLaunchKernelGGL((qmm_t_kernel<RQ_BITS, XD, BM>), grid, dim3(kBlock), 0, stream, x, wq,
                            scales, biases, sb_dt, m, rows, cols, gs_shift, y, y_dt));
+    return hipGetLastError();
+}
+
+// Split-K form of the 64-wide-stage GEMM (transpose=1; the caller checked the
+// k64 conditions): `splits` blocks per bm x bn output tile, each over a whole
+// number of 8-group periods of the contraction, fp32 partial tiles into
+// part[splits][m][rows] (launch_splitk_reduce sums them in split order).
+hipError_t RQ_CAT(launch_qmm_t_splitk_b, RQ_BITS)(const void* x, int x_dt, const uint32_t* wq,
+                                             const void* scales, const void* biases, int sb_dt,
+                                             int64_t m, int64_t rows, int64_t cols, int gs,
+                                             int bm, int splits, float* part, hipStream_t stream) {
+    const int gs_shift = __builtin_ctz(gs);
+    const int bn = (RQ_BITS == 4 && rows % 160 == 0) ? 160 : 128;
+    const int tn = (int)((rows + bn - 1) / bn), tm = (int)((m + bm - 1) / bm);
+    const int blocks = ((tm * tn * splits + 7) / 8) * 8;
+    const bool xf = x_dt == RQ_F32;
+    const LoraArgs lo{nullptr, nullptr, 0, 0.f};
+#define RQ_SK(SD, BNV, GSHV, BMV, XFV)                                                            \
+    hipLaunchKernelGGL((qmm_t_k64<RQ_BITS, SD, BNV, GSHV, BMV, false, XFV>), dim3(blocks),        \
+                       dim3(kWsBlock), 0, stream, x, wq, scales, biases, m, rows, cols, nullptr,  \
+                       (int)RQ_F32, tm, tn, lo, splits, part)
+#define RQ_SK_X(SD, BNV, GSHV, BMV) \
+    if (xf) { RQ_SK(SD, BNV, GSHV, BMV, true); } else { RQ_SK(SD, BNV, GSHV, BMV, false); }
+#define RQ_SK_BM(SD, BNV, GSHV) \
+    if (bm == 256) { RQ_SK_X(SD, BNV, GSHV, 256); } else { RQ_SK_X(SD, BNV, GSHV, 128); }
+#define RQ_SK_GS(SD, BNV)                  \
+    switch (gs_shift) {                    \
+        case 5: RQ_SK_BM(SD, BNV, 5); break; \
+        case 6: RQ_SK_BM(SD, BNV, 6); break; \
+        default: RQ_SK_BM(SD, BNV, 7); break; \
+    }
+#if RQ_BITS == 4
+    if (bn == 160) {
+        if (sb_dt == RQ_BF16) { RQ_SK_GS(RQ_BF16, 160) } else { RQ_SK_GS(RQ_F16, 160) }
+        return hipGetLastError();
+    }
+#endif
+    if (sb_dt == RQ_BF16) { RQ_SK_GS(RQ_BF16, 128) } else { RQ_SK_GS(RQ_F16, 128) }
+#undef RQ_SK_GS
+#undef RQ_SK_BM
+#undef RQ_SK_X
+#undef RQ_SK
     return hipGetLastError();
 }
 

@@ -226,6 +226,38 @@ inline int grid_for(int64_t threads) { return (int)((threads + kBlock - 1) / kBl
 
 }  // namespace
 
+// Split-K reduction: y = sum over splits s = 0, 1, .. of part[s] (fp32 partial
+// products of a split GEMM, [splits][n]), added in split order (the same bits
+// on every run), rounded once into y's dtype.  Four consecutive outputs per
+// thread when vec (rows % 4 == 0), one otherwise.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part,
+                                                            int splits, int64_t n,
+                                                            void* __restrict__ y, int y_dt,
+                                                            bool vec) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (vec) {
+        const int64_t i = 4 * t;
+        if (i >= n) return;
+        f32x4_t acc = *(const f32x4_t*)(part + i);
+        for (int s = 1; s < splits; ++s) acc += *(const f32x4_t*)(part + (int64_t)s * n + i);
+        if (y_dt == RQ_F32) {
+            *(f32x4_t*)((float*)y + i) = acc;
+        } else {
+            typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+            const u32x2_t v = y_dt == RQ_BF16
+                ? u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])}
+                : u32x2_t{f32_to_f16_bits(acc[0]) | (f32_to_f16_bits(acc[1]) << 16),
+                          f32_to_f16_bits(acc[2]) | (f32_to_f16_bits(acc[3]) << 16)};
+            *(u32x2_t*)((uint16_t*)y + i) = v;
+        }
+        return;
+    }
+    if (t >= n) return;
+    float acc = part[t];
+    for (int s = 1; s < splits; ++s) acc += part[(int64_t)s * n + t];
+    store_dt(y, y_dt, t, acc);
+}
+
 namespace rq {
 
 hipError_t launch_quantize(const void* w, int w_dt, int64_t rows, int64_t cols, int gs,
@@ -284,6 +316,18 @@ hipError_t launch_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bit
     RQ_DISPATCH_BITS(bits, B,
         hipLaunchKernelGGL((unpack_kernel<B>), dim3(grid_for(threads)), dim3(kBlock), 0, stream,
                            wq, rows, cols, codes));
+    return hipGetLastError();
+}
+
+hipError_t launch_splitk_reduce(const float* part, int splits, int64_t m, int64_t rows, void* y,
+                                int y_dt, hipStream_t stream) {
+    const int64_t n = m * rows;
+    if (n == 0) return hipSuccess;
+    const bool vec = rows % 4 == 0;
+    const int64_t threads = vec ? n / 4 : n;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    hipLaunchKernelGGL(splitk_reduce_kernel, grid, dim3(256), 0, stream, part, splits, n, y, y_dt,
+                       vec);
     return hipGetLastError();
 }
 

@@ -51,6 +51,9 @@ SIGNATURES = {
     "rq_dequantize": ([_vp, _vp, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _i32, _vp], _i32),
     "rq_qmm": ([_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _i32, _vp],
                _i32),
+    "rq_qmm_splitk_workspace_bytes": ([_i64, _i64, _i64, _i32, _i32], _i64),
+    "rq_qmm_splitk": ([_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _i32,
+                       _vp, _i64, _vp], _i32),
     "rq_qmm_lora": ([_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _vp,
                      _i64, ctypes.c_float, _vp, _i32, _vp], _i32),
     "rq_qlora": ([_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _vp,

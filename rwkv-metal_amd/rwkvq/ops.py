@@ -269,12 +269,44 @@ def _qmm_op(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, transpose: b
     y = torch.empty(*x.shape[:-1], n_out, dtype=out_dtype, device=x.device)
     if y.numel() == 0:
         return y
+    L = lib()
     with _DeviceGuard(x.device):
-        rc = lib().rq_qmm(_ptr(x), DTYPE_CODE[x.dtype], _ptr(w_q), _ptr(scales), _ptr(biases),
+        stream = _stream(x)
+        # prefill batches with few output tiles over a long contraction split it
+        # (rq_qmm_splitk, a per-stream workspace); everything else is rq_qmm
+        nbytes = L.rq_qmm_splitk_workspace_bytes(m, R, K, group_size, bits) if (
+            transpose and m >= 256) else 0
+        if nbytes > 0:
+            ws = _splitk_workspace(x.device, stream, nbytes)
+            rc = L.rq_qmm_splitk(_ptr(x), DTYPE_CODE[x.dtype], _ptr(w_q), _ptr(scales),
+                                 _ptr(biases), DTYPE_CODE[scales.dtype], m, R, K, group_size,
+                                 bits, _ptr(y), DTYPE_CODE[out_dtype], ws.data_ptr(), ws.numel(),
+                                 stream)
+        else:
+            rc = L.rq_qmm(_ptr(x), DTYPE_CODE[x.dtype], _ptr(w_q), _ptr(scales), _ptr(biases),
                           DTYPE_CODE[scales.dtype], m, R, K, group_size, bits,
-                          1 if transpose else 0, _ptr(y), DTYPE_CODE[out_dtype], _stream(x))
+                          1 if transpose else 0, _ptr(y), DTYPE_CODE[out_dtype], stream)
     check(rc, "quantized_matmul")
     return y
+
+
+_splitk_workspaces: "collections.OrderedDict" = collections.OrderedDict()
+
+
+def _splitk_workspace(device: torch.device, stream: int, nbytes: int) -> Tensor:
+    """The split-K GEMM's partial tiles, one buffer per (device, stream) and at
+    most _GRAD_WORKSPACES_MAX of them (least recently used out), as for the
+    gradient workspaces; it needs no initialisation.  Allocated while its
+    stream is current, so torch's caching allocator reuses a dropped one only
+    on that stream, after the work queued there."""
+    key = (device.index, stream)
+    ws = _splitk_workspaces.pop(key, None)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    _splitk_workspaces[key] = ws
+    while len(_splitk_workspaces) > _GRAD_WORKSPACES_MAX:
+        _splitk_workspaces.popitem(last=False)
+    return ws
 
 
 @_qmm_op.register_fake
@@ -513,7 +545,8 @@ def quantized_matmul_lora(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor
 
 class BoundQmm:
     """One validated quantized_matmul (either transpose) with a fixed output
-    buffer: run() is a single rq_qmm call on the current stream, with no
+    buffer: run() is a single rq_qmm call (rq_qmm_splitk, with a workspace of
+    its own, where the split-K plan applies) on the current stream, with no
     per-call validation, allocation or custom-op dispatch.  For serving or
     training loops that repeat the same product on the same buffers (and for
     timing the kernel rather than the Python dispatch).  Same semantics and
@@ -554,6 +587,13 @@ class BoundQmm:
                       1 if transpose else 0, y.data_ptr(), DTYPE_CODE[ydt])
         self._empty = y.numel() == 0
         self._guard, self._fn = _DeviceGuard(self.device), lib().rq_qmm
+        nbytes = lib().rq_qmm_splitk_workspace_bytes(m, R, K, group_size, bits) if (
+            transpose and m >= 256) else 0
+        if nbytes > 0:   # its own partial-tile workspace, held with the bound buffers
+            self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+            a = self._args
+            self._args = (*a[:11], a[12], a[13], self.workspace.data_ptr(), nbytes)
+            self._fn = lib().rq_qmm_splitk
 
     def run(self) -> Tensor:
         if not self._empty:

@@ -29,7 +29,8 @@ def test_header_declares_the_expected_surface():
         "rq_pack", "rq_unpack", "rq_qmm_grouped", "rq_grouped_plan_table_bytes",
         "rq_grouped_plan_init", "rq_grouped_plan_run", "rq_embedding", "rq_sb6_dequantize",
         "rq_sb6_to_affine", "rq_qmm_lora", "rq_lora_down", "rq_lora_grads_workspace_bytes",
-        "rq_lora_grads", "rq_lora_grads_f32", "rq_lora_grads_noalloc", "rq_qlora"])
+        "rq_lora_grads", "rq_lora_grads_f32", "rq_lora_grads_noalloc", "rq_qlora",
+        "rq_qmm_splitk_workspace_bytes", "rq_qmm_splitk"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -191,3 +192,27 @@ def test_lora_grads_noalloc_rejections_before_any_device_work(L):
     assert "exceeds" in _err(L)
     assert L.rq_lora_grads_noalloc(p, p, p, p, 4096, 2048, 2048, 20, 1.0, p, p, None) == -1
     assert L.rq_lora_grads_noalloc(p, p + 4, p, p, 4096, 2048, 2048, 16, 1.0, p, p, None) == -2
+
+
+def test_qmm_splitk_plan_and_rejections(L):
+    """The split-K plan (host only): config 3's long contraction at M = 512 and
+    2048 splits; the K = 2560 shapes, M = 4096 and small M do not (their
+    workspace size is 0 and rq_qmm_splitk is then rq_qmm)."""
+    nb = L.rq_qmm_splitk_workspace_bytes
+    for m in (512, 2048):
+        b = nb(m, 2560, 10240, 64, 4)
+        assert b > 0 and b % (m * 2560 * 4) == 0, (m, b)
+        assert 2 <= b // (m * 2560 * 4) <= 32
+    for m, r, k in [(4096, 2560, 2560), (4096, 10240, 2560), (4096, 2560, 10240),
+                    (2048, 2560, 2560), (512, 2560, 2560), (100, 2560, 10240)]:
+        assert nb(m, r, k, 64, 4) == 0, (m, r, k)
+    assert nb(512, 2560, 10240, 48, 4) == -1 and "group_size" in _err(L)
+    assert nb(512, 2560, 10240, 64, 7) == -1
+    assert nb(-1, 2560, 10240, 64, 4) == -1
+    p = 0x1000
+    # a split problem without enough workspace is refused before any launch
+    assert L.rq_qmm_splitk(p, 0, p, p, p, 0, 512, 2560, 10240, 64, 4, p, 0, p, 64, None) == -1
+    assert "workspace" in _err(L)
+    need = nb(512, 2560, 10240, 64, 4)
+    assert L.rq_qmm_splitk(p, 0, p, p, p, 0, 512, 2560, 10240, 64, 4, p, 0, p + 8, need,
+                           None) == -2

@@ -554,6 +554,66 @@ def test_qmm_t_k64_256_row_tiles_oracle(O, rq, dev):
                                     weights="exact"), what="k64 256-row oracle")
 
 
+# split-K prefill (rq_qmm_splitk, routed by quantized_matmul where its plan
+# splits): config 3's long contraction at M = 512 / 2048, a partial row tile
+# with fp32 x, 3- and 8-bit codes, group sizes 32 / 128, f16 scales
+SPLITK_CASES = [
+    (512, 2560, 10240, 4, 64, torch.bfloat16, torch.bfloat16),
+    (2048, 2560, 10240, 4, 64, torch.bfloat16, torch.bfloat16),
+    (600, 2560, 10240, 4, 64, torch.bfloat16, torch.float32),
+    (512, 2048, 16384, 3, 64, torch.bfloat16, torch.bfloat16),
+    (512, 2048, 8192, 8, 32, torch.float16, torch.bfloat16),
+    (512, 2560, 10240, 4, 128, torch.bfloat16, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("M,R,K,bits,gs,sdt,xdt", SPLITK_CASES)
+def test_qmm_splitk(rq, dev, M, R, K, bits, gs, sdt, xdt):
+    """Every output element against an fp32 dense product; the split path is
+    the one that runs, is deterministic (two calls, the same bits) and agrees
+    with the unsplit rq_qmm within the bar."""
+    from rwkvq._lib import DTYPE_CODE, lib
+    from rwkvq.ops import _stream_on
+    L = lib()
+    nb = L.rq_qmm_splitk_workspace_bytes(M, R, K, gs, bits)
+    assert nb > 0, "the plan must split this problem"
+    say(f"splitk M={M} R={R} K={K} b={bits} gs={gs} s={sdt} x={xdt} ({nb // (M * R * 4)} splits)")
+    wq, s, b = rq.quantize(weights(R, K, 96_000 + R + K + bits, sdt).to(dev), gs, bits)
+    x = acts(M, K, 97_000 + M + bits, xdt).to(dev)
+    y = rq.quantized_matmul(x, wq, s, b, True, gs, bits)
+    y2 = rq.quantized_matmul(x, wq, s, b, True, gs, bits)
+    assert bits_equal(y, y2), "split-K is not deterministic"
+    ref = _gpu_dense_ref(rq, x, wq, s, b, gs, bits, True)
+    rel_check(y, ref, what=f"splitk M{M} [{R},{K}] b{bits}")
+    err = (y.float() - ref).abs()
+    assert bool((err <= 1e-2 * ref.abs().max() + 1e-3).all())
+    # the unsplit kernel on the same inputs
+    yp = torch.empty_like(y)
+    rc = L.rq_qmm(x.data_ptr(), DTYPE_CODE[x.dtype], wq.data_ptr(), s.data_ptr(), b.data_ptr(),
+                  DTYPE_CODE[s.dtype], M, R, K, gs, bits, 1, yp.data_ptr(), DTYPE_CODE[yp.dtype],
+                  _stream_on(dev))
+    assert rc == 0, L.rq_last_error().decode()
+    rel_check(y, yp.float(), what="splitk vs unsplit")
+    # BoundQmm takes the same path with its own workspace
+    bound = rq.BoundQmm(x, wq, s, b, True, gs, bits)
+    assert bits_equal(bound.run(), y)
+
+
+def test_qmm_splitk_oracle(O, rq, dev):
+    """A split problem against the CPU oracle itself (M = 300: a partial row
+    tile; K = 8192 in 16 shares)."""
+    from rwkvq._lib import lib
+    M, R, K = 300, 1280, 8192
+    assert lib().rq_qmm_splitk_workspace_bytes(M, R, K, 64, 4) > 0
+    w = weights(R, K, 98)
+    wq, s, b = O.quantize(w, 64, 4)
+    x = acts(M, K, 99)
+    say("splitk vs oracle")
+    y = rq.quantized_matmul(x.to(dev), wq.to(dev), s.to(dev), b.to(dev), True, 64, 4)
+    rel_check(y, O.quantized_matmul(x, wq, s, b, True, 64, 4, out_dtype=torch.float32,
+                                    weights="exact"), what="splitk oracle")
+
+
 @pytest.mark.parametrize("R", [130, 77, 64])
 def test_qmm_n_unaligned_rows(O, rq, dev, R):
     """Row counts whose activation rows are not 16-byte multiples (scalar loads)."""
