@@ -328,8 +328,9 @@ def config1(torch, rq, dev, args):
     n = max(20, args.steps)
     out["quantize_us"] = round(time_region(torch, lambda: rq.quantize(w, gs, bits), n, 10) * 1e6, 2)
     out["dequantize_us"] = round(time_region(torch, lambda: rq.dequantize(wq, s, b, gs, bits), n, 10) * 1e6, 2)
-    # the same calls replayed from a HIP graph: the GPU side without the
-    # Python op dispatch that bounds the single calls above
+    # the same calls replayed from a HIP graph: the GPU side without the host
+    # work (argument checks, output allocation, the launch) that bounds the
+    # single calls above
     for name, fn in (("quantize", lambda: rq.quantize(w, gs, bits)),
                      ("dequantize", lambda: rq.dequantize(wq, s, b, gs, bits))):
         reps = 20

@@ -126,10 +126,31 @@ def _ptr(t: Tensor) -> int:
     return t.data_ptr() if t.numel() else 0
 
 
+_dispatch_modes = torch._C._len_torch_dispatch_stack
+_function_modes = torch._C._len_torch_function_stack
+_functorch_active = torch._C._are_functorch_transforms_active
+
+
+def _direct(*ts: Tensor) -> bool:
+    """True when a call may run an op's body without the torch.library
+    dispatcher: plain GPU tensors, no autograd to record, no tracing, no
+    dispatch or function mode and no functorch transform.  Such a call does
+    exactly what the registered op would do and skips about 13 us of host
+    dispatch, which is longer than the small launches take on the GPU.
+    Anything else (torch.compile, meta and fake tensors, autograd, CPU
+    tensors, which the op refuses) goes through the registered op."""
+    if _dispatch_modes() or _function_modes() or _functorch_active():
+        return False
+    grad = torch.is_grad_enabled()
+    for t in ts:
+        if type(t) is not Tensor or not t.is_cuda or (grad and t.requires_grad):
+            return False
+    return not torch.compiler.is_compiling()
+
+
 # --------------------------------------------------------------- quantize
 
-@torch.library.custom_op("rwkvq::quantize", mutates_args=())
-def _quantize_op(w: Tensor, group_size: int, bits: int) -> Tuple[Tensor, Tensor, Tensor]:
+def _quantize_impl(w: Tensor, group_size: int, bits: int) -> Tuple[Tensor, Tensor, Tensor]:
     _on_gpu(w)
     w = _ready(w)
     K = w.shape[-1]
@@ -143,6 +164,9 @@ def _quantize_op(w: Tensor, group_size: int, bits: int) -> Tuple[Tensor, Tensor,
                                _ptr(s), _ptr(b), _stream(w))
     check(rc, "quantize")
     return wq, s, b
+
+
+_quantize_op = torch.library.custom_op("rwkvq::quantize", _quantize_impl, mutates_args=())
 
 
 @_quantize_op.register_fake
@@ -162,13 +186,14 @@ def quantize(w: Tensor, group_size: int = 64, bits: int = 4) -> Tuple[Tensor, Te
     if w.shape[-1] % group_size:
         raise ValueError(f"the last dimension ({w.shape[-1]}) must be divisible by "
                          f"group_size {group_size}")
+    if _direct(w):
+        return _quantize_impl(w, group_size, bits)
     return _quantize_op(w, group_size, bits)
 
 
 # ------------------------------------------------------------- dequantize
 
-@torch.library.custom_op("rwkvq::dequantize", mutates_args=())
-def _dequantize_op(w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int,
+def _dequantize_impl(w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int,
                    bits: int) -> Tensor:
     _on_gpu(w_q, scales, biases)
     w_q, scales, biases = _ready(w_q), _ready(scales), _ready(biases.to(scales.dtype))
@@ -181,6 +206,10 @@ def _dequantize_op(w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int,
                                  _stream(w_q))
     check(rc, "dequantize")
     return out
+
+
+_dequantize_op = torch.library.custom_op("rwkvq::dequantize", _dequantize_impl,
+                                         mutates_args=())
 
 
 @_dequantize_op.register_fake
@@ -209,13 +238,14 @@ def dequantize(w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int = 64
     w_q = _words(w_q)
     _float(scales, "scales")
     _check_packed(w_q, scales, biases, group_size, bits)
+    if _direct(w_q, scales, biases):
+        return _dequantize_impl(w_q, scales, biases, group_size, bits)
     return _dequantize_op(w_q, scales, biases, group_size, bits)
 
 
 # ------------------------------------------------------------ embedding
 
-@torch.library.custom_op("rwkvq::quantized_embedding", mutates_args=())
-def _embedding_op(idx: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int,
+def _embedding_impl(idx: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, group_size: int,
                   bits: int) -> Tensor:
     _on_gpu(idx, w_q, scales, biases)
     flat = _ready(idx.reshape(-1).to(torch.int64))
@@ -230,6 +260,10 @@ def _embedding_op(idx: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, grou
                                 DTYPE_CODE[out.dtype], _stream(w_q))
     check(rc, "quantized_embedding")
     return out
+
+
+_embedding_op = torch.library.custom_op("rwkvq::quantized_embedding", _embedding_impl,
+                                        mutates_args=())
 
 
 @_embedding_op.register_fake
@@ -250,13 +284,14 @@ def quantized_embedding(idx: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor
     _check_packed(w_q, scales, biases, group_size, bits)
     if idx.dtype not in (torch.int64, torch.int32, torch.int16, torch.uint8):
         raise ValueError(f"indices must be an integer tensor (got {idx.dtype})")
+    if _direct(idx, w_q, scales, biases):
+        return _embedding_impl(idx, w_q, scales, biases, group_size, bits)
     return _embedding_op(idx, w_q, scales, biases, group_size, bits)
 
 
 # ------------------------------------------------------- quantized_matmul
 
-@torch.library.custom_op("rwkvq::quantized_matmul", mutates_args=())
-def _qmm_op(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, transpose: bool,
+def _qmm_impl(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, transpose: bool,
             group_size: int, bits: int) -> Tensor:
     _on_gpu(x, w_q, scales, biases)
     x, w_q, scales = _ready(x), _ready(w_q), _ready(scales)
@@ -309,6 +344,10 @@ def _splitk_workspace(device: torch.device, stream: int, nbytes: int) -> Tensor:
     return ws
 
 
+_qmm_op = torch.library.custom_op("rwkvq::quantized_matmul", _qmm_impl,
+                                  mutates_args=())
+
+
 @_qmm_op.register_fake
 def _(x, w_q, scales, biases, transpose, group_size, bits):
     R = w_q.shape[0]
@@ -350,6 +389,8 @@ def quantized_matmul(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor,
     if x.shape[-1] != n_in:
         raise ValueError(f"x has inner dimension {x.shape[-1]} but the quantized weight expects "
                          f"{n_in} (transpose={transpose})")
+    if _direct(x, w_q, scales, biases):
+        return _qmm_impl(x, w_q, scales, biases, bool(transpose), group_size, bits)
     return _qmm_op(x, w_q, scales, biases, bool(transpose), group_size, bits)
 
 
@@ -697,8 +738,7 @@ def grouped_qmv(xs: Sequence[Tensor], ws: Sequence[Tuple[Tensor, Tensor, Tensor]
 
 # ---------------------------------------------------------- pack / unpack
 
-@torch.library.custom_op("rwkvq::pack_codes", mutates_args=())
-def _pack_op(codes: Tensor, bits: int) -> Tensor:
+def _pack_impl(codes: Tensor, bits: int) -> Tensor:
     _on_gpu(codes)
     codes = _ready(codes)
     K = codes.shape[-1]
@@ -710,13 +750,15 @@ def _pack_op(codes: Tensor, bits: int) -> Tensor:
     return wq
 
 
+_pack_op = torch.library.custom_op("rwkvq::pack_codes", _pack_impl, mutates_args=())
+
+
 @_pack_op.register_fake
 def _(codes, bits):
     return codes.new_empty(*codes.shape[:-1], codes.shape[-1] * bits // 32, dtype=torch.int32)
 
 
-@torch.library.custom_op("rwkvq::unpack_codes", mutates_args=())
-def _unpack_op(w_q: Tensor, bits: int) -> Tensor:
+def _unpack_impl(w_q: Tensor, bits: int) -> Tensor:
     _on_gpu(w_q)
     w_q = _ready(w_q)
     K = w_q.shape[-1] * 32 // bits
@@ -726,6 +768,9 @@ def _unpack_op(w_q: Tensor, bits: int) -> Tensor:
         rc = lib().rq_unpack(_ptr(w_q), R, K, bits, _ptr(codes), _stream(w_q))
     check(rc, "unpack_codes")
     return codes
+
+
+_unpack_op = torch.library.custom_op("rwkvq::unpack_codes", _unpack_impl, mutates_args=())
 
 
 @_unpack_op.register_fake
@@ -741,6 +786,8 @@ def pack_codes(codes: Tensor, bits: int) -> Tensor:
         raise ValueError("codes must be uint8")
     if codes.shape[-1] % 32:
         raise ValueError("the code row length must be a multiple of 32")
+    if _direct(codes):
+        return _pack_impl(codes, bits)
     return _pack_op(codes, bits)
 
 
@@ -751,4 +798,6 @@ def unpack_codes(w_q: Tensor, bits: int) -> Tensor:
     w_q = _words(w_q)
     if w_q.shape[-1] % bits:
         raise ValueError("packed width must be a multiple of bits words")
+    if _direct(w_q):
+        return _unpack_impl(w_q, bits)
     return _unpack_op(w_q, bits)

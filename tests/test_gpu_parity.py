@@ -1027,6 +1027,38 @@ def test_autograd_dx_is_transposed_qmm(O, rq, dev):
     rel_check(x.grad, ref, what="dX")
 
 
+def test_direct_calls_equal_registered_ops(rq, dev):
+    """Eager calls on plain GPU tensors without autograd skip the torch.library
+    dispatcher; they must give what the registered ops give, bit for bit, and
+    calls that need the dispatcher (autograd, no_grad aside) must still take it."""
+    from rwkvq import ops
+    R, K, M = 192, 512, 5
+    w = weights(R, K, 46).to(dev)
+    x = acts(M, K, 46).to(dev)
+    assert ops._direct(w, x)
+    say("direct vs registered ops")
+    got = rq.quantize(w, 64, 4)
+    want = torch.ops.rwkvq.quantize(w, 64, 4)
+    assert all(bits_equal(a, b) for a, b in zip(got, want))
+    wq, s, b = got
+    assert bits_equal(rq.dequantize(wq, s, b, 64, 4), torch.ops.rwkvq.dequantize(wq, s, b, 64, 4))
+    for tr, xx in ((True, x), (False, acts(M, R, 47).to(dev))):
+        assert bits_equal(rq.quantized_matmul(xx, wq, s, b, tr, 64, 4),
+                          torch.ops.rwkvq.quantized_matmul(xx, wq, s, b, tr, 64, 4))
+    idx = torch.tensor([[3, 0], [191, 7]], device=dev)
+    assert bits_equal(rq.quantized_embedding(idx, wq, s, b, 64, 4),
+                      torch.ops.rwkvq.quantized_embedding(idx, wq, s, b, 64, 4))
+    codes = rq.unpack_codes(wq, 4)
+    assert bits_equal(codes, torch.ops.rwkvq.unpack_codes(wq, 4))
+    assert bits_equal(rq.pack_codes(codes, 4), torch.ops.rwkvq.pack_codes(codes, 4))
+    xg = x.clone().requires_grad_(True)
+    assert not ops._direct(xg, wq)
+    with torch.no_grad():
+        assert ops._direct(xg, wq)
+    y = rq.quantized_matmul(xg, wq, s, b, True, 64, 4)
+    assert y.grad_fn is not None and bits_equal(y, rq.quantized_matmul(x, wq, s, b, True, 64, 4))
+
+
 @pytest.mark.parametrize("M", [96, 320])
 def test_qlora_layer_forward_backward(rq, dev, M):
     """benchmark config 4 math at a reduced shape: y = qmm(x,Wq) + (a/r)(xA^T)B^T;
