@@ -25,6 +25,7 @@
  *                     output stage
  *   rq_qlora       <- the same layer with x . A^T (or dY . B) computed inside the GEMM:
  *                     forward and dX each one launch
+ *   rq_qlora_dx    <- its dX from the adapters as stored (no transposed copies)
  *   rq_lora_down   <- its x . A^T and the backward's dY . B (the same lines)
  *   rq_lora_grads  <- the backward's adapter gradients u^T x and dY^T z (the same
  *                     layer under nn.value_and_grad, rwkv_metal/lora/finetune.py:141)
@@ -280,6 +281,23 @@ int rq_qlora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scal
              const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
              int group_size, int bits, int transpose, const void* a, const void* lora,
              int64_t rank, float scale, void* z_out, void* y, rq_dtype y_dt, void* stream);
+
+/* The QLoRA layer's dX in ONE launch from the adapters as the layer stores
+ * them (LoRALinear.lora_a [rank, cols] and lora_b [rows, rank] bf16,
+ * rwkv_metal/lora/lora.py:55-56, differentiated as in
+ * rwkv_metal/lora/finetune.py:141): u = dy . lora_b is accumulated by the
+ * transposed GEMM from the dy tiles it already holds, then
+ *   dx = rq_qmm(dy, ..., transpose=0) + scale * u . lora_a
+ * and u is stored to u_out [m, rank] bf16 (if not NULL) for the adapter
+ * gradients.  The same product as rq_qlora with transpose=0, a = lora_b^T
+ * and lora = lora_a^T, bit for bit, without the two transposed copies.
+ * Covers what rq_qlora's dX covers (rank 16, 4- or 8-bit codes); other
+ * problems return RQ_EUNSUPPORTED.  dy, w_q and u_out 16-byte aligned,
+ * lora_a and lora_b 2-byte aligned. */
+int rq_qlora_dx(const void* dy, rq_dtype dy_dt, const uint32_t* w_q, const void* scales,
+                const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
+                int group_size, int bits, const void* lora_a, const void* lora_b, int64_t rank,
+                float scale, void* u_out, void* dx, rq_dtype dx_dt, void* stream);
 
 /* Pack codes uint8[rows, cols] (values < 2^bits) into the MLX bitstream
  * w_q uint32[rows, cols*bits/32].  cols must be a multiple of 32. */

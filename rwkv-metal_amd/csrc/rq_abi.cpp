@@ -539,6 +539,42 @@ int rq_qlora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scal
     return launch_status(e, "rq_qlora");
 }
 
+int rq_qlora_dx(const void* dy, rq_dtype dy_dt, const uint32_t* w_q, const void* scales,
+                const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
+                int group_size, int bits, const void* lora_a, const void* lora_b, int64_t rank,
+                float scale, void* u_out, void* dx, rq_dtype dx_dt, void* stream) {
+    if (int rc = check_common(rows, cols, group_size, bits)) return rc;
+    if (!valid_dt(dy_dt) || !valid_dt(sb_dt) || !valid_dt(dx_dt)) return fail(RQ_EINVAL, "unsupported dtype");
+    if (m < 0) return fail(RQ_EINVAL, "negative m");
+    if (rank < 16 || rank > 64 || rank % 16)
+        return fail(RQ_EINVAL, "rq_qlora_dx: rank must be 16, 32, 48 or 64 (got %lld)", (long long)rank);
+    if (m == 0 || cols == 0) return ok();
+    if (rows == 0) return fail(RQ_EINVAL, "rq_qlora_dx: empty contraction is not supported");
+    if (!dy || !w_q || !scales || !biases || !dx || !lora_a || !lora_b)
+        return fail(RQ_EINVAL, "rq_qlora_dx: NULL pointer");
+    if (!aligned16(dy) || !aligned16(w_q) || !aligned16(u_out))
+        return fail(RQ_EALIGN, "rq_qlora_dx: dy, w_q and u_out must be 16-byte aligned");
+    if (((uintptr_t)lora_a | (uintptr_t)lora_b) & 1)
+        return fail(RQ_EALIGN, "rq_qlora_dx: lora_a and lora_b must be 2-byte aligned");
+    // u = dY . B from B [rows, rank] as stored; the term scale * u . A from A
+    // [rank, cols] as stored
+    rq::LoraArgs lo{nullptr, lora_a, (int)rank, scale};
+    lo.a = lora_b;
+    lo.z_out = u_out;
+    lo.a_ld = rows;
+    lo.stored = true;
+    lo.l_ld = cols;
+    const hipError_t e = rq::launch_qmm(0, dy, dy_dt, w_q, scales, biases, sb_dt, m, rows, cols,
+                                        group_size, bits, dx, dx_dt, (hipStream_t)stream, &lo);
+    if (e == hipErrorNotSupported)
+        return fail(RQ_EUNSUPPORTED,
+                    "rq_qlora_dx: the in-kernel down-projection covers rank 16 with 4- or 8-bit "
+                    "codes on the 64-wide-stage transposed GEMM (bf16 or fp32 dy, m >= 256, "
+                    "16-bit 16-byte aligned scales, rows %% 64 == 0, cols %% 128 == 0); use "
+                    "rq_lora_down and rq_qmm_lora");
+    return launch_status(e, "rq_qlora_dx");
+}
+
 static int check_grouped(const char* what, const rq_problem* problems, int n, rq_dtype x_dt,
                          rq_dtype sb_dt, rq_dtype y_dt, int64_t m, int group_size, int bits) {
     if (n < 0 || (n > 0 && !problems)) return fail(RQ_EINVAL, "%s: bad problem list", what);

@@ -88,6 +88,13 @@ struct LoraArgs {
     const void* a = nullptr;
     void* z_out = nullptr;
     int64_t a_ld = 0;
+    // The transposed GEMM's down-projection from the adapters as a LoRA
+    // layer stores them (transpose=0, rank 16): `a` is then B [a_ld, 16]
+    // (element (j, c) of a at a[c * 16 + j]) and `l` is A [16, l_ld]
+    // (element (n, j) of L at l[j * l_ld + n]), so that dX needs no
+    // transposed copies of the adapters.
+    bool stored = false;
+    int64_t l_ld = 0;
 };
 
 // Low-rank down-projection z[m, rank] = x[m, k] . a[rank, k]^T, bf16 (rank

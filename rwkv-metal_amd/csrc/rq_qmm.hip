@@ -21,6 +21,8 @@
 //  * qmm_n: the contraction runs over the weight rows, so the B tile is
 //    stored transposed ([k][r]); a thread dequantizes the same run of two
 //    adjacent rows and writes (row, row+1) pairs as one dword per k.
+#include <type_traits>
+
 #include "rq_common.h"
 #include "rq_launch.h"
 
@@ -1009,6 +1011,16 @@ RQ_DEV void lora_epilogue(f32x4_t (&acc)[TM][TN], const rq::LoraArgs& lo, int64_
     }
 }
 
+// Eight bf16 values p[0], p[stride], .., p[7 * stride] as one MFMA operand
+// fragment (a column of a row-major matrix: 2-byte loads).
+RQ_DEV u32x4_t gather8_bf16(const uint16_t* p, int64_t stride) {
+    u32x4_t v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        v[q] = (uint32_t)p[2 * q * stride] | ((uint32_t)p[(2 * q + 1) * stride] << 16);
+    return v;
+}
+
 // The fused QLoRA layer's down-projection, computed in the GEMM (rank 16).
 // Each MFMA wave of a (wm) pair accumulated z over the k-steps h == wn of
 // every stage (accz: lane (lg, lr) holds row lr of 16-row tile a, ranks
@@ -1017,13 +1029,26 @@ RQ_DEV void lora_epilogue(f32x4_t (&acc)[TM][TN], const rq::LoraArgs& lo, int64_
 // fp32 partials are exchanged through one slot (zx: [4 waves][rows][16]),
 // summed in the same order by both waves, rounded once to bf16, stored to
 // z_out by the column-tile-0 blocks (one wave of the pair), and the term
-// scale * z . L^T is added to acc (L [ncols, 16] bf16 from global memory).
+// scale * z . L^T is added to acc (L [ncols, 16] bf16 from global memory,
+// or its transpose [16, l_ld] when lo.stored).
 template <int TM, int TN>
 RQ_DEV void fused_lora_tail(f32x4_t (&acc)[TM][TN], const f32x4_t (&accz)[TM], float* zx, int wm,
                             int wn, int lane, const rq::LoraArgs& lo, bool write_z, int64_t nrows,
                             int64_t ncols, int64_t r0, int64_t c0) {
     const int lg = lane >> 4, lr = lane & 15;
     constexpr int ROWS = TM * 16;
+    // L's fragments first: their global-memory latency overlaps the exchange
+    const uint16_t* l = (const uint16_t*)lo.l;
+    bf16x8_t lf[TN];
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+        const int64_t n = c0 + b * 16 + lr;
+        u32x4_t v = {0u, 0u, 0u, 0u};
+        if (lg < 2 && n < ncols)
+            v = lo.stored ? gather8_bf16(l + 8 * lg * lo.l_ld + n, lo.l_ld)
+                          : *(const u32x4_t*)(l + n * 16 + 8 * lg);
+        lf[b] = __builtin_bit_cast(bf16x8_t, v);
+    }
 #pragma unroll
     for (int a = 0; a < TM; ++a)
         *(f32x4_t*)(zx + ((wm * 2 + wn) * ROWS + a * 16 + lr) * 16 + 4 * lg) = accz[a];
@@ -1048,15 +1073,6 @@ RQ_DEV void fused_lora_tail(f32x4_t (&acc)[TM][TN], const f32x4_t (&accz)[TM], f
             if (write_z && m < nrows) *(u32x4_t*)((uint16_t*)lo.z_out + m * 16 + 8 * lg) = v;
         }
         zf[a] = __builtin_bit_cast(bf16x8_t, v);
-    }
-    const uint16_t* l = (const uint16_t*)lo.l;
-    bf16x8_t lf[TN];
-#pragma unroll
-    for (int b = 0; b < TN; ++b) {
-        const int64_t n = c0 + b * 16 + lr;
-        u32x4_t v = {0u, 0u, 0u, 0u};
-        if (lg < 2 && n < ncols) v = *(const u32x4_t*)(l + n * 16 + 8 * lg);
-        lf[b] = __builtin_bit_cast(bf16x8_t, v);
     }
 #pragma unroll
     for (int a = 0; a < TM; ++a)
@@ -1339,8 +1355,8 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     f32x4_t accz[TM];
     u32x4_t zfa_cur = {0u, 0u, 0u, 0u}, zfa_nxt = zfa_cur;
     const uint16_t* zarow = nullptr;
-    // wn as a wave-uniform (scalar) value: the k-step this wave projects is
-    // chosen by a scalar branch, since an EXEC-masked MFMA still runs
+    // wn as a wave-uniform (scalar) value selects the main loop's
+    // instantiation (an EXEC-masked MFMA would still run)
     const int wn_s = __builtin_amdgcn_readfirstlane(wn);
     if constexpr (FZ) {
 #pragma unroll
@@ -1352,62 +1368,73 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     __builtin_amdgcn_s_barrier();  // the producers' prologue barrier
     asm volatile("" ::: "memory");
 
-    for (int per = 0; per < nper; ++per) {
+    // the main loop, instantiated once per value of wn in the fused form so
+    // that the k-step a wave projects (h == ZH) is fixed at compile time:
+    // no branch inside the MFMA schedule
+    auto main_loop = [&](auto zh_c) {
+        constexpr int ZH = decltype(zh_c)::value;
+        for (int per = 0; per < nper; ++per) {
 #pragma unroll
-        for (int u = 0; u < P; ++u) {
-            const int st = per * P + u;
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // own LDS reads of the previous stage are done
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            if (st < nst) {
-                const uint8_t* xs = (u & 1) ? xs1 : xs0;
-                const uint16_t* bq = (u & 1) ? bq1 : bq0;
-                if constexpr (FZ) {
-                    zfa_cur = zfa_nxt;
-                    if (st + 1 < nst) zfa_nxt = *(const u32x4_t*)(zarow + (int64_t)(st + 1) * 64);
-                }
-                // software pipeline over (h, a): B fragments of k-step h+1 are read
-                // while k-step h runs; A fragments rotate through 3 registers, read
-                // 2 MFMA groups (10 MFMAs) ahead of their use.
-                bf16x8_t bf[2][TN], af[3];
-                auto rdA = [&](int h, int a) {
-                    return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
-                };
-                auto rdB = [&](int h, int b) {
-                    return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(bq + boff[h] + b * 16 * BLD));
-                };
+            for (int u = 0; u < P; ++u) {
+                const int st = per * P + u;
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // own LDS reads of the previous stage are done
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                if (st < nst) {
+                    const uint8_t* xs = (u & 1) ? xs1 : xs0;
+                    const uint16_t* bq = (u & 1) ? bq1 : bq0;
+                    if constexpr (FZ) {
+                        zfa_cur = zfa_nxt;
+                        if (st + 1 < nst) zfa_nxt = *(const u32x4_t*)(zarow + (int64_t)(st + 1) * 64);
+                    }
+                    // software pipeline over (h, a): B fragments of k-step h+1 are read
+                    // while k-step h runs; A fragments rotate through 3 registers, read
+                    // 2 MFMA groups (10 MFMAs) ahead of their use.
+                    bf16x8_t bf[2][TN], af[3];
+                    auto rdA = [&](int h, int a) {
+                        return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
+                    };
+                    auto rdB = [&](int h, int b) {
+                        return __builtin_bit_cast(bf16x8_t,
+                                                  *(const u32x4_t*)(bq + boff[h] + b * 16 * BLD));
+                    };
 #pragma unroll
-                for (int b = 0; b < TN; ++b) bf[0][b] = rdB(0, b);
-                af[0] = rdA(0, 0);
-                af[1] = rdA(0, 1);
+                    for (int b = 0; b < TN; ++b) bf[0][b] = rdB(0, b);
+                    af[0] = rdA(0, 0);
+                    af[1] = rdA(0, 1);
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
+                    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                    for (int a = 0; a < TM; ++a) {
-                        const int q = h * TM + a + 2;   // the (h, a) index read now
-                        if (q < 2 * TM) af[q % 3] = rdA(q / TM, q % TM);
-                        if (h == 0 && a == (TM > 2 ? 2 : TM - 1)) {
+                        for (int a = 0; a < TM; ++a) {
+                            const int q = h * TM + a + 2;   // the (h, a) index read now
+                            if (q < 2 * TM) af[q % 3] = rdA(q / TM, q % TM);
+                            if (h == 0 && a == (TM > 2 ? 2 : TM - 1)) {
 #pragma unroll
-                            for (int b = 0; b < TN; ++b) bf[1][b] = rdB(1, b);
+                                for (int b = 0; b < TN; ++b) bf[1][b] = rdB(1, b);
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                            for (int b = 0; b < TN; ++b)
+                                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                    bf[h][b], af[(h * TM + a) % 3], acc[a][b], 0, 0, 0);
+                            if constexpr (FZ) {
+                                if (h == ZH)  // folds: h and ZH are both constants here
+                                    accz[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                        __builtin_bit_cast(bf16x8_t, zfa_cur), af[(h * TM + a) % 3],
+                                        accz[a], 0, 0, 0);
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
                         }
-                        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                        for (int b = 0; b < TN; ++b)
-                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[h][b], af[(h * TM + a) % 3],
-                                                                                acc[a][b], 0, 0, 0);
-                        if constexpr (FZ) {
-                            if (h == wn_s)  // a scalar branch: MFMAs ignore the EXEC mask
-                                accz[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                                    __builtin_bit_cast(bf16x8_t, zfa_cur), af[(h * TM + a) % 3],
-                                    accz[a], 0, 0, 0);
-                        }
-                        __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             }
         }
-    }
+    };
+    if (FZ && wn_s != 0)
+        main_loop(std::integral_constant<int, 1>{});
+    else
+        main_loop(std::integral_constant<int, 0>{});
 
     // after the last barrier the ring slot of stage nst - 2 (nst & 1) is read
     // by nobody and written by nobody: 8 KB of it per wave stage the output
@@ -1486,6 +1513,9 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
     __shared__ __attribute__((aligned(16))) uint8_t xs1[BM * 128];
     __shared__ __attribute__((aligned(16))) uint8_t bq0[64 * ROWB];
     __shared__ __attribute__((aligned(16))) uint8_t bq1[64 * ROWB];
+    // fused form with the adapter as stored (B [R, 16]): a stage's 64 rows of
+    // B, 2 KB, copied as they lie by the first two producer waves
+    __shared__ __attribute__((aligned(16))) uint8_t zb[2][FZ ? 64 * 32 : 16];
 
     const int ntiles = tiles_m * tiles_n;
     const int per_xcd = (ntiles + 7) / 8;
@@ -1662,11 +1692,19 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
         XChunk<XF> xv[D][8];
         uint32_t cv[D][BITS];
         uint16_t sv[D][2];
+        // the stored adapter's slab: thread pt < 128 (waves 4 and 5) copies
+        // bytes 16 pt .. +15 of the stage's 2 KB of B
+        u32x4_t zv[D];
+        const bool zst = FZ && lora.stored && pw < 2;
+        const uint16_t* zsrc = (const uint16_t*)lora.a + pt * 8;
         auto issue = [&](int st, int r) {
             const int sc = st < nst ? st : nst - 1;
             const uint8_t* xb = xbase + (int64_t)sc * 64 * XChunk<XF>::EB;
 #pragma unroll
             for (int i = 0; i < 8; ++i) xv[r][i].load(xb + xoff[i]);
+            if constexpr (FZ) {
+                if (zst) zv[r] = *(gv_t)(zsrc + (int64_t)sc * 64 * 16);
+            }
             const int64_t row = (int64_t)sc * 64 + jr;
             const uint32_t* ws = wbase + row * wpr;
             if constexpr (BITS % 4 == 0) {
@@ -1702,6 +1740,9 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     *(u32x4_t*)(bq + qdst[q]) = u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
+                if constexpr (FZ) {
+                    if (zst) *(u32x4_t*)(zb[u] + pt * 16) = zv[u];
+                }
                 issue(st + D, u);
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this stage's LDS writes are done
                 asm volatile("" ::: "memory");
@@ -1749,83 +1790,112 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_n_k64(
         }
     typedef short s16x4_t __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_p;
-    // fused down-projection (u = dY . B with a = B^T [16, R]): as in qmm_t_k64
+    // fused down-projection (u = dY . B with a = B^T [16, R]): as in qmm_t_k64.
+    // With the adapter as stored (lora.stored: B [R, 16]) a lane's fragment
+    // (rank lr, weight rows 8 lg .. +7 of its k-step) comes from the stage's
+    // LDS slab of B with two transposed reads, like the weight fragments:
+    // source lane 4 s + c of a 16-lane group reads ranks 4 c .. +3 of row s.
     f32x4_t accz[TM];
     u32x4_t zfa_cur = {0u, 0u, 0u, 0u}, zfa_nxt = zfa_cur;
     const uint16_t* zarow = nullptr;
-    // wn as a wave-uniform (scalar) value: the k-step this wave projects is
-    // chosen by a scalar branch, since an EXEC-masked MFMA still runs
+    uint32_t zoff[2] = {0u, 0u};
+    // wn as a wave-uniform (scalar) value selects the main loop's
+    // instantiation (an EXEC-masked MFMA would still run)
     const int wn_s = __builtin_amdgcn_readfirstlane(wn);
     if constexpr (FZ) {
 #pragma unroll
         for (int a = 0; a < TM; ++a) accz[a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        zarow = (const uint16_t*)lora.a + (int64_t)lr * lora.a_ld + 32 * wn + 8 * lg;
-        zfa_nxt = *(const u32x4_t*)zarow;
+        if (lora.stored) {
+#pragma unroll
+            for (int v = 0; v < 2; ++v)
+                zoff[v] = (uint32_t)((32 * wn + 8 * lg + 4 * v + (lr >> 2)) * 32 + (lr & 3) * 8);
+        } else {
+            zarow = (const uint16_t*)lora.a + (int64_t)lr * lora.a_ld + 32 * wn + 8 * lg;
+            zfa_nxt = *(const u32x4_t*)zarow;
+        }
     }
 
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();  // the producers' initial barrier
     asm volatile("" ::: "memory");
-    for (int s0 = 0; s0 < nst; s0 += 2) {
+    // one instantiation per value of wn in the fused form, as in qmm_t_k64
+    auto main_loop = [&](auto zh_c) {
+        constexpr int ZH = decltype(zh_c)::value;
+        for (int s0 = 0; s0 < nst; s0 += 2) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int st = s0 + u;
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // own LDS reads of the previous stage are done
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            if (st < nst) {
-                const uint8_t* xs = u ? xs1 : xs0;
-                uint8_t* bq = u ? bq1 : bq0;
-                if constexpr (FZ) {
-                    zfa_cur = zfa_nxt;
-                    if (st + 1 < nst) zfa_nxt = *(const u32x4_t*)(zarow + (int64_t)(st + 1) * 64);
-                }
-                // fragments software-pipelined as in qmm_t_k64
-                bf16x8_t bf[2][TN], af[3];
-                auto rdA = [&](int h, int a) {
-                    return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
-                };
-                auto rdB = [&](int h, int b) {
-                    const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_s16x4_p)(bq + boff[0][b] + h * 32 * ROWB));
-                    const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_s16x4_p)(bq + boff[1][b] + h * 32 * ROWB));
-                    typedef short s16x8_t __attribute__((ext_vector_type(8)));
-                    const s16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    return __builtin_bit_cast(bf16x8_t, v);
-                };
-#pragma unroll
-                for (int b = 0; b < TN; ++b) bf[0][b] = rdB(0, b);
-                af[0] = rdA(0, 0);
-                af[1] = rdA(0, 1);
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                    for (int a = 0; a < TM; ++a) {
-                        const int q = h * TM + a + 2;
-                        if (q < 2 * TM) af[q % 3] = rdA(q / TM, q % TM);
-                        if (h == 0 && a == (TM > 2 ? 2 : TM - 1)) {
-#pragma unroll
-                            for (int b = 0; b < TN; ++b) bf[1][b] = rdB(1, b);
+            for (int u = 0; u < 2; ++u) {
+                const int st = s0 + u;
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // own LDS reads of the previous stage are done
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                if (st < nst) {
+                    const uint8_t* xs = u ? xs1 : xs0;
+                    uint8_t* bq = u ? bq1 : bq0;
+                    if constexpr (FZ) {
+                        if (lora.stored) {
+                            const s16x4_t lo =
+                                __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_p)(zb[u] + zoff[0]));
+                            const s16x4_t hi =
+                                __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_p)(zb[u] + zoff[1]));
+                            typedef short s16x8_t __attribute__((ext_vector_type(8)));
+                            const s16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                            zfa_cur = __builtin_bit_cast(u32x4_t, v);
+                        } else {
+                            zfa_cur = zfa_nxt;
+                            if (st + 1 < nst) zfa_nxt = *(const u32x4_t*)(zarow + (int64_t)(st + 1) * 64);
                         }
-                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    // fragments software-pipelined as in qmm_t_k64
+                    bf16x8_t bf[2][TN], af[3];
+                    auto rdA = [&](int h, int a) {
+                        return __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(xs + aoff[h][a]));
+                    };
+                    auto rdB = [&](int h, int b) {
+                        const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (lds_s16x4_p)(bq + boff[0][b] + h * 32 * ROWB));
+                        const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (lds_s16x4_p)(bq + boff[1][b] + h * 32 * ROWB));
+                        typedef short s16x8_t __attribute__((ext_vector_type(8)));
+                        const s16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                        return __builtin_bit_cast(bf16x8_t, v);
+                    };
 #pragma unroll
-                        for (int b = 0; b < TN; ++b)
-                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                                bf[h][b], af[(h * TM + a) % 3], acc[a][b], 0, 0, 0);
-                        if constexpr (FZ) {
-                            if (h == wn_s)  // a scalar branch: MFMAs ignore the EXEC mask
-                                accz[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                                    __builtin_bit_cast(bf16x8_t, zfa_cur), af[(h * TM + a) % 3],
-                                    accz[a], 0, 0, 0);
+                    for (int b = 0; b < TN; ++b) bf[0][b] = rdB(0, b);
+                    af[0] = rdA(0, 0);
+                    af[1] = rdA(0, 1);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                        for (int a = 0; a < TM; ++a) {
+                            const int q = h * TM + a + 2;
+                            if (q < 2 * TM) af[q % 3] = rdA(q / TM, q % TM);
+                            if (h == 0 && a == (TM > 2 ? 2 : TM - 1)) {
+#pragma unroll
+                                for (int b = 0; b < TN; ++b) bf[1][b] = rdB(1, b);
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                            for (int b = 0; b < TN; ++b)
+                                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                    bf[h][b], af[(h * TM + a) % 3], acc[a][b], 0, 0, 0);
+                            if constexpr (FZ) {
+                                if (h == ZH)  // folds: h and ZH are both constants here
+                                    accz[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                        __builtin_bit_cast(bf16x8_t, zfa_cur), af[(h * TM + a) % 3],
+                                        accz[a], 0, 0, 0);
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
                         }
-                        __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             }
         }
-    }
+    };
+    if (FZ && wn_s != 0)
+        main_loop(std::integral_constant<int, 1>{});
+    else
+        main_loop(std::integral_constant<int, 0>{});
 
     // after the last barrier the ring slot of stage nst - 2 (nst & 1) is free
     if constexpr (FZ) {

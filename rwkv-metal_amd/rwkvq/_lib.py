@@ -58,6 +58,8 @@ SIGNATURES = {
                      _i64, ctypes.c_float, _vp, _i32, _vp], _i32),
     "rq_qlora": ([_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _vp,
                   _i64, ctypes.c_float, _vp, _vp, _i32, _vp], _i32),
+    "rq_qlora_dx": ([_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp,
+                     _i64, ctypes.c_float, _vp, _vp, _i32, _vp], _i32),
     "rq_lora_down": ([_vp, _i64, _i64, _vp, _i64, _vp, _vp], _i32),
     "rq_lora_grads_workspace_bytes": ([_i64, _i64, _i64, _i64, _i32, _i32], _i64),
     "rq_lora_grads": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _vp,

@@ -12,8 +12,8 @@ y = base(x) + (alpha/rank) * (x @ A^T) @ B^T with A ~ N(0, 1)/sqrt(in_features)
 and B = 0 (lora.py:54-56).  Only lora_a / lora_b are trainable (lora.py:101-102).
 Over a QuantizedLinear base with bf16 or fp32 activations (bf16 adapters)
 the low-rank term is fused into the packed-weight GEMMs, forward and dX
-(rq_qlora / rq_qmm_lora, _QLoRAFunction); other bases and dtypes compose the
-ops.
+(rq_qlora / rq_qlora_dx / rq_qmm_lora, _QLoRAFunction); other bases and
+dtypes compose the ops.
 The model layout is the reference's: model.blocks[i].tmix.{r,k,v,o}_proj and
 model.blocks[i].cmix.{key,value}.
 
@@ -48,9 +48,9 @@ class _QLoRAFunction(torch.autograd.Function):
     low-rank term fused into the packed-weight GEMMs.  Rank 16 at 4 or 8 bits
     (rq_qlora): the forward is one launch that also computes z = x A^T
     inside the transpose=True GEMM and adds z B^T in its output stage; dX is
-    one launch that computes u = dY B inside the transpose=False GEMM and adds
-    scale * u A; dA = scale * u^T x and dB = scale * dY^T z are one
-    rq_lora_grads launch.  Other ranks run z and u as rq_lora_down launches
+    one launch (rq_qlora_dx) that computes u = dY B inside the
+    transpose=False GEMM and adds scale * u A, reading A and B as stored; dA =
+    scale * u^T x and dB = scale * dY^T z are one rq_lora_grads launch.  Other ranks run z and u as rq_lora_down launches
     and the term with rq_qmm_lora.  The frozen base gets no gradient.
 
     fp32 x (the reference's default activations) is rounded to bf16 once, by
@@ -84,22 +84,22 @@ class _QLoRAFunction(torch.autograd.Function):
         gs, bits = base.group_size, base.bits
         dy = dy.contiguous().to(xdt)
         dyb = dy.to(torch.bfloat16) if xdt == torch.float32 else dy
-        bt = lora_b.t().contiguous()
         dx = da = db = None
         dxu = None
         if ctx.needs_input_grad[0]:
-            at = lora_a.t().contiguous()
-            dxu = ops.qlora_fused(dyb, base.weight, base.scales, base.biases, bt, at, scale, False,
-                                  gs, bits, out_dtype=ops._promote(xdt, base.scales.dtype))
+            # one launch from the adapters as stored: u = dY B inside the GEMM
+            dxu = ops.qlora_dx_fused(dyb, base.weight, base.scales, base.biases, lora_a, lora_b,
+                                     scale, gs, bits, out_dtype=ops._promote(xdt, base.scales.dtype))
             if dxu is not None:
-                dx, u = dxu  # one launch: u = dY B inside the GEMM
+                dx, u = dxu
             else:
+                bt = lora_b.t().contiguous()
                 u = ops.lora_down(dy, bt)
-                dx = ops.quantized_matmul_lora(dy, base.weight, base.scales, base.biases, u, at,
-                                               scale, False, gs, bits)
+                dx = ops.quantized_matmul_lora(dy, base.weight, base.scales, base.biases, u,
+                                               lora_a.t().contiguous(), scale, False, gs, bits)
             dx = dx.to(xdt)
         else:
-            u = ops.lora_down(dyb, bt)
+            u = ops.lora_down(dyb, lora_b.t().contiguous())
         # both adapter gradients in one launch, fp32 accumulation, one rounding
         want_a, want_b = ctx.needs_input_grad[1], ctx.needs_input_grad[2]
         da, db = ops.lora_grads(xb if want_a else None, u if want_a else None,

@@ -556,6 +556,47 @@ def qlora_fused(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, a: Tenso
     return y, z
 
 
+def qlora_dx_fused(dy: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, lora_a: Tensor,
+                   lora_b: Tensor, scale: float, group_size: int = 64, bits: int = 4,
+                   out_dtype: torch.dtype | None = None):
+    """The QLoRA layer's dX in one rq_qlora_dx launch from the adapters as
+    the layer stores them (lora_a [rank, K], lora_b [R, rank]): (dx, u) with
+    u = dy @ lora_b [m, rank] (bf16) computed inside the transposed GEMM and
+    dx = quantized_matmul(dy, ..., transpose=False) + scale * u @ lora_a;
+    equal bit for bit to qlora_fused(dy, ..., lora_b^T, lora_a^T, scale,
+    False), without the transposed copies.  dy is 2-D.  None where the fused
+    kernels do not apply; no autograd."""
+    _check_args(group_size, bits)
+    w_q = _words(w_q)
+    K = _check_packed(w_q, scales, biases, group_size, bits)
+    R = w_q.shape[0]
+    rank = lora_a.shape[0]
+    if (dy.dim() != 2 or dy.shape[1] != R or tuple(lora_a.shape) != (rank, K)
+            or tuple(lora_b.shape) != (R, rank)):
+        raise ValueError("qlora_dx_fused: dy, lora_a and lora_b shapes do not agree")
+    if not (dy.dtype in (torch.bfloat16, torch.float32)
+            and lora_a.dtype == lora_b.dtype == torch.bfloat16 and rank == 16):
+        return None
+    _on_gpu(dy, w_q, scales, biases, lora_a, lora_b)
+    dy, w_q, scales = _ready(dy), _ready(w_q), _ready(scales)
+    lora_a, lora_b = lora_a.contiguous(), lora_b.contiguous()
+    biases = _ready(biases.to(scales.dtype))
+    m = dy.shape[0]
+    dx = torch.empty(m, K, dtype=out_dtype or _promote(dy.dtype, scales.dtype), device=dy.device)
+    u = torch.empty(m, rank, dtype=torch.bfloat16, device=dy.device)
+    if m == 0:
+        return dx, u
+    with _DeviceGuard(dy.device):
+        rc = lib().rq_qlora_dx(_ptr(dy), DTYPE_CODE[dy.dtype], _ptr(w_q), _ptr(scales),
+                               _ptr(biases), DTYPE_CODE[scales.dtype], m, R, K, group_size, bits,
+                               _ptr(lora_a), _ptr(lora_b), rank, float(scale), _ptr(u), _ptr(dx),
+                               DTYPE_CODE[dx.dtype], _stream(dy))
+    if rc == RQ_EUNSUPPORTED:
+        return None
+    check(rc, "qlora_dx_fused")
+    return dx, u
+
+
 def quantized_matmul_lora(x: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, z: Tensor,
                           lora: Tensor, scale: float, transpose: bool = True,
                           group_size: int = 64, bits: int = 4) -> Tensor:

@@ -30,7 +30,7 @@ def test_header_declares_the_expected_surface():
         "rq_grouped_plan_init", "rq_grouped_plan_run", "rq_embedding", "rq_sb6_dequantize",
         "rq_sb6_to_affine", "rq_qmm_lora", "rq_lora_down", "rq_lora_grads_workspace_bytes",
         "rq_lora_grads", "rq_lora_grads_f32", "rq_lora_grads_noalloc", "rq_qlora",
-        "rq_qmm_splitk_workspace_bytes", "rq_qmm_splitk"])
+        "rq_qlora_dx", "rq_qmm_splitk_workspace_bytes", "rq_qmm_splitk"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -216,3 +216,24 @@ def test_qmm_splitk_plan_and_rejections(L):
     need = nb(512, 2560, 10240, 64, 4)
     assert L.rq_qmm_splitk(p, 0, p, p, p, 0, 512, 2560, 10240, 64, 4, p, 0, p + 8, need,
                            None) == -2
+
+
+def test_qlora_dx_rejections_before_any_device_work(L):
+    """rq_qlora_dx validates before it launches: the rank, NULL adapters,
+    alignment (16 bytes for dy and u_out, 2 for the adapters as stored) and
+    an empty contraction; an empty output is a no-op."""
+    p = 0x1000
+    f = L.rq_qlora_dx
+    assert f(p, 0, p, p, p, 0, 512, 2048, 2048, 64, 4, p, p, 8, 1.0, p, p, 0, None) == -1
+    assert "rank" in _err(L)
+    assert f(p, 0, p, p, p, 0, 512, 2048, 2048, 64, 4, 0, p, 16, 1.0, p, p, 0, None) == -1
+    assert "NULL" in _err(L)
+    assert f(p + 8, 0, p, p, p, 0, 512, 2048, 2048, 64, 4, p, p, 16, 1.0, p, p, 0, None) == -2
+    assert f(p, 0, p, p, p, 0, 512, 2048, 2048, 64, 4, p + 1, p, 16, 1.0, p, p, 0, None) == -2
+    assert "2-byte" in _err(L)
+    assert f(p, 0, p, p, p, 0, 512, 2048, 2048, 64, 4, p, p + 2, 16, 1.0, p + 8, p, 0,
+             None) == -2
+    assert f(p, 0, p, p, p, 0, 512, 0, 2048, 64, 4, p, p, 16, 1.0, p, p, 0, None) == -1
+    assert "contraction" in _err(L)
+    assert f(p, 0, p, p, p, 0, 512, 2048, 2048, 64, 7, p, p, 16, 1.0, p, p, 0, None) == -1
+    assert f(p, 0, p, p, p, 0, 0, 2048, 2048, 64, 4, p, p, 16, 1.0, p, p, 0, None) == 0

@@ -6,7 +6,7 @@ reference on the dequantized base."""
 import pytest
 import torch
 
-from test_gpu_parity import acts, rel_check, say, weights
+from test_gpu_parity import acts, bits_equal, rel_check, say, weights
 
 pytestmark = pytest.mark.gpu
 
@@ -123,6 +123,32 @@ def test_qlora_one_launch(rq, dev, transpose, M, R, K, bits, gs, sdt):
     # and the two-launch path gives the same product within the bar
     y2 = ops.quantized_matmul_lora(x, wq, s, b, ops.lora_down(x, a), L, 0.75, transpose, gs, bits)
     rel_check(y, y2.float(), what="y vs lora_down + rq_qmm_lora")
+
+
+@pytest.mark.parametrize("M,R,K,bits,gs,sdt", [c[1:] for c in QLORA_CASES if not c[0]])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+def test_qlora_dx_from_stored_adapters(rq, dev, M, R, K, bits, gs, sdt, xdt):
+    """rq_qlora_dx reads lora_a [16, K] and lora_b [R, 16] as the layer
+    stores them (strided fragment loads) and must give rq_qlora(transpose=0)'s
+    bits on their transposed copies: dX and u = dY lora_b."""
+    from rwkvq import ops
+    say(f"qlora dx stored adapters M={M} R={R} K={K} b={bits} gs={gs} s={sdt} x={xdt}")
+    wq, s, b = rq.quantize(weights(R, K, 71_000 + R + K, sdt).to(dev), gs, bits)
+    g = torch.Generator().manual_seed(M + R + K + 1)
+    dy = acts(M, R, M + R).to(xdt).to(dev)
+    lora_a = (torch.randn(16, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
+    lora_b = (torch.randn(R, 16, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    got = ops.qlora_dx_fused(dy, wq, s, b, lora_a, lora_b, 0.75, gs, bits)
+    want = ops.qlora_fused(dy, wq, s, b, lora_b.t().contiguous(), lora_a.t().contiguous(), 0.75,
+                           False, gs, bits)
+    assert got is not None and want is not None, "this problem must run the one-launch kernels"
+    assert bits_equal(got[1], want[1]), "u"
+    assert bits_equal(got[0], want[0]), "dX"
+    # adapters that are views with gaps are made contiguous, not misread
+    wide = torch.zeros(R, 32, dtype=torch.bfloat16, device=dev)
+    wide[:, :16] = lora_b
+    again = ops.qlora_dx_fused(dy, wq, s, b, lora_a, wide[:, :16], 0.75, gs, bits)
+    assert bits_equal(again[0], want[0])
 
 
 def test_qlora_one_launch_declines_other_ranks_and_bits(rq, dev):
