@@ -110,7 +110,7 @@ hipError_t launch_lora_down(const void* x, int64_t m, int64_t k, const void* a, 
 // anything else: zero before the first use, left zero by every launch,
 // whatever problem used the buffer last) followed by `partial_bytes` of fp32
 // partial tiles.
-constexpr int kLoraGradTargetBlocks = 1024;          // ~4 jobs per CU
+constexpr int kLoraGradTargetBlocks = 512;           // ~2 jobs per CU
 constexpr int64_t kLoraGradPartialCap = 8ll << 20;   // fp32 partial bytes at most
 constexpr int kLoraGradMaxTiles = 16384;             // k/64 + n/64 at most
 constexpr size_t kLoraGradCounterBytes = (size_t)kLoraGradMaxTiles * 4;
