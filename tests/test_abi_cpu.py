@@ -154,13 +154,13 @@ def test_lora_grads_workspace_and_rejections(L):
     fills the GPU, fp32 partial tiles plus one counter per tile otherwise;
     bad ranks, unaligned operands and a short workspace are refused."""
     p = 0x1000
-    # 4096 rows, K = N = 2048, rank 16: 64 tiles, 16 chunks of 256 rows
+    # 4096 rows, K = N = 2048, rank 16: 64 tiles, 8 chunks of 512 rows (~512 jobs)
     counters = 16384 * 4
     nb = L.rq_lora_grads_workspace_bytes(4096, 2048, 2048, 16, 1, 1)
-    assert nb == counters + 64 * 16 * 64 * 16 * 4
-    # only dB: 32 tiles, 32 chunks of 128 rows (64 rows per step, 64 steps)
+    assert nb == counters + 64 * 8 * 64 * 16 * 4
+    # only dB: 32 tiles, 16 chunks of 256 rows (64 rows per step, 64 steps)
     assert L.rq_lora_grads_workspace_bytes(4096, 2048, 2048, 16, 0, 1) == \
-        counters + 32 * 32 * 64 * 16 * 4
+        counters + 32 * 16 * 64 * 16 * 4
     # few rows: one chunk, no workspace
     assert L.rq_lora_grads_workspace_bytes(64, 2048, 2048, 16, 1, 1) == 0
     # wide outputs at rank 64 stay within the 8 MiB partial cap
