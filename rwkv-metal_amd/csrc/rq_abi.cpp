@@ -508,6 +508,21 @@ int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* s
     return launch_status(e, "rq_qmm_lora");
 }
 
+// The fused QLoRA products compute the down-projection once per output
+// column tile: 12.5 % more MFMA work in every 128-column tile, on the waves
+// that bound the GEMM.  Its rq_lora_down pass instead reads the activations
+// once, so for outputs much wider than the contraction two launches cost
+// less (MI355X, M = 4096: forward [8192, 2048] and dX of [2048, 8192] about
+// +22 us fused against +8 us for the pass and the output-stage term; the
+// [2048, 2048] ones +5 us against +7).  bf16 or fp32 activations (the pass
+// rounds fp32 ones to bf16 as the GEMM does, so either gives the bits of
+// bf16(x)), rank 16, 4 or 8 bits, m >= 256: where the fused kernels apply.
+static bool qlora_two_launch(int x_dt, int bits, int64_t rank, int64_t m, int64_t n_in,
+                             int64_t n_out) {
+    return (x_dt == RQ_BF16 || x_dt == RQ_F32) && (bits == 4 || bits == 8) && rank == 16 &&
+           m >= 256 && n_in % 32 == 0 && n_out >= 4096 && n_out >= 2 * n_in;
+}
+
 int rq_qlora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
              const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
              int group_size, int bits, int transpose, const void* a, const void* lora,
@@ -524,12 +539,22 @@ int rq_qlora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scal
         return fail(RQ_EINVAL, "rq_qlora: NULL pointer");
     if (!aligned16(x) || !aligned16(w_q) || !aligned16(a) || !aligned16(lora) || !aligned16(z_out))
         return fail(RQ_EALIGN, "rq_qlora: x, w_q, a, lora and z_out must be 16-byte aligned");
-    rq::LoraArgs lo{nullptr, lora, (int)rank, scale};
-    lo.a = a;
-    lo.z_out = z_out;
-    lo.a_ld = n_in;
-    const hipError_t e = rq::launch_qmm(transpose, x, x_dt, w_q, scales, biases, sb_dt, m, rows,
-                                        cols, group_size, bits, y, y_dt, (hipStream_t)stream, &lo);
+    hipError_t e;
+    if (z_out && qlora_two_launch(x_dt, bits, rank, m, n_in, n_out)) {
+        e = rq::launch_lora_down(x, m, n_in, a, (int)rank, z_out, (hipStream_t)stream,
+                                 /*a_t=*/false, x_dt == RQ_F32);
+        rq::LoraArgs lo{z_out, lora, (int)rank, scale};
+        if (e == hipSuccess)
+            e = rq::launch_qmm(transpose, x, x_dt, w_q, scales, biases, sb_dt, m, rows, cols,
+                               group_size, bits, y, y_dt, (hipStream_t)stream, &lo);
+    } else {
+        rq::LoraArgs lo{nullptr, lora, (int)rank, scale};
+        lo.a = a;
+        lo.z_out = z_out;
+        lo.a_ld = n_in;
+        e = rq::launch_qmm(transpose, x, x_dt, w_q, scales, biases, sb_dt, m, rows, cols,
+                           group_size, bits, y, y_dt, (hipStream_t)stream, &lo);
+    }
     if (e == hipErrorNotSupported)
         return fail(RQ_EUNSUPPORTED,
                     "rq_qlora: the in-kernel down-projection covers rank 16 with 4- or 8-bit codes "
@@ -558,14 +583,26 @@ int rq_qlora_dx(const void* dy, rq_dtype dy_dt, const uint32_t* w_q, const void*
         return fail(RQ_EALIGN, "rq_qlora_dx: lora_a and lora_b must be 2-byte aligned");
     // u = dY . B from B [rows, rank] as stored; the term scale * u . A from A
     // [rank, cols] as stored
-    rq::LoraArgs lo{nullptr, lora_a, (int)rank, scale};
-    lo.a = lora_b;
-    lo.z_out = u_out;
-    lo.a_ld = rows;
-    lo.stored = true;
-    lo.l_ld = cols;
-    const hipError_t e = rq::launch_qmm(0, dy, dy_dt, w_q, scales, biases, sb_dt, m, rows, cols,
-                                        group_size, bits, dx, dx_dt, (hipStream_t)stream, &lo);
+    hipError_t e;
+    if (u_out && aligned16(lora_b) && qlora_two_launch(dy_dt, bits, rank, m, rows, cols)) {
+        e = rq::launch_lora_down(dy, m, rows, lora_b, (int)rank, u_out, (hipStream_t)stream,
+                                 /*a_t=*/true, dy_dt == RQ_F32);
+        rq::LoraArgs lo{u_out, lora_a, (int)rank, scale};
+        lo.stored = true;
+        lo.l_ld = cols;
+        if (e == hipSuccess)
+            e = rq::launch_qmm(0, dy, dy_dt, w_q, scales, biases, sb_dt, m, rows, cols, group_size,
+                               bits, dx, dx_dt, (hipStream_t)stream, &lo);
+    } else {
+        rq::LoraArgs lo{nullptr, lora_a, (int)rank, scale};
+        lo.a = lora_b;
+        lo.z_out = u_out;
+        lo.a_ld = rows;
+        lo.stored = true;
+        lo.l_ld = cols;
+        e = rq::launch_qmm(0, dy, dy_dt, w_q, scales, biases, sb_dt, m, rows, cols, group_size,
+                           bits, dx, dx_dt, (hipStream_t)stream, &lo);
+    }
     if (e == hipErrorNotSupported)
         return fail(RQ_EUNSUPPORTED,
                     "rq_qlora_dx: the in-kernel down-projection covers rank 16 with 4- or 8-bit "

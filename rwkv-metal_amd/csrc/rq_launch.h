@@ -98,9 +98,11 @@ struct LoraArgs {
 };
 
 // Low-rank down-projection z[m, rank] = x[m, k] . a[rank, k]^T, bf16 (rank
-// 16, 32, 48 or 64; k a multiple of 32).
+// 16, 32, 48 or 64; k a multiple of 32).  a_t: the adapter is given as
+// a^T [k, rank] (row-major, 16-byte aligned) instead.  x_f32: x is fp32
+// (rounded to bf16 as it is read; z is then that of bf16(x)).
 hipError_t launch_lora_down(const void* x, int64_t m, int64_t k, const void* a, int rank, void* z,
-                            hipStream_t stream);
+                            hipStream_t stream, bool a_t = false, bool x_f32 = false);
 
 // QLoRA adapter gradients dA[rank, k] = scale * u^T x and dB[n, rank] =
 // scale * dY^T z in one launch (bf16 in and out, fp32 accumulation).  The

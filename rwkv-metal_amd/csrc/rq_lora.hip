@@ -16,6 +16,15 @@
 //    the next U before the MFMAs of the current ones (two register sets).
 //  * The W waves' partial 16 x rank tiles are summed through LDS behind one
 //    barrier and stored as bf16.
+//  * AT: the adapter comes as its transpose b = a^T [K, rank] (row-major; the
+//    QLoRA backward's B as the layer stores it, u = dY . B).  A k-step's 32
+//    rows of b (rank * 64 bytes) are loaded as they lie, 16 bytes a lane, and
+//    copied to the wave's own LDS buffer; each 16 x 32 fragment then comes
+//    from two gfx950 ds_read_b64_tr_b16 (source lane 4 s + c of a 16-lane
+//    group reads ranks 4 c .. +3 of row s).  The sums are the same as with a,
+//    in the same order.
+//  * XF: x is fp32; each 8-value chunk is loaded as 32 bytes and rounded to
+//    bf16 (RNE) before its MFMA, so z equals the bf16(x) launch's bit for bit.
 #include <mutex>
 
 #include "rq_common.h"
@@ -25,27 +34,39 @@ namespace {
 
 // waves per block and k-steps per batch of loads, by rank tiles: two
 // register sets of U x (1 + RT) 16-byte loads stay within the VGPRs the
-// block size allows (128 at 16 waves, 256 at 8)
-template <int RT> struct LoraShape {
+// block size allows (128 at 16 waves, 256 at 8; the a^T and fp32-x forms
+// hold more per k-step and batch 2 at rank 16).  Wave w sums k-steps w,
+// w + W, .. in order and the waves are summed in order, so the bits depend
+// on W alone: the forms of one rank share it.
+template <int RT, bool AT = false, bool XF = false> struct LoraShape {
     static constexpr int W = RT == 1 ? 16 : 8;
-    static constexpr int U = RT <= 2 ? 4 : 2;
+    static constexpr int U = (RT == 1 && (AT || XF)) ? 2 : (RT <= 2 ? 4 : 2);
 };
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-template <int RT>  // rank tiles of 16
-__global__ __launch_bounds__(64 * LoraShape<RT>::W) void lora_down_kernel(
-    const uint16_t* __restrict__ x, int64_t M, int64_t K, const uint16_t* __restrict__ a,
+template <int RT, bool AT = false, bool XF = false>  // rank tiles of 16; AT: a given as
+                                                    // a^T [K, rank]; XF: fp32 x
+__global__ __launch_bounds__((64 * LoraShape<RT, AT, XF>::W)) void lora_down_kernel(
+    const void* __restrict__ x, int64_t M, int64_t K, const uint16_t* __restrict__ a,
     uint16_t* __restrict__ z) {
-    constexpr int kLoraWaves = LoraShape<RT>::W, U = LoraShape<RT>::U;
+    constexpr int kLoraWaves = LoraShape<RT, AT, XF>::W, U = LoraShape<RT, AT, XF>::U;
+    constexpr int RANK = 16 * RT;
     __shared__ __attribute__((aligned(16))) float red[kLoraWaves][RT][4][64];
+    __shared__ __attribute__((aligned(16))) uint8_t slab[AT ? kLoraWaves : 1][AT ? 64 * RANK : 16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lg = lane >> 4, lr = lane & 15;
     const int64_t m0 = (int64_t)blockIdx.x * 16;
     const int64_t row = (m0 + lr) < M ? (m0 + lr) : M - 1;  // rows past M: any valid row
     const int nsteps = (int)(K >> 5);
-    const uint16_t* xr = x + row * K + lg * 8;
-    const uint16_t* ar = a + (int64_t)lr * K + lg * 8;
+    constexpr int EB = XF ? 4 : 2;  // bytes per x element
+    const uint8_t* xr = (const uint8_t*)x + (row * K + lg * 8) * EB;
+    // a: this lane's fragment row; a^T: this lane's 16-byte chunks of a k-step's rows
+    const uint16_t* ar = AT ? a + lane * 8 : a + (int64_t)lr * K + lg * 8;
+    typedef short s16x4_t __attribute__((ext_vector_type(4)));
+    typedef short s16x8_t __attribute__((ext_vector_type(8)));
+    typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_p;
+    uint8_t* wslab = slab[AT ? wave : 0];
 
     f32x4_t acc[RT];
 #pragma unroll
@@ -53,27 +74,59 @@ __global__ __launch_bounds__(64 * LoraShape<RT>::W) void lora_down_kernel(
     // Batches of U k-steps, software-pipelined: the loads of batch j + 1 are
     // issued before the MFMAs of batch j.  Loads past the end read the last
     // k-step (valid memory) and are not used.
-    u32x4_t xa[2][U], wb[2][U][RT];
+    u32x4_t xa[2][U][XF ? 2 : 1], wb[2][U][RT];
     auto load = [&](int b, int s0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             int s = s0 + kLoraWaves * u;
             s = s < nsteps ? s : nsteps - 1;
-            xa[b][u] = *(const u32x4_t*)(xr + (int64_t)s * 32);
+            const u32x4_t* xs = (const u32x4_t*)(xr + (int64_t)s * 32 * EB);
+            xa[b][u][0] = xs[0];
+            if constexpr (XF) xa[b][u][1] = xs[1];
 #pragma unroll
             for (int t = 0; t < RT; ++t)
-                wb[b][u][t] = *(const u32x4_t*)(ar + ((int64_t)t * 16 * K + (int64_t)s * 32));
+                wb[b][u][t] = AT ? *(const u32x4_t*)(ar + (int64_t)s * 32 * RANK + t * 512)
+                                 : *(const u32x4_t*)(ar + ((int64_t)t * 16 * K + (int64_t)s * 32));
         }
     };
     auto mma = [&](int b, int s0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (s0 + kLoraWaves * u < nsteps) {
-                const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa[b][u]);
+                u32x4_t xv = xa[b][u][0];
+                if constexpr (XF) {
+                    const u32x4_t p = xa[b][u][0], q = xa[b][u][1];
+                    xv = u32x4_t{pack_bf16x2(__uint_as_float(p[0]), __uint_as_float(p[1])),
+                                 pack_bf16x2(__uint_as_float(p[2]), __uint_as_float(p[3])),
+                                 pack_bf16x2(__uint_as_float(q[0]), __uint_as_float(q[1])),
+                                 pack_bf16x2(__uint_as_float(q[2]), __uint_as_float(q[3]))};
+                }
+                const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xv);
+                if constexpr (AT) {
+                    // the k-step's rows of a^T into this wave's buffer (one wave's LDS
+                    // operations complete in order: the reads below see these
+                    // writes, and the next u's writes follow these reads)
+                    asm volatile("" ::: "memory");
 #pragma unroll
-                for (int t = 0; t < RT; ++t)
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        av, __builtin_bit_cast(bf16x8_t, wb[b][u][t]), acc[t], 0, 0, 0);
+                    for (int t = 0; t < RT; ++t) *(u32x4_t*)(wslab + (lane + 64 * t) * 16) = wb[b][u][t];
+                    asm volatile("" ::: "memory");
+                }
+#pragma unroll
+                for (int t = 0; t < RT; ++t) {
+                    bf16x8_t bv;
+                    if constexpr (AT) {
+                        // rows 8 lg + 4 v + lr / 4 of the k-step, ranks 16 t + 4 (lr % 4) .. +3
+                        const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_p)(
+                            wslab + (8 * lg + (lr >> 2)) * 2 * RANK + (16 * t + 4 * (lr & 3)) * 2));
+                        const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_p)(
+                            wslab + (8 * lg + 4 + (lr >> 2)) * 2 * RANK + (16 * t + 4 * (lr & 3)) * 2));
+                        bv = __builtin_bit_cast(bf16x8_t,
+                                                s16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+                    } else {
+                        bv = __builtin_bit_cast(bf16x8_t, wb[b][u][t]);
+                    }
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[t], 0, 0, 0);
+                }
             }
         }
     };
@@ -429,20 +482,34 @@ hipError_t launch_lora_grads(const void* x, const void* u, const void* dy, const
 }
 
 hipError_t launch_lora_down(const void* x, int64_t m, int64_t k, const void* a, int rank, void* z,
-                            hipStream_t stream) {
+                            hipStream_t stream, bool a_t, bool x_f32) {
     const int blocks = (int)((m + 15) / 16);
     if (blocks == 0) return hipSuccess;
     const dim3 grid(blocks);
-    const uint16_t* xp = (const uint16_t*)x;
     const uint16_t* ap = (const uint16_t*)a;
     uint16_t* zp = (uint16_t*)z;
+#define RQ_DOWN_X(RT, ATV)                                                                         \
+    if (x_f32)                                                                                     \
+        hipLaunchKernelGGL((lora_down_kernel<RT, ATV, true>), grid,                                \
+                           dim3(64 * LoraShape<RT, ATV, true>::W), 0, stream, x, m, k, ap, zp);    \
+    else                                                                                           \
+        hipLaunchKernelGGL((lora_down_kernel<RT, ATV, false>), grid,                               \
+                           dim3(64 * LoraShape<RT, ATV, false>::W), 0, stream, x, m, k, ap, zp);
+#define RQ_DOWN(RT)                                                                                \
+    if (a_t) {                                                                                     \
+        RQ_DOWN_X(RT, true)                                                                        \
+    } else {                                                                                       \
+        RQ_DOWN_X(RT, false)                                                                       \
+    }
     switch (rank) {
-        case 16: hipLaunchKernelGGL((lora_down_kernel<1>), grid, dim3(64 * LoraShape<1>::W), 0, stream, xp, m, k, ap, zp); break;
-        case 32: hipLaunchKernelGGL((lora_down_kernel<2>), grid, dim3(64 * LoraShape<2>::W), 0, stream, xp, m, k, ap, zp); break;
-        case 48: hipLaunchKernelGGL((lora_down_kernel<3>), grid, dim3(64 * LoraShape<3>::W), 0, stream, xp, m, k, ap, zp); break;
-        case 64: hipLaunchKernelGGL((lora_down_kernel<4>), grid, dim3(64 * LoraShape<4>::W), 0, stream, xp, m, k, ap, zp); break;
+        case 16: RQ_DOWN(1) break;
+        case 32: RQ_DOWN(2) break;
+        case 48: RQ_DOWN(3) break;
+        case 64: RQ_DOWN(4) break;
         default: return hipErrorInvalidValue;
     }
+#undef RQ_DOWN
+#undef RQ_DOWN_X
     return hipGetLastError();
 }
 

@@ -969,12 +969,24 @@ RQ_DEV void store_wave_tile(const f32x4_t (&acc)[TM][TN], uint8_t* stg, void* __
     }
 }
 
+// Eight bf16 values p[0], p[stride], .., p[7 * stride] as one MFMA operand
+// fragment (a column of a row-major matrix: 2-byte loads).
+RQ_DEV u32x4_t gather8_bf16(const uint16_t* p, int64_t stride) {
+    u32x4_t v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        v[q] = (uint32_t)p[2 * q * stride] | ((uint32_t)p[(2 * q + 1) * stride] << 16);
+    return v;
+}
+
 // The QLoRA low-rank term in the output stage: acc += scale * z . L^T for a
 // wave's 128 x WN tile (rows r0.., columns c0..; acc in the weight-as-A
 // layout of store_wave_tile).  z [nrows, rank] and L [ncols, rank] are bf16
 // and small (rank <= 64), read straight from global memory: lane (lg, lr)
 // takes elements 8*lg .. +7 of a 32-wide rank slice of row lr of each 16-row
-// tile; slices past the rank and rows past the bounds read as zero.
+// tile; slices past the rank and rows past the bounds read as zero.  With
+// lo.stored, L comes as its transpose [rank, l_ld] (eight 2-byte loads a
+// fragment, once per tile).
 template <int TM, int TN>
 RQ_DEV void lora_epilogue(f32x4_t (&acc)[TM][TN], const rq::LoraArgs& lo, int64_t nrows,
                           int64_t ncols, int64_t r0, int64_t c0, int lane) {
@@ -996,7 +1008,9 @@ RQ_DEV void lora_epilogue(f32x4_t (&acc)[TM][TN], const rq::LoraArgs& lo, int64_
         for (int b = 0; b < TN; ++b) {
             const int64_t n = c0 + b * 16 + lr;
             u32x4_t v = {0u, 0u, 0u, 0u};
-            if (has && n < ncols) v = *(const u32x4_t*)(l + n * lo.rank + j);
+            if (has && n < ncols)
+                v = lo.stored ? gather8_bf16(l + j * lo.l_ld + n, lo.l_ld)
+                              : *(const u32x4_t*)(l + n * lo.rank + j);
             lf[b] = __builtin_bit_cast(bf16x8_t, v);
         }
 #pragma unroll
@@ -1009,16 +1023,6 @@ RQ_DEV void lora_epilogue(f32x4_t (&acc)[TM][TN], const rq::LoraArgs& lo, int64_
                 for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(lo.scale, t[r], acc[a][b][r]);
             }
     }
-}
-
-// Eight bf16 values p[0], p[stride], .., p[7 * stride] as one MFMA operand
-// fragment (a column of a row-major matrix: 2-byte loads).
-RQ_DEV u32x4_t gather8_bf16(const uint16_t* p, int64_t stride) {
-    u32x4_t v;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        v[q] = (uint32_t)p[2 * q * stride] | ((uint32_t)p[(2 * q + 1) * stride] << 16);
-    return v;
 }
 
 // The fused QLoRA layer's down-projection, computed in the GEMM (rank 16).

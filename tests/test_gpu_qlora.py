@@ -151,6 +151,58 @@ def test_qlora_dx_from_stored_adapters(rq, dev, M, R, K, bits, gs, sdt, xdt):
     assert bits_equal(again[0], want[0])
 
 
+@pytest.mark.parametrize("transpose,M,R,K,bits", [(True, 4096, 8192, 2048, 4),
+                                                  (False, 4096, 2048, 8192, 4),
+                                                  (True, 512, 4096, 1024, 8),
+                                                  (False, 300, 1024, 4096, 8)])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+def test_qlora_wide_outputs_take_two_launches(rq, dev, transpose, M, R, K, bits, xdt):
+    """Outputs at least 4096 wide and twice the contraction run the
+    down-projection as its own pass (x read once) and the term in the GEMM's
+    output stage: the forward and both dX entry points give exactly the bits
+    of lora_down + quantized_matmul_lora on bf16(x) -- for rq_qlora_dx with B
+    read as stored [R, 16] by the pass and A as stored [16, K] by the output
+    stage."""
+    from rwkvq import ops
+    say(f"qlora two launches t={transpose} M={M} R={R} K={K} b={bits} x={xdt}")
+    wq, s, b = rq.quantize(weights(R, K, 72_000 + R + K).to(dev), 64, bits)
+    n_in, n_out = (K, R) if transpose else (R, K)
+    g = torch.Generator().manual_seed(M + R + K + 2)
+    x = acts(M, n_in, M + n_in + 2).to(xdt).to(dev)
+    xb = x.to(torch.bfloat16)
+    lora_a = (torch.randn(16, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
+    lora_b = (torch.randn(R, 16, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    if transpose:
+        y, z = ops.qlora_fused(x, wq, s, b, lora_a, lora_b, 0.75, True, 64, bits,
+                               out_dtype=torch.float32)
+        zr = ops.lora_down(xb, lora_a)
+        yr = ops.quantized_matmul_lora(xb, wq, s, b, zr, lora_b, 0.75, True, 64, bits)
+    else:
+        y, z = ops.qlora_dx_fused(x, wq, s, b, lora_a, lora_b, 0.75, 64, bits,
+                                  out_dtype=torch.float32)
+        y2, z2 = ops.qlora_fused(x, wq, s, b, lora_b.t().contiguous(), lora_a.t().contiguous(),
+                                 0.75, False, 64, bits, out_dtype=torch.float32)
+        assert bits_equal(z, z2) and bits_equal(y, y2), "rq_qlora_dx against rq_qlora(transpose=0)"
+        zr = ops.lora_down(xb, lora_b.t().contiguous())
+        yr = ops.quantized_matmul_lora(xb, wq, s, b, zr, lora_a.t().contiguous(), 0.75, False, 64,
+                                       bits)
+    assert bits_equal(z, zr), "the down-projection pass"
+    assert yr.dtype == torch.bfloat16
+    # the GEMM rounds once into y's dtype: compare against the fp32 output of
+    # the same two launches
+    yr32 = torch.empty_like(y)
+    from rwkvq import _lib
+    from rwkvq.ops import _stream_on
+    lo = lora_b if transpose else lora_a.t().contiguous()
+    rc = _lib.lib().rq_qmm_lora(xb.data_ptr(), _lib.RQ_BF16, wq.data_ptr(), s.data_ptr(),
+                                b.data_ptr(), _lib.RQ_BF16, M, R, K, 64, bits, 1 if transpose else 0,
+                                zr.data_ptr(), lo.data_ptr(), 16, 0.75, yr32.data_ptr(),
+                                _lib.RQ_F32, _stream_on(dev))
+    assert rc == 0, _lib.lib().rq_last_error().decode()
+    assert bits_equal(y, yr32), "the GEMM with the term in its output stage"
+    rel_check(yr32, yr.float(), what="fp32 vs bf16 output")
+
+
 def test_qlora_one_launch_declines_other_ranks_and_bits(rq, dev):
     from rwkvq import ops
     wq, s, b = rq.quantize(weights(256, 512, 3).to(dev), 64, 3)
