@@ -559,6 +559,12 @@ constexpr int kWsBlock = 512;
 #ifndef RQ_K64_DEPTH
 #define RQ_K64_DEPTH 2  // qmm_t_k64: stages of loads in flight per producer thread
 #endif
+#ifndef RQ_K64_SB64
+#define RQ_K64_SB64 2  // qmm_t_k64, 64 x 96 tiles: 64-wide stages per barrier
+#endif
+#ifndef RQ_K64_SB128
+#define RQ_K64_SB128 1  // qmm_t_k64, 128 x 128 tiles: 64-wide stages per barrier
+#endif
 #ifndef RQ_K64_PPRIO
 #define RQ_K64_PPRIO 2  // qmm_t_k64: wave priority of the producer waves (0-3; 2 measured +4-6%)
 #endif
@@ -1155,11 +1161,18 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     static_assert(P % D == 0, "the register ring index is the unrolled stage index mod D");
     static_assert(SDT != RQ_F32, "16-bit scales");
     static_assert(BN <= 256, "one producer thread stages one row's (scale, bias)");
-    __shared__ __attribute__((aligned(16))) uint8_t xs0[BM * 128];
-    __shared__ __attribute__((aligned(16))) uint8_t xs1[BM * 128];
-    __shared__ __attribute__((aligned(16))) uint16_t bq0[BN * BLD];
-    __shared__ __attribute__((aligned(16))) uint16_t bq1[BN * BLD];
+    // SB stages per barrier: a small tile's stage is short next to the fixed
+    // cost of the barrier and the LDS round trip around it, so its producers
+    // stage SB stages into a 2 SB-slot ring before each barrier and its MFMA
+    // waves run all SB of them after it
+    constexpr int SB = BM == 64 ? RQ_K64_SB64 : ((BM == 128 && BN <= 128 && !FZ) ? RQ_K64_SB128 : 1);
+    constexpr int NS = 2 * SB;  // ring slots
+    static_assert(P % SB == 0 && (SB == 1 || SB == 2), "whole groups of stages per period");
+    __shared__ __attribute__((aligned(16))) uint8_t xsr[NS][BM * 128];
+    __shared__ __attribute__((aligned(16))) uint16_t bqr[NS][BN * BLD];
     __shared__ __attribute__((aligned(16))) float sbf[2][BN * 16];  // fp32 (scale, bias), [row][8 groups]
+    uint8_t* const xs0 = xsr[0];
+    uint8_t* const xs1 = xsr[1];
 
     // split-K (splits > 1): block tt is tile tt % ntiles over the ks = tt / ntiles-th
     // share of the contraction, whole 8-group periods each, written as an fp32
@@ -1290,8 +1303,8 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int st = per * P + u;
-                uint8_t* xs = (u & 1) ? xs1 : xs0;
-                uint16_t* bq = (u & 1) ? bq1 : bq0;
+                uint8_t* xs = xsr[u % NS];
+                uint16_t* bq = bqr[u % NS];
                 if (u == 0) {
                     put_sb((per + 1) & 1);  // the next period's values (read from stage (per+1)*P on)
                     load_sb(per + 2);
@@ -1316,10 +1329,12 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
                             u32x4_t{d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]};
                 }
                 issue(st + D, u % D);
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this stage's LDS writes are done
-                asm volatile("" ::: "memory");
-                __builtin_amdgcn_s_barrier();
-                asm volatile("" ::: "memory");
+                if (u % SB == SB - 1) {
+                    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): these stages' LDS writes are done
+                    asm volatile("" ::: "memory");
+                    __builtin_amdgcn_s_barrier();
+                    asm volatile("" ::: "memory");
+                }
             }
         }
         if constexpr (FZ) {
@@ -1381,13 +1396,15 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int st = per * P + u;
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // own LDS reads of the previous stage are done
-                asm volatile("" ::: "memory");
-                __builtin_amdgcn_s_barrier();
-                asm volatile("" ::: "memory");
+                if (u % SB == 0) {
+                    __builtin_amdgcn_s_waitcnt(0xc07f);  // own LDS reads of the previous stages are done
+                    asm volatile("" ::: "memory");
+                    __builtin_amdgcn_s_barrier();
+                    asm volatile("" ::: "memory");
+                }
                 if (st < nst) {
-                    const uint8_t* xs = (u & 1) ? xs1 : xs0;
-                    const uint16_t* bq = (u & 1) ? bq1 : bq0;
+                    const uint8_t* xs = xsr[u % NS];
+                    const uint16_t* bq = bqr[u % NS];
                     if constexpr (FZ) {
                         zfa_cur = zfa_nxt;
                         if (st + 1 < nst) zfa_nxt = *(const u32x4_t*)(zarow + (int64_t)(st + 1) * 64);
@@ -1440,8 +1457,9 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     else
         main_loop(std::integral_constant<int, 0>{});
 
-    // after the last barrier the ring slot of stage nst - 2 (nst & 1) is read
-    // by nobody and written by nobody: 8 KB of it per wave stage the output
+    // after the last barrier the ring slot of stage nst - 2 SB (nst % NS: nst
+    // is a whole number of periods) is read by nobody and written by nobody:
+    // 8 KB of it per wave stage the output
     if constexpr (FZ) {
         __builtin_amdgcn_s_waitcnt(0xc07f);
         asm volatile("" ::: "memory");
@@ -1457,11 +1475,11 @@ __global__ __launch_bounds__(kWsBlock, 1) void qmm_t_k64(
     constexpr int SA = BM == 256 ? 2 : 1;
     static_assert(16 * SA * (BN + 16) <= BM * 32, "a wave's staging strip fits its share of a slot");
     if (splits > 1)  // fp32 partial tile of split ks
-        store_wave_tile<TM, TN, SA>(acc, ((nst & 1) ? xs1 : xs0) + wave * (BM * 32),
+        store_wave_tile<TM, TN, SA>(acc, xsr[nst % NS] + wave * (BM * 32),
                                     part + (int64_t)ks * M * R, RQ_F32, M, R, m0 + wm * (BM / 2),
                                     n0 + wn * WN, lane);
     else
-        store_wave_tile<TM, TN, SA>(acc, ((nst & 1) ? xs1 : xs0) + wave * (BM * 32), y, y_dt, M,
+        store_wave_tile<TM, TN, SA>(acc, xsr[nst % NS] + wave * (BM * 32), y, y_dt, M,
                                     R, m0 + wm * (BM / 2), n0 + wn * WN, lane);
 }
 
