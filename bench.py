@@ -448,8 +448,7 @@ def qlora_step_workload(torch, rq, dev):
     layers, _ = qlora_layers(torch, rq, dev, ws)
 
     def fused():
-        for lay, x, dy in layers:
-            torch.autograd.grad(lay(x), (x, lay.lora_a, lay.lora_b), dy)
+        layer_step(torch, layers, lambda lay, x: lay(x))
     for _ in range(5):
         fused()
     torch.cuda.synchronize()
@@ -458,6 +457,18 @@ def qlora_step_workload(torch, rq, dev):
         fused()
     torch.cuda.synchronize()
     print(f"config-4 QLoRA layer step: {1e3 * (time.perf_counter() - t0) / 20:.3f} ms", flush=True)
+
+
+def layer_step(torch, layers, forward):
+    """One training step of the layer's projections: every forward, then one
+    backward pass over all of them (dX, dA, dB for each), as a training
+    step's single backward call runs it."""
+    ys, ins, dys = [], [], []
+    for lay, x, dy in layers:
+        ys.append(forward(lay, x))
+        ins += [x, lay.lora_a, lay.lora_b]
+        dys.append(dy)
+    torch.autograd.grad(ys, ins, dys)
 
 
 def qlora_step(torch, rq, dev, ws, args):
@@ -475,15 +486,12 @@ def qlora_step(torch, rq, dev, ws, args):
     layers, flops = qlora_layers(torch, rq, dev, ws)
 
     def fused():
-        for lay, x, dy in layers:
-            torch.autograd.grad(lay(x), (x, lay.lora_a, lay.lora_b), dy)
+        layer_step(torch, layers, lambda lay, x: lay(x))
 
     def composed():
-        for lay, x, dy in layers:
-            base = rq.quantized_matmul(x, lay.linear.weight, lay.linear.scales,
-                                       lay.linear.biases, True, 64, 4)
-            y = base + lay.scale * ((x @ lay.lora_a.t()) @ lay.lora_b.t())
-            torch.autograd.grad(y, (x, lay.lora_a, lay.lora_b), dy)
+        layer_step(torch, layers, lambda lay, x: rq.quantized_matmul(
+            x, lay.linear.weight, lay.linear.scales, lay.linear.biases, True, 64, 4)
+            + lay.scale * ((x @ lay.lora_a.t()) @ lay.lora_b.t()))
 
     out = {}
     for key, fn in (("fused", fused), ("composed", composed)):
@@ -497,8 +505,7 @@ def qlora_step(torch, rq, dev, ws, args):
     layers32, _ = qlora_layers(torch, rq, dev, ws, torch.float32)
 
     def fused32():
-        for lay, x, dy in layers32:
-            torch.autograd.grad(lay(x), (x, lay.lora_a, lay.lora_b), dy)
+        layer_step(torch, layers32, lambda lay, x: lay(x))
     t = time_region(torch, fused32, max(5, args.steps // 10), 3)
     out["fused_fp32_x"] = {"ms_per_layer_step": round(t * 1e3, 3),
                            "tflops": round(flops / t / 1e12, 1),

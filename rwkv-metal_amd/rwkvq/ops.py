@@ -444,6 +444,9 @@ def _lora_workspace(device: torch.device, stream: int, nbytes: int) -> Tensor:
     return ws
 
 
+_grad_ws_bytes: dict = {}  # (m, k, n, rank, dA?, dB?) -> rq_lora_grads_workspace_bytes
+
+
 def lora_grads(x: Tensor | None, u: Tensor | None, dy: Tensor | None, z: Tensor | None,
                scale: float) -> Tuple[Tensor | None, Tensor | None]:
     """The QLoRA adapter gradients of rwkv_metal/lora/lora.py:58-63 under
@@ -456,18 +459,18 @@ def lora_grads(x: Tensor | None, u: Tensor | None, dy: Tensor | None, z: Tensor 
     ref = x if want_a else dy
     if ref is None:
         return None, None
+    _on_gpu(*[t for t in (x, u, dy, z) if t is not None])
     q = u if want_a else z
     rank = q.shape[-1]
     xdt = ref.dtype
-    if not (ref.is_cuda and rank in (16, 32, 48, 64) and xdt in (torch.bfloat16, torch.float32)
+    if not (rank in (16, 32, 48, 64) and xdt in (torch.bfloat16, torch.float32)
             and all(t is None or t.dtype == xdt for t in (x, dy))
             and all(t is None or t.dtype == torch.bfloat16 for t in (u, z))
             and (not want_a or x.shape[-1] % 8 == 0) and (not want_b or dy.shape[-1] % 8 == 0)):
+        # ranks and dtypes the launch does not cover: fp32 products on the GPU
         da = (scale * (u.float().t() @ x.float())).to(u.dtype) if want_a else None
         db = (scale * (dy.float().t() @ z.float())).to(z.dtype) if want_b else None
         return da, db
-    ops_ = [t for t in (x, u, dy, z) if t is not None]
-    _on_gpu(*ops_)
     m = ref.numel() // ref.shape[-1]
     x2 = _ready(x.reshape(m, x.shape[-1])) if want_a else None
     u2 = _ready(u.reshape(m, rank)) if want_a else None
@@ -480,8 +483,14 @@ def lora_grads(x: Tensor | None, u: Tensor | None, dy: Tensor | None, z: Tensor 
     L = lib()
     with _DeviceGuard(ref.device):
         stream = _stream_on(ref.device)
-        nbytes = L.rq_lora_grads_workspace_bytes(m, K, N, rank, int(want_a), int(want_b))
-        check(nbytes if nbytes < 0 else 0, "lora_grads")
+        key = (m, K, N, rank, want_a, want_b)
+        nbytes = _grad_ws_bytes.get(key)
+        if nbytes is None:
+            nbytes = L.rq_lora_grads_workspace_bytes(m, K, N, rank, int(want_a), int(want_b))
+            check(nbytes if nbytes < 0 else 0, "lora_grads")
+            if len(_grad_ws_bytes) > 4096:
+                _grad_ws_bytes.clear()
+            _grad_ws_bytes[key] = nbytes
         ws = _lora_workspace(ref.device, stream, int(nbytes)) if nbytes > 0 else None
         fn = L.rq_lora_grads_f32 if xdt == torch.float32 else L.rq_lora_grads
         rc = fn(_ptr(x2) if want_a else 0, _ptr(u2) if want_a else 0,

@@ -239,3 +239,17 @@ def test_embedding_op_refuses_cpu_and_bad_indices(rq):
         rq.quantized_embedding(torch.zeros(3, dtype=torch.int64), wq, s, s, 64, 4)
     with pytest.raises(ValueError):
         rq.quantized_embedding(torch.zeros(3), wq, s, s, 64, 4)
+
+
+@pytest.mark.parametrize("rank,dt", [(16, torch.bfloat16), (8, torch.bfloat16), (16, torch.float16)])
+def test_lora_grads_refuses_cpu_tensors(rq, rank, dt):
+    """The adapter gradients run on the GPU only, also for the ranks and
+    dtypes that take the fp32-product route there: CPU tensors are refused,
+    never computed on the host."""
+    from rwkvq import ops
+    x = torch.zeros(64, 128, dtype=dt)
+    u = torch.zeros(64, rank, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.lora_grads(x, u, x, u, 1.0)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.lora_grads(None, None, x, u, 1.0)
