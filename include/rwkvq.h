@@ -276,9 +276,8 @@ int rq_lora_grads_noalloc(const void* x, const void* u, const void* dy, const vo
  * do.  Large problems (with z_out given) take two launches instead: z as its
  * own pass, which reads x once, then the GEMM with the term in its output
  * stage -- exactly rq_lora_down + rq_qmm_lora on bf16(x); recomputing z in
- * every output column tile costs more there.  Forward: outputs at least 4096
- * wide and twice the contraction; dX: an output or a contraction of at least
- * 4096.  Covers rank 16 with 4- or 8-bit codes on the 64-wide-stage
+ * every output column tile costs more there: outputs at least 4096 wide and
+ * twice the contraction.  Covers rank 16 with 4- or 8-bit codes on the 64-wide-stage
  * GEMMs (the conditions of rq_qmm_lora); other problems return
  * RQ_EUNSUPPORTED (z_out may have been written) and the caller runs
  * rq_lora_down and rq_qmm_lora.  a, lora and z_out 16-byte aligned. */
@@ -296,8 +295,8 @@ int rq_qlora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scal
  * and u is stored to u_out [m, rank] bf16 (if not NULL) for the adapter
  * gradients.  The same product as rq_qlora with transpose=0, a = lora_b^T
  * and lora = lora_a^T, bit for bit, without the two transposed copies
- * (also where it takes two launches: cols or rows >= 4096, u_out given and
- * lora_b 16-byte aligned).  Covers what rq_qlora's dX covers
+ * (also where it takes two launches: cols >= 4096 and >= 2 rows, u_out
+ * given and lora_b 16-byte aligned).  Covers what rq_qlora's dX covers
  * (rank 16, 4- or 8-bit codes); other problems return RQ_EUNSUPPORTED.  dy,
  * w_q and u_out 16-byte aligned, lora_a and lora_b 2-byte aligned. */
 int rq_qlora_dx(const void* dy, rq_dtype dy_dt, const uint32_t* w_q, const void* scales,

@@ -511,20 +511,20 @@ int rq_qmm_lora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* s
 // The fused QLoRA products compute the down-projection once per output
 // column tile: 12.5 % more MFMA work in every 128-column tile, on the waves
 // that bound the GEMM.  Its rq_lora_down pass instead reads the activations
-// once, so for large problems two launches cost less.  MI355X, M = 4096:
-// forward [8192, 2048] and dX of [2048, 8192] about +22 us fused against
-// +8 us for the pass and the output-stage term, dX of [8192, 2048] 150-152
-// against 142-145 us; the forward of [2048, 8192] (a 64 MB pass) 146-149
-// fused against 151-153, and the [2048, 2048] products +5 us fused against
-// +7.  bf16 or fp32 activations (the pass rounds fp32 ones to bf16 as the
-// GEMM does, so either gives the bits of bf16(x)), rank 16, 4 or 8 bits,
-// m >= 256: where the fused kernels apply.
-static bool qlora_two_launch(int transpose, int x_dt, int bits, int64_t rank, int64_t m,
-                             int64_t n_in, int64_t n_out) {
-    if (!((x_dt == RQ_BF16 || x_dt == RQ_F32) && (bits == 4 || bits == 8) && rank == 16 &&
-          m >= 256 && n_in % 32 == 0))
-        return false;
-    return transpose ? (n_out >= 4096 && n_out >= 2 * n_in) : (n_out >= 4096 || n_in >= 4096);
+// once, so for outputs much wider than the contraction two launches cost
+// less.  MI355X, M = 4096, inside the config-4 layer step (activations not
+// cache-resident): dX of [2048, 8192] 180 us fused against 172 (a 7 us
+// pass); the forward of [8192, 2048] 167 against 159 + 7 (its pass reads
+// 16 MB at K = 2048, latency-bound).  Long contractions keep the fused
+// kernels: a 64 MB pass costs 15-23 us there (dX of [8192, 2048] fused
+// 150-155 against 139 + 23), and the [2048, 2048] products +5 us fused
+// against +7.  bf16 or fp32 activations (the pass rounds fp32 ones to bf16
+// as the GEMM does, so either gives the bits of bf16(x)), rank 16, 4 or 8
+// bits, m >= 256: where the fused kernels apply.
+static bool qlora_two_launch(int x_dt, int bits, int64_t rank, int64_t m, int64_t n_in,
+                             int64_t n_out) {
+    return (x_dt == RQ_BF16 || x_dt == RQ_F32) && (bits == 4 || bits == 8) && rank == 16 &&
+           m >= 256 && n_in % 32 == 0 && n_out >= 4096 && n_out >= 2 * n_in;
 }
 
 int rq_qlora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scales,
@@ -544,7 +544,7 @@ int rq_qlora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scal
     if (!aligned16(x) || !aligned16(w_q) || !aligned16(a) || !aligned16(lora) || !aligned16(z_out))
         return fail(RQ_EALIGN, "rq_qlora: x, w_q, a, lora and z_out must be 16-byte aligned");
     hipError_t e;
-    if (z_out && qlora_two_launch(transpose, x_dt, bits, rank, m, n_in, n_out)) {
+    if (z_out && qlora_two_launch(x_dt, bits, rank, m, n_in, n_out)) {
         e = rq::launch_lora_down(x, m, n_in, a, (int)rank, z_out, (hipStream_t)stream,
                                  /*a_t=*/false, x_dt == RQ_F32);
         rq::LoraArgs lo{z_out, lora, (int)rank, scale};
@@ -588,7 +588,7 @@ int rq_qlora_dx(const void* dy, rq_dtype dy_dt, const uint32_t* w_q, const void*
     // u = dY . B from B [rows, rank] as stored; the term scale * u . A from A
     // [rank, cols] as stored
     hipError_t e;
-    if (u_out && aligned16(lora_b) && qlora_two_launch(0, dy_dt, bits, rank, m, rows, cols)) {
+    if (u_out && aligned16(lora_b) && qlora_two_launch(dy_dt, bits, rank, m, rows, cols)) {
         e = rq::launch_lora_down(dy, m, rows, lora_b, (int)rank, u_out, (hipStream_t)stream,
                                  /*a_t=*/true, dy_dt == RQ_F32);
         rq::LoraArgs lo{u_out, lora_a, (int)rank, scale};
