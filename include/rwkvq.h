@@ -296,9 +296,9 @@ int rq_qlora(const void* x, rq_dtype x_dt, const uint32_t* w_q, const void* scal
  * gradients.  The same product as rq_qlora with transpose=0, a = lora_b^T
  * and lora = lora_a^T, bit for bit, without the two transposed copies
  * (also where it takes two launches: cols >= 4096 and >= 2 rows, u_out
- * given and lora_b 16-byte aligned).  Covers what rq_qlora's dX covers
- * (rank 16, 4- or 8-bit codes); other problems return RQ_EUNSUPPORTED.  dy,
- * w_q and u_out 16-byte aligned, lora_a and lora_b 2-byte aligned. */
+ * given).  Covers what rq_qlora's dX covers (rank 16, 4- or 8-bit codes);
+ * other problems return RQ_EUNSUPPORTED.  dy, w_q, lora_b and u_out 16-byte
+ * aligned, lora_a 2-byte aligned. */
 int rq_qlora_dx(const void* dy, rq_dtype dy_dt, const uint32_t* w_q, const void* scales,
                 const void* biases, rq_dtype sb_dt, int64_t m, int64_t rows, int64_t cols,
                 int group_size, int bits, const void* lora_a, const void* lora_b, int64_t rank,

@@ -581,14 +581,15 @@ int rq_qlora_dx(const void* dy, rq_dtype dy_dt, const uint32_t* w_q, const void*
     if (rows == 0) return fail(RQ_EINVAL, "rq_qlora_dx: empty contraction is not supported");
     if (!dy || !w_q || !scales || !biases || !dx || !lora_a || !lora_b)
         return fail(RQ_EINVAL, "rq_qlora_dx: NULL pointer");
-    if (!aligned16(dy) || !aligned16(w_q) || !aligned16(u_out))
-        return fail(RQ_EALIGN, "rq_qlora_dx: dy, w_q and u_out must be 16-byte aligned");
-    if (((uintptr_t)lora_a | (uintptr_t)lora_b) & 1)
-        return fail(RQ_EALIGN, "rq_qlora_dx: lora_a and lora_b must be 2-byte aligned");
+    // lora_b is read in 16-byte pieces (a stage's rows of B), lora_a in 2-byte ones
+    if (!aligned16(dy) || !aligned16(w_q) || !aligned16(u_out) || !aligned16(lora_b))
+        return fail(RQ_EALIGN, "rq_qlora_dx: dy, w_q, lora_b and u_out must be 16-byte aligned");
+    if ((uintptr_t)lora_a & 1)
+        return fail(RQ_EALIGN, "rq_qlora_dx: lora_a must be 2-byte aligned");
     // u = dY . B from B [rows, rank] as stored; the term scale * u . A from A
     // [rank, cols] as stored
     hipError_t e;
-    if (u_out && aligned16(lora_b) && qlora_two_launch(dy_dt, bits, rank, m, rows, cols)) {
+    if (u_out && qlora_two_launch(dy_dt, bits, rank, m, rows, cols)) {
         e = rq::launch_lora_down(dy, m, rows, lora_b, (int)rank, u_out, (hipStream_t)stream,
                                  /*a_t=*/true, dy_dt == RQ_F32);
         rq::LoraArgs lo{u_out, lora_a, (int)rank, scale};

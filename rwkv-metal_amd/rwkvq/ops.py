@@ -588,7 +588,7 @@ def qlora_dx_fused(dy: Tensor, w_q: Tensor, scales: Tensor, biases: Tensor, lora
         return None
     _on_gpu(dy, w_q, scales, biases, lora_a, lora_b)
     dy, w_q, scales = _ready(dy), _ready(w_q), _ready(scales)
-    lora_a, lora_b = lora_a.contiguous(), lora_b.contiguous()
+    lora_a, lora_b = lora_a.contiguous(), _ready(lora_b)
     biases = _ready(biases.to(scales.dtype))
     m = dy.shape[0]
     dx = torch.empty(m, K, dtype=out_dtype or _promote(dy.dtype, scales.dtype), device=dy.device)

@@ -220,8 +220,9 @@ def test_qmm_splitk_plan_and_rejections(L):
 
 def test_qlora_dx_rejections_before_any_device_work(L):
     """rq_qlora_dx validates before it launches: the rank, NULL adapters,
-    alignment (16 bytes for dy and u_out, 2 for the adapters as stored) and
-    an empty contraction; an empty output is a no-op."""
+    alignment (16 bytes for dy, lora_b and u_out, which are read or written
+    in 16-byte pieces; 2 for lora_a) and an empty contraction; an empty
+    output is a no-op."""
     p = 0x1000
     f = L.rq_qlora_dx
     assert f(p, 0, p, p, p, 0, 512, 2048, 2048, 64, 4, p, p, 8, 1.0, p, p, 0, None) == -1
@@ -231,8 +232,9 @@ def test_qlora_dx_rejections_before_any_device_work(L):
     assert f(p + 8, 0, p, p, p, 0, 512, 2048, 2048, 64, 4, p, p, 16, 1.0, p, p, 0, None) == -2
     assert f(p, 0, p, p, p, 0, 512, 2048, 2048, 64, 4, p + 1, p, 16, 1.0, p, p, 0, None) == -2
     assert "2-byte" in _err(L)
-    assert f(p, 0, p, p, p, 0, 512, 2048, 2048, 64, 4, p, p + 2, 16, 1.0, p + 8, p, 0,
-             None) == -2
+    assert f(p, 0, p, p, p, 0, 512, 2048, 2048, 64, 4, p, p + 2, 16, 1.0, p, p, 0, None) == -2
+    assert "lora_b" in _err(L)
+    assert f(p, 0, p, p, p, 0, 512, 2048, 2048, 64, 4, p, p, 16, 1.0, p + 8, p, 0, None) == -2
     assert f(p, 0, p, p, p, 0, 512, 0, 2048, 64, 4, p, p, 16, 1.0, p, p, 0, None) == -1
     assert "contraction" in _err(L)
     assert f(p, 0, p, p, p, 0, 512, 2048, 2048, 64, 7, p, p, 16, 1.0, p, p, 0, None) == -1
