@@ -702,8 +702,8 @@ hipError_t launch_cfg(const QmvArgs& a, int sb_dt, int nmc, bool xlds, int block
 //  * A "stage" is 256 codes of 16 weight rows.  Lane L takes the two
 //    consecutive runs 2g, 2g+1 (g = L/16) of row L%16: 64 contiguous codes,
 //    so one wave-load covers 16 rows x 128 B, whole cache lines (measured:
-//    +18% streaming rate over 16 rows x 64 B per load).  Stage s+3 is in
-//    flight while stage s is computed.
+//    +18% streaming rate over 16 rows x 64 B per load).  Stage s+1 is in
+//    flight while stage s is computed (s+3 at 32-code groups).
 //  * Each lane group owns a different k-slice of the MFMA, so the 16 A rows
 //    are split into 4 slots (A row m' carries x[m'%4] on lane group m'/4's
 //    slice only): D row 4g+i sums exactly lane group g's codes, i.e. one
@@ -731,6 +731,14 @@ constexpr int kStreamSlotsMax = 4;  // largest m of the slotted streamed kernel;
 #ifndef RQ_QMV_WIN_G
 #define RQ_QMV_WIN_G 32
 #endif
+// Streamed GEMV, groups of 64 codes or more: stages per iteration, NS - 1 of
+// them in flight.  Two (one stage ahead, 76 VGPRs at m = 1, 6 waves per
+// SIMD) measured faster than four (98 VGPRs, 4 waves): the config-2 sweep
+// 5.89 vs 5.67-5.71 TB/s, the head's single launch 17.6 vs 19.0-19.3 us;
+// eight (7 ahead) was slower still (5.1 TB/s).
+#ifndef RQ_QMV_STREAM_NS
+#define RQ_QMV_STREAM_NS 2
+#endif
 // (scale, bias) windows: a window is RQ_QMV_WIN_G groups of a row (64 B of
 // each array at 16-bit scales), loaded once for the IPW iterations that read
 // it.  Loaded in 32-B parts one iteration apart, a 128-B line was often
@@ -738,10 +746,10 @@ constexpr int kStreamSlotsMax = 4;  // largest m of the slotted streamed kernel;
 // long as the streamed codes need to turn the L2 over.  64 groups (whole
 // lines) would remove the rest of the refetch at K >= 4096 but need 8 more
 // VGPRs per lane, one wave per SIMD less at 4 bits.
-template <int GSH, int WGV = RQ_QMV_WIN_G>
+template <int GSH, int WGV = RQ_QMV_WIN_G, int NSV = 4>
 struct StreamWin {
     static constexpr int GPS = 256 >> GSH;             // groups per stage: 8, 4, 2
-    static constexpr int GPI = 4 * GPS;                // groups per iteration: 32, 16, 8
+    static constexpr int GPI = NSV * GPS;              // groups per iteration (4 stages: 32, 16, 8)
     static constexpr int WG = WGV;                     // groups per window
     static constexpr int WW = WG * 2;                  // bytes per array per row per window
     static constexpr int IPW = WG / GPI;               // iterations per window: 2, 4, 8
@@ -893,8 +901,9 @@ template <int BITS, int SDT, int NMC, int MI, int GSH>
 RQ_DEV void qmv_stream_body(const rq_problem& P, int lblock, int M, int x_dt, int y_dt, int xsplit) {
     static_assert(SDT != RQ_F32, "streamed scales are 16-bit");
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-    typedef StreamWin<GSH> W;
-    constexpr int NS = 4;  // stages per iteration; NS-1 stages of codes in flight
+    // stages per iteration; NS-1 stages of codes in flight
+    constexpr int NS = GSH >= 6 ? RQ_QMV_STREAM_NS : 4;
+    typedef StreamWin<GSH, RQ_QMV_WIN_G, NS> W;
     typedef Words<W::WW / 2 / 4> win_t;  // a lane's half of one array's window row
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
