@@ -808,7 +808,9 @@ def test_grouped_more_problems_than_one_launch(O, rq, dev):
 
 # ------------------------------------------- planned (one-launch) grouped GEMV
 
-PLAN_SHAPES = [(100, 512), (64, 1024), (17, 2048)]
+# the streamed kernel's (scale, bias) windows cover 32 groups: 1536 and 2560
+# columns end in a partial window (and, at 64-code groups, mid-iteration pair)
+PLAN_SHAPES = [(100, 512), (64, 1024), (17, 2048), (24, 1536), (40, 2560)]
 
 
 def _planned(O, rq, dev, shapes, M, gs, bits, seed, xdt=torch.bfloat16, sdt=torch.bfloat16):
